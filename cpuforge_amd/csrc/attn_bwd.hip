@@ -1,0 +1,507 @@
+// Causal grouped-query attention backward on gfx950 MFMA.
+//
+// Reference semantics (crates/core/src/ops/attention.rs:142-262): with
+// P = exp(s*scale - lse) recomputed from the saved log-sum-exp,
+//   dV_g += P^T dO,   dP = dO V^T,   dS = P * (dP - delta) * scale,
+//   dQ   += dS K,     dK_g += dS^T Q,   delta_t = sum_d dO[t,d] * O[t,d],
+// all accumulated (+=) into the caller's gradients (ops/mod.rs:1-6).
+//
+// Three kernels, no atomics, so every result is bitwise reproducible:
+//   delta: one row reduction per (token, head).
+//   dK/dV: a workgroup owns 32*waves keys of one KV head and loops over
+//          every query head of its GQA group and every query tile that can
+//          see those keys; K and V stay in registers, Q/dO tiles are staged
+//          in LDS (row-major for S = Q K^T and dP = dO V^T, transposed for
+//          dV^T += dO^T P and dK^T += Q^T dS).  Each dK/dV element is owned
+//          by one lane, and its sum over heads and query tiles runs in a
+//          fixed order.
+//   dQ:    the forward's decomposition (a wave owns 32 queries of one head);
+//          K/V tiles in LDS are shared across the heads of the group;
+//          S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
+#include "cfattn_common.hpp"
+#include "cfattn_kernels.hpp"
+
+namespace cfattn {
+
+struct BwdParams {
+    const void* d_o;
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* o;
+    const float* lse;
+    float* delta;
+    float* dq;
+    float* dk;
+    float* dv;
+    int batch, seq, nh, nkv, hd, group;
+    // dK/dV grid
+    int kv_tile, n_kvtiles, n_wg_kv;
+    // dQ grid
+    int hpw, tpw, n_sub, n_ttiles, n_wg_q;
+    float scale, sl2;
+    long q_bs, kv_bs;
+    int vec_ok, g_vec_ok, xcd;
+};
+
+// delta[b][h][t] = sum_d dO[b,t,h,d] * O[b,t,h,d]; 16 lanes per row.
+template <typename T>
+__global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams p) {
+    const long rows = (long)p.batch * p.seq * p.nh;
+    const long row = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int sl = threadIdx.x & 15;
+    float acc = 0.0f;
+    if (row < rows) {
+        const T* g = static_cast<const T*>(p.d_o) + row * p.hd;
+        const float* o = p.o + row * p.hd;
+        for (int d = sl; d < p.hd; d += 16) acc += to_f32<T>(g[d]) * o[d];
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+    if (row < rows && sl == 0) {
+        const long b = row / ((long)p.seq * p.nh);
+        const long t = (row / p.nh) % p.seq;
+        const long h = row % p.nh;
+        p.delta[(b * p.nh + h) * p.seq + t] = acc;
+    }
+}
+
+// Accumulate one lane's 4 x (4 consecutive head dims) of a transposed
+// accumulator block into a global row: dst[d0 + 8*rq + 4*hh + i] += acc[4*rq + i].
+__device__ __forceinline__ void add_row_block(float* row, const f32x16& acc, int dbase, int hh, int hd, bool vec_ok) {
+#pragma unroll
+    for (int rq = 0; rq < 4; rq++) {
+        const int d0 = dbase + rq * 8 + hh * 4;
+        if (vec_ok && d0 + 4 <= hd) {
+            float4 v = *reinterpret_cast<float4*>(row + d0);
+            v.x += acc[rq * 4 + 0];
+            v.y += acc[rq * 4 + 1];
+            v.z += acc[rq * 4 + 2];
+            v.w += acc[rq * 4 + 3];
+            *reinterpret_cast<float4*>(row + d0) = v;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (d0 + i < hd) row[d0 + i] += acc[rq * 4 + i];
+        }
+    }
+}
+
+template <typename T, int DP, int BM>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const BwdParams p) {
+    using M = Mode<T>;
+    constexpr int EPL = M::EPL;
+    constexpr int HALF = DP / 2;
+    constexpr int NKD = HALF / EPL;
+    constexpr int NDB = DP / 32;
+    constexpr int LDQ = RowLD<T, DP>::value;
+    constexpr int LDT = TLD<T, BM>::value;
+    __shared__ __attribute__((aligned(16))) T sQ[BM * LDQ];
+    __shared__ __attribute__((aligned(16))) T sO[BM * LDQ];  // dO rows
+    __shared__ __attribute__((aligned(16))) T sQt[DP * LDT];
+    __shared__ __attribute__((aligned(16))) T sOt[DP * LDT];  // dO transposed
+    __shared__ float sL[BM], sD[BM];
+
+    const int nthreads = blockDim.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
+    const int kvt = id % p.n_kvtiles;  // low key tiles see the most queries: first
+    const int rest = id / p.n_kvtiles;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+    const int wg_key0 = kvt * p.kv_tile;
+    const int key0 = wg_key0 + wave * 32;
+    const int kw = key0 + l32;
+    const bool wave_active = key0 < p.seq;
+
+    const long qrs = (long)p.nh * p.hd, kvrs = (long)p.nkv * p.hd;
+    const T* qg = static_cast<const T*>(p.q) + (long)b * p.q_bs;
+    const T* og = static_cast<const T*>(p.d_o) + (long)b * p.q_bs;
+    const T* kg = static_cast<const T*>(p.k) + (long)b * p.kv_bs + (long)g * p.hd;
+    const T* vg = static_cast<const T*>(p.v) + (long)b * p.kv_bs + (long)g * p.hd;
+
+    // K and V operand rows for key kw, head dims [hh*HALF, hh*HALF+HALF).
+    typename M::frag kf[NKD], vf[NKD];
+    {
+        T raw[HALF];
+        load_row_frag<T, HALF>(raw, kg + (long)kw * kvrs, hh * HALF, p.hd, kw < p.seq, p.vec_ok);
+#pragma unroll
+        for (int kd = 0; kd < NKD; kd++) {
+            if constexpr (EPL == 8) {
+                Chunk<T> c;
+#pragma unroll
+                for (int i = 0; i < 8; i++) c.e[i] = raw[kd * 8 + i];
+                kf[kd] = __builtin_bit_cast(bf16x8, c.u);
+            } else {
+                kf[kd] = raw[kd];
+            }
+        }
+        load_row_frag<T, HALF>(raw, vg + (long)kw * kvrs, hh * HALF, p.hd, kw < p.seq, p.vec_ok);
+#pragma unroll
+        for (int kd = 0; kd < NKD; kd++) {
+            if constexpr (EPL == 8) {
+                Chunk<T> c;
+#pragma unroll
+                for (int i = 0; i < 8; i++) c.e[i] = raw[kd * 8 + i];
+                vf[kd] = __builtin_bit_cast(bf16x8, c.u);
+            } else {
+                vf[kd] = raw[kd];
+            }
+        }
+    }
+
+    f32x16 dkt[NDB], dvt[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) {
+        dkt[i] = zero16();
+        dvt[i] = zero16();
+    }
+
+    const int qt_begin = wg_key0 / BM;
+    const int n_qt = (p.seq + BM - 1) / BM;
+    for (int hi = 0; hi < p.group; hi++) {
+        const int h = g * p.group + hi;
+        const float* lse_h = p.lse + ((long)b * p.nh + h) * p.seq;
+        const float* dlt_h = p.delta + ((long)b * p.nh + h) * p.seq;
+        for (int qt = qt_begin; qt < n_qt; qt++) {
+            const int q0 = qt * BM;
+            const int nrows = min(BM, p.seq - q0);
+            __syncthreads();
+            const long goff = (long)q0 * qrs + (long)h * p.hd;
+            stage_rows<T, BM, DP, LDQ>(sQ, qg + goff, qrs, nrows, p.hd, p.vec_ok, nthreads);
+            stage_rows<T, BM, DP, LDQ>(sO, og + goff, qrs, nrows, p.hd, p.vec_ok, nthreads);
+            stage_rows_t<T, BM, DP, LDT>(sQt, qg + goff, qrs, nrows, p.hd, p.vec_ok, nthreads);
+            stage_rows_t<T, BM, DP, LDT>(sOt, og + goff, qrs, nrows, p.hd, p.vec_ok, nthreads);
+            for (int i = threadIdx.x; i < BM; i += nthreads) {
+                const bool ok = q0 + i < p.seq;
+                // Rows past the sequence get lse = +inf, so P = 0 there.
+                sL[i] = ok ? lse_h[q0 + i] * kLog2e : INFINITY;
+                sD[i] = ok ? dlt_h[q0 + i] : 0.0f;
+            }
+            __syncthreads();
+            if (!wave_active || q0 + BM - 1 < key0) continue;
+
+#pragma unroll
+            for (int qb = 0; qb < BM / 32; qb++) {
+                const int tq0 = q0 + qb * 32;
+                if (tq0 + 31 < key0 || tq0 >= p.seq) continue;
+                // S and dP: rows = queries tq0 + [0,32), columns = this wave's keys.
+                f32x16 s = zero16(), dp = zero16();
+                const T* qrow = sQ + (qb * 32 + l32) * LDQ + hh * HALF;
+                const T* orow = sO + (qb * 32 + l32) * LDQ + hh * HALF;
+                if constexpr (EPL == 8) {
+#pragma unroll
+                    for (int kd = 0; kd < NKD; kd++) {
+                        s = mfma32(load_bf16x8(qrow + kd * 8), kf[kd], s);
+                        dp = mfma32(load_bf16x8(orow + kd * 8), vf[kd], dp);
+                    }
+                } else {
+#pragma unroll
+                    for (int kd = 0; kd < NKD; kd += 4) {
+                        const float4 a = *reinterpret_cast<const float4*>(qrow + kd);
+                        const float4 c = *reinterpret_cast<const float4*>(orow + kd);
+                        s = mfma32(a.x, kf[kd + 0], s);
+                        s = mfma32(a.y, kf[kd + 1], s);
+                        s = mfma32(a.z, kf[kd + 2], s);
+                        s = mfma32(a.w, kf[kd + 3], s);
+                        dp = mfma32(c.x, vf[kd + 0], dp);
+                        dp = mfma32(c.y, vf[kd + 1], dp);
+                        dp = mfma32(c.z, vf[kd + 2], dp);
+                        dp = mfma32(c.w, vf[kd + 3], dp);
+                    }
+                }
+                const bool need_mask = tq0 < key0 + 31;
+                float pr[16], ds[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int qi = qb * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+                    float pv = exp2f(s[r] * p.sl2 - sL[qi]);
+                    if (need_mask && kw > q0 + qi) pv = 0.0f;
+                    pr[r] = pv;
+                    ds[r] = pv * (dp[r] - sD[qi]) * p.scale;
+                }
+                if constexpr (EPL == 8) {
+                    const bf16x8 p0 = pack_bf16x8(&pr[0]), p1 = pack_bf16x8(&pr[8]);
+                    const bf16x8 d0 = pack_bf16x8(&ds[0]), d1 = pack_bf16x8(&ds[8]);
+#pragma unroll
+                    for (int db = 0; db < NDB; db++) {
+                        const T* ot = sOt + (db * 32 + l32) * LDT + qb * 32 + hh * 4;
+                        const T* qt_ = sQt + (db * 32 + l32) * LDT + qb * 32 + hh * 4;
+                        dvt[db] = mfma32(load_bf16x4x2(ot, ot + 8), p0, dvt[db]);
+                        dvt[db] = mfma32(load_bf16x4x2(ot + 16, ot + 24), p1, dvt[db]);
+                        dkt[db] = mfma32(load_bf16x4x2(qt_, qt_ + 8), d0, dkt[db]);
+                        dkt[db] = mfma32(load_bf16x4x2(qt_ + 16, qt_ + 24), d1, dkt[db]);
+                    }
+                } else {
+#pragma unroll
+                    for (int db = 0; db < NDB; db++) {
+                        const T* ot = sOt + (db * 32 + l32) * LDT + qb * 32 + hh * 4;
+                        const T* qt_ = sQt + (db * 32 + l32) * LDT + qb * 32 + hh * 4;
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const float4 a = *reinterpret_cast<const float4*>(ot + j * 8);
+                            const float4 c = *reinterpret_cast<const float4*>(qt_ + j * 8);
+                            dvt[db] = mfma32(a.x, pr[j * 4 + 0], dvt[db]);
+                            dvt[db] = mfma32(a.y, pr[j * 4 + 1], dvt[db]);
+                            dvt[db] = mfma32(a.z, pr[j * 4 + 2], dvt[db]);
+                            dvt[db] = mfma32(a.w, pr[j * 4 + 3], dvt[db]);
+                            dkt[db] = mfma32(c.x, ds[j * 4 + 0], dkt[db]);
+                            dkt[db] = mfma32(c.y, ds[j * 4 + 1], dkt[db]);
+                            dkt[db] = mfma32(c.z, ds[j * 4 + 2], dkt[db]);
+                            dkt[db] = mfma32(c.w, ds[j * 4 + 3], dkt[db]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    if (!wave_active || kw >= p.seq) return;
+    float* dkrow = p.dk + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * p.hd;
+    float* dvrow = p.dv + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * p.hd;
+#pragma unroll
+    for (int db = 0; db < NDB; db++) {
+        add_row_block(dkrow, dkt[db], db * 32, hh, p.hd, p.g_vec_ok);
+        add_row_block(dvrow, dvt[db], db * 32, hh, p.hd, p.g_vec_ok);
+    }
+}
+
+template <typename T, int DP, int BN>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams p) {
+    using M = Mode<T>;
+    constexpr int EPL = M::EPL;
+    constexpr int HALF = DP / 2;
+    constexpr int NKD = HALF / EPL;
+    constexpr int NDB = DP / 32;
+    constexpr int NKB = BN / 32;
+    constexpr int LDK = RowLD<T, DP>::value;
+    constexpr int LDT = TLD<T, BN>::value;
+    __shared__ __attribute__((aligned(16))) T sK[BN * LDK];
+    __shared__ __attribute__((aligned(16))) T sV[BN * LDK];
+    __shared__ __attribute__((aligned(16))) T sKt[DP * LDT];
+
+    const int nthreads = blockDim.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg_q, p.xcd);
+    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;
+    int rest = id / p.n_ttiles;
+    const int sub = rest % p.n_sub;
+    rest /= p.n_sub;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+
+    const int head = g * p.group + sub * p.hpw + wave % p.hpw;
+    const int TT = 32 * p.tpw;
+    const int t_wave = tile * TT + (wave / p.hpw) * 32;
+    const int tq = t_wave + l32;
+    const int wg_end = min(p.seq, tile * TT + TT);
+    const int n_kt = (wg_end + BN - 1) / BN;
+    const bool wave_active = t_wave < p.seq;
+    const int wave_last = min(t_wave + 31, p.seq - 1);
+    const bool row_ok = tq < p.seq;
+
+    const long qrs = (long)p.nh * p.hd, kvrs = (long)p.nkv * p.hd;
+    const long qoff = (long)b * p.q_bs + (long)tq * qrs + (long)head * p.hd;
+    const T* kg = static_cast<const T*>(p.k) + (long)b * p.kv_bs + (long)g * p.hd;
+    const T* vg = static_cast<const T*>(p.v) + (long)b * p.kv_bs + (long)g * p.hd;
+
+    typename M::frag qf[NKD], of[NKD];
+    {
+        T raw[HALF];
+        load_row_frag<T, HALF>(raw, static_cast<const T*>(p.q) + qoff, hh * HALF, p.hd, row_ok, p.vec_ok);
+#pragma unroll
+        for (int kd = 0; kd < NKD; kd++) {
+            if constexpr (EPL == 8) {
+                Chunk<T> c;
+#pragma unroll
+                for (int i = 0; i < 8; i++) c.e[i] = raw[kd * 8 + i];
+                qf[kd] = __builtin_bit_cast(bf16x8, c.u);
+            } else {
+                qf[kd] = raw[kd];
+            }
+        }
+        load_row_frag<T, HALF>(raw, static_cast<const T*>(p.d_o) + qoff, hh * HALF, p.hd, row_ok, p.vec_ok);
+#pragma unroll
+        for (int kd = 0; kd < NKD; kd++) {
+            if constexpr (EPL == 8) {
+                Chunk<T> c;
+#pragma unroll
+                for (int i = 0; i < 8; i++) c.e[i] = raw[kd * 8 + i];
+                of[kd] = __builtin_bit_cast(bf16x8, c.u);
+            } else {
+                of[kd] = raw[kd];
+            }
+        }
+    }
+    const long lrow = ((long)b * p.nh + head) * p.seq + tq;
+    const float lse2 = row_ok ? p.lse[lrow] * kLog2e : INFINITY;
+    const float dlt = row_ok ? p.delta[lrow] : 0.0f;
+
+    f32x16 dqt[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) dqt[i] = zero16();
+
+    for (int kt = 0; kt < n_kt; kt++) {
+        const int k0 = kt * BN;
+        const int nrows = min(BN, p.seq - k0);
+        __syncthreads();
+        stage_rows<T, BN, DP, LDK>(sK, kg + (long)k0 * kvrs, kvrs, nrows, p.hd, p.vec_ok, nthreads);
+        stage_rows<T, BN, DP, LDK>(sV, vg + (long)k0 * kvrs, kvrs, nrows, p.hd, p.vec_ok, nthreads);
+        stage_rows_t<T, BN, DP, LDT>(sKt, kg + (long)k0 * kvrs, kvrs, nrows, p.hd, p.vec_ok, nthreads);
+        __syncthreads();
+        if (!wave_active || k0 > wave_last) continue;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const int kb0 = k0 + kb * 32;
+            if (kb0 > wave_last) continue;
+            f32x16 s = zero16(), dp = zero16();
+            const T* krow = sK + (kb * 32 + l32) * LDK + hh * HALF;
+            const T* vrow = sV + (kb * 32 + l32) * LDK + hh * HALF;
+            if constexpr (EPL == 8) {
+#pragma unroll
+                for (int kd = 0; kd < NKD; kd++) {
+                    s = mfma32(load_bf16x8(krow + kd * 8), qf[kd], s);
+                    dp = mfma32(load_bf16x8(vrow + kd * 8), of[kd], dp);
+                }
+            } else {
+#pragma unroll
+                for (int kd = 0; kd < NKD; kd += 4) {
+                    const float4 a = *reinterpret_cast<const float4*>(krow + kd);
+                    const float4 c = *reinterpret_cast<const float4*>(vrow + kd);
+                    s = mfma32(a.x, qf[kd + 0], s);
+                    s = mfma32(a.y, qf[kd + 1], s);
+                    s = mfma32(a.z, qf[kd + 2], s);
+                    s = mfma32(a.w, qf[kd + 3], s);
+                    dp = mfma32(c.x, of[kd + 0], dp);
+                    dp = mfma32(c.y, of[kd + 1], dp);
+                    dp = mfma32(c.z, of[kd + 2], dp);
+                    dp = mfma32(c.w, of[kd + 3], dp);
+                }
+            }
+            const bool need_mask = kb0 + 31 > t_wave;
+            float ds[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = kb0 + (r >> 2) * 8 + hh * 4 + (r & 3);
+                float pv = exp2f(s[r] * p.sl2 - lse2);
+                if (need_mask && key > tq) pv = 0.0f;
+                ds[r] = pv * (dp[r] - dlt) * p.scale;
+            }
+            if constexpr (EPL == 8) {
+                const bf16x8 d0 = pack_bf16x8(&ds[0]), d1 = pack_bf16x8(&ds[8]);
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    const T* kt_ = sKt + (db * 32 + l32) * LDT + kb * 32 + hh * 4;
+                    dqt[db] = mfma32(load_bf16x4x2(kt_, kt_ + 8), d0, dqt[db]);
+                    dqt[db] = mfma32(load_bf16x4x2(kt_ + 16, kt_ + 24), d1, dqt[db]);
+                }
+            } else {
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    const T* kt_ = sKt + (db * 32 + l32) * LDT + kb * 32 + hh * 4;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float4 a = *reinterpret_cast<const float4*>(kt_ + j * 8);
+                        dqt[db] = mfma32(a.x, ds[j * 4 + 0], dqt[db]);
+                        dqt[db] = mfma32(a.y, ds[j * 4 + 1], dqt[db]);
+                        dqt[db] = mfma32(a.z, ds[j * 4 + 2], dqt[db]);
+                        dqt[db] = mfma32(a.w, ds[j * 4 + 3], dqt[db]);
+                    }
+                }
+            }
+        }
+    }
+
+    if (!wave_active || !row_ok) return;
+    float* dqrow = p.dq + qoff;
+#pragma unroll
+    for (int db = 0; db < NDB; db++) add_row_block(dqrow, dqt[db], db * 32, hh, p.hd, p.g_vec_ok);
+}
+
+static int pick_hpw_b(int group, int cap) {
+    for (int h = cap < group ? cap : group; h >= 1; h--)
+        if (group % h == 0) return h;
+    return 1;
+}
+
+template <typename T, int DP>
+static hipError_t bwd_dp(const BwdParams& p, hipStream_t st, int kv_waves, int q_waves) {
+    const long rows = (long)p.batch * p.seq * p.nh;
+    hipLaunchKernelGGL((attn_bwd_delta_kernel<T>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    constexpr int BM = sizeof(T) == 2 ? 64 : 32;
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, DP, BM>), dim3(p.n_wg_kv), dim3(64 * kv_waves), 0, st, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    constexpr int BN = sizeof(T) == 2 ? 64 : 32;
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, DP, BN>), dim3(p.n_wg_q), dim3(64 * q_waves), 0, st, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
+                           const float* o, const float* lse, float* delta, float* dq, float* dk, float* dv,
+                           hipStream_t st, const Tuning& tu) {
+    if (d.batch == 0 || d.seq == 0 || d.nh == 0) return hipSuccess;
+    BwdParams p{};
+    p.d_o = d_o;
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.o = o;
+    p.lse = lse;
+    p.delta = delta;
+    p.dq = dq;
+    p.dk = dk;
+    p.dv = dv;
+    p.batch = d.batch;
+    p.seq = d.seq;
+    p.nh = d.nh;
+    p.nkv = d.nkv;
+    p.hd = d.hd;
+    p.group = d.nh / d.nkv;
+    const int kv_waves = tu.bwd_kv_waves > 0 ? tu.bwd_kv_waves : 4;
+    p.kv_tile = 32 * kv_waves;
+    p.n_kvtiles = (d.seq + p.kv_tile - 1) / p.kv_tile;
+    long nkv_wg = (long)p.n_kvtiles * d.nkv * d.batch;
+    p.hpw = pick_hpw_b(p.group, 4);
+    p.tpw = 4 / p.hpw > 0 ? 4 / p.hpw : 1;
+    p.n_sub = p.group / p.hpw;
+    p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
+    long nq_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+    if (nkv_wg > 0x7fffffffL || nq_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    p.n_wg_kv = (int)nkv_wg;
+    p.n_wg_q = (int)nq_wg;
+    p.scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:163
+    p.sl2 = p.scale * kLog2e;
+    p.q_bs = (long)d.seq * d.nh * d.hd;
+    p.kv_bs = (long)d.seq * d.nkv * d.hd;
+    const int ch = dt == kBF16 ? 8 : 4;
+    const size_t al = 16;
+    p.vec_ok = (d.hd % ch == 0) && ((uintptr_t)q % al == 0) && ((uintptr_t)k % al == 0) &&
+               ((uintptr_t)v % al == 0) && ((uintptr_t)d_o % al == 0);
+    p.g_vec_ok = (d.hd % 4 == 0) && ((uintptr_t)dq % al == 0) && ((uintptr_t)dk % al == 0) && ((uintptr_t)dv % al == 0);
+    p.xcd = tu.xcd_remap;
+    const int q_waves = p.hpw * p.tpw;
+    const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;
+    if (dt == kBF16) {
+        switch (dp) {
+            case 32: return bwd_dp<bf16_bits, 32>(p, st, kv_waves, q_waves);
+            case 64: return bwd_dp<bf16_bits, 64>(p, st, kv_waves, q_waves);
+            case 128: return bwd_dp<bf16_bits, 128>(p, st, kv_waves, q_waves);
+            default: return bwd_dp<bf16_bits, 256>(p, st, kv_waves, q_waves);
+        }
+    }
+    switch (dp) {
+        case 32: return bwd_dp<float, 32>(p, st, kv_waves, q_waves);
+        case 64: return bwd_dp<float, 64>(p, st, kv_waves, q_waves);
+        case 128: return bwd_dp<float, 128>(p, st, kv_waves, q_waves);
+        default: return bwd_dp<float, 256>(p, st, kv_waves, q_waves);
+    }
+}
+
+}  // namespace cfattn

@@ -1,0 +1,296 @@
+// Causal grouped-query attention forward on gfx950 MFMA.
+//
+// Computes, per query head h and token t (reference semantics:
+// crates/core/src/ops/attention.rs:46-122):
+//   O[t,h]   = sum_{j<=t} softmax_j(q_t . k_j / sqrt(D)) v_j   (overwritten)
+//   lse[h,t] = max_j s_tj + ln sum_j exp(s_tj - max)            (overwritten)
+// with KV head g = h / group serving `group` consecutive query heads.
+//
+// Work decomposition.  A workgroup owns one tile of TT = 32*tpw tokens and
+// `hpw` query heads of one GQA group (hpw divides group).  Each wave owns 32
+// tokens of one head.  K/V tiles of BN keys are staged once into LDS and
+// shared by every head and token block of the workgroup.  Per wave and key
+// tile:
+//   S^T = K Q^T  (MFMA, K from LDS rows, Q held in registers)
+//        -> each lane owns one query (column) and 16 keys of every 32-key
+//           block, so the row max needs one exchange between lane halves;
+//   online softmax in the exp2 domain (running max m, per-lane partial sum);
+//   O^T += V^T P^T (MFMA, V^T read from a transposed LDS tile, P^T fed
+//        straight from the S^T accumulators, rounded to bf16 in bf16 mode).
+// Workgroups are ordered longest-first (most key tiles) and remapped so each
+// XCD works through contiguous (sequence, KV head) ranges.
+#include "cfattn_common.hpp"
+#include "cfattn_kernels.hpp"
+
+namespace cfattn {
+
+struct FwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    float* o;
+    float* lse;
+    int seq, nh, nkv, hd;
+    int group, hpw, tpw, n_sub, n_ttiles, n_wg;
+    float sl2;  // softmax scale * log2(e)
+    long q_bs, kv_bs;
+    int vec_ok, o_vec_ok, xcd;
+};
+
+template <typename T, int DP, int BN>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams p) {
+    using M = Mode<T>;
+    constexpr int EPL = M::EPL;
+    constexpr int HALF = DP / 2;     // head-dim range of each lane half
+    constexpr int NKD = HALF / EPL;  // MFMAs over the head dim per 32x32 block
+    constexpr int NDB = DP / 32;     // 32-row head-dim blocks of O^T
+    constexpr int NKB = BN / 32;     // 32-key blocks per key tile
+    constexpr int LDK = RowLD<T, DP>::value;
+    constexpr int LDV = TLD<T, BN>::value;
+    __shared__ __attribute__((aligned(16))) T sK[BN * LDK];
+    __shared__ __attribute__((aligned(16))) T sVt[DP * LDV];
+
+    const int nthreads = blockDim.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
+    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;  // longest tiles first
+    int rest = id / p.n_ttiles;
+    const int sub = rest % p.n_sub;
+    rest /= p.n_sub;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+
+    const int head = g * p.group + sub * p.hpw + wave % p.hpw;
+    const int TT = 32 * p.tpw;
+    const int t_wave = tile * TT + (wave / p.hpw) * 32;
+    const int tq = t_wave + l32;
+    const int wg_end = min(p.seq, tile * TT + TT);
+    const int n_kt = (wg_end + BN - 1) / BN;
+    const bool wave_active = t_wave < p.seq;
+    const int wave_last = min(t_wave + 31, p.seq - 1);
+
+    const long qrs = (long)p.nh * p.hd, kvrs = (long)p.nkv * p.hd;
+    const T* qg = static_cast<const T*>(p.q) + (long)b * p.q_bs;
+    const T* kg = static_cast<const T*>(p.k) + (long)b * p.kv_bs + (long)g * p.hd;
+    const T* vg = static_cast<const T*>(p.v) + (long)b * p.kv_bs + (long)g * p.hd;
+
+    // Q^T operand for this lane: query tq, head dims [hh*HALF, hh*HALF+HALF).
+    T qraw[HALF];
+    load_row_frag<T, HALF>(qraw, qg + (long)tq * qrs + (long)head * p.hd, hh * HALF, p.hd, tq < p.seq, p.vec_ok);
+    typename M::frag qf[NKD];
+#pragma unroll
+    for (int kd = 0; kd < NKD; kd++) {
+        if constexpr (EPL == 8) {
+            Chunk<T> c;
+#pragma unroll
+            for (int i = 0; i < 8; i++) c.e[i] = qraw[kd * 8 + i];
+            qf[kd] = __builtin_bit_cast(bf16x8, c.u);
+        } else {
+            qf[kd] = qraw[kd];
+        }
+    }
+
+    f32x16 oacc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) oacc[i] = zero16();
+    float m2 = -INFINITY, lsum = 0.0f;
+
+    for (int kt = 0; kt < n_kt; kt++) {
+        const int k0 = kt * BN;
+        const int nrows = min(BN, p.seq - k0);
+        __syncthreads();
+        stage_rows<T, BN, DP, LDK>(sK, kg + (long)k0 * kvrs, kvrs, nrows, p.hd, p.vec_ok, nthreads);
+        stage_rows_t<T, BN, DP, LDV>(sVt, vg + (long)k0 * kvrs, kvrs, nrows, p.hd, p.vec_ok, nthreads);
+        __syncthreads();
+        if (!wave_active || k0 > wave_last) continue;
+
+        // S^T blocks: rows = keys k0 + kb*32 + [0,32), columns = this wave's queries.
+        f32x16 s[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            s[kb] = zero16();
+            if (k0 + kb * 32 > wave_last) continue;
+            const T* krow = sK + (kb * 32 + l32) * LDK + hh * HALF;
+            if constexpr (EPL == 8) {
+#pragma unroll
+                for (int kd = 0; kd < NKD; kd++) s[kb] = mfma32(load_bf16x8(krow + kd * 8), qf[kd], s[kb]);
+            } else {
+#pragma unroll
+                for (int kd = 0; kd < NKD; kd += 4) {
+                    const float4 a = *reinterpret_cast<const float4*>(krow + kd);
+                    s[kb] = mfma32(a.x, qf[kd + 0], s[kb]);
+                    s[kb] = mfma32(a.y, qf[kd + 1], s[kb]);
+                    s[kb] = mfma32(a.z, qf[kd + 2], s[kb]);
+                    s[kb] = mfma32(a.w, qf[kd + 3], s[kb]);
+                }
+            }
+        }
+
+        // Scale into the exp2 domain, apply the causal mask, row max.
+        const bool need_mask = k0 + BN - 1 > t_wave;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float x = s[kb][r] * p.sl2;
+                if (need_mask) {
+                    const int key = k0 + kb * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+                    if (key > tq) x = -INFINITY;
+                }
+                s[kb][r] = x;
+                mx = fmaxf(mx, x);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // Key 0 is in the first tile every wave processes, so m2 is finite
+        // from the first tile on and alpha never sees inf - inf.
+        const float mnew = fmaxf(m2, mx);
+        const float alpha = exp2f(m2 - mnew);
+        m2 = mnew;
+        lsum *= alpha;
+#pragma unroll
+        for (int i = 0; i < NDB; i++) oacc[i] *= alpha;
+
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float e = exp2f(s[kb][r] - mnew);
+                s[kb][r] = e;
+                lsum += e;
+            }
+        }
+
+        // O^T += V^T P^T.
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            if (k0 + kb * 32 > wave_last) continue;
+            float pv[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) pv[r] = s[kb][r];
+            if constexpr (EPL == 8) {
+                const bf16x8 p0 = pack_bf16x8(&pv[0]);
+                const bf16x8 p1 = pack_bf16x8(&pv[8]);
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    const T* vt = sVt + (db * 32 + l32) * LDV + kb * 32 + hh * 4;
+                    oacc[db] = mfma32(load_bf16x4x2(vt, vt + 8), p0, oacc[db]);
+                    oacc[db] = mfma32(load_bf16x4x2(vt + 16, vt + 24), p1, oacc[db]);
+                }
+            } else {
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    const T* vt = sVt + (db * 32 + l32) * LDV + kb * 32 + hh * 4;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float4 a = *reinterpret_cast<const float4*>(vt + j * 8);
+                        oacc[db] = mfma32(a.x, pv[j * 4 + 0], oacc[db]);
+                        oacc[db] = mfma32(a.y, pv[j * 4 + 1], oacc[db]);
+                        oacc[db] = mfma32(a.z, pv[j * 4 + 2], oacc[db]);
+                        oacc[db] = mfma32(a.w, pv[j * 4 + 3], oacc[db]);
+                    }
+                }
+            }
+        }
+    }
+
+    if (!wave_active) return;
+    const float ltot = lsum + __shfl_xor(lsum, 32);
+    if (tq >= p.seq) return;
+    const float inv = 1.0f / ltot;
+    float* orow = p.o + (long)b * p.q_bs + (long)tq * qrs + (long)head * p.hd;
+#pragma unroll
+    for (int db = 0; db < NDB; db++) {
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            const int d0 = db * 32 + rq * 8 + hh * 4;
+            const float4 v = make_float4(oacc[db][rq * 4 + 0] * inv, oacc[db][rq * 4 + 1] * inv,
+                                         oacc[db][rq * 4 + 2] * inv, oacc[db][rq * 4 + 3] * inv);
+            if (p.o_vec_ok && d0 + 4 <= p.hd) {
+                *reinterpret_cast<float4*>(orow + d0) = v;
+            } else {
+                if (d0 + 0 < p.hd) orow[d0 + 0] = v.x;
+                if (d0 + 1 < p.hd) orow[d0 + 1] = v.y;
+                if (d0 + 2 < p.hd) orow[d0 + 2] = v.z;
+                if (d0 + 3 < p.hd) orow[d0 + 3] = v.w;
+            }
+        }
+    }
+    if (hh == 0) p.lse[((long)b * p.nh + head) * p.seq + tq] = (m2 + log2f(ltot)) * kLn2;
+}
+
+// Heads per workgroup: the largest divisor of `group` not above `cap`.
+static int pick_hpw(int group, int cap) {
+    for (int h = cap < group ? cap : group; h >= 1; h--)
+        if (group % h == 0) return h;
+    return 1;
+}
+
+template <typename T, int DP, int BN>
+static hipError_t fwd_dispatch(const Dims& d, FwdParams p, hipStream_t st, int nwaves) {
+    hipLaunchKernelGGL((attn_fwd_kernel<T, DP, BN>), dim3(p.n_wg), dim3(64 * nwaves), 0, st, p);
+    return hipGetLastError();
+}
+
+template <typename T, int DP>
+static hipError_t fwd_dp(const Dims& d, FwdParams p, hipStream_t st, int nwaves) {
+    // fp32 tiles are twice the bytes: keep them to 32 keys.
+    if constexpr (sizeof(T) == 2)
+        return fwd_dispatch<T, DP, 64>(d, p, st, nwaves);
+    else
+        return fwd_dispatch<T, DP, 32>(d, p, st, nwaves);
+}
+
+hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k, const void* v, float* o,
+                           float* lse, hipStream_t st, const Tuning& tu) {
+    if (d.batch == 0 || d.seq == 0 || d.nh == 0) return hipSuccess;
+    FwdParams p{};
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.o = o;
+    p.lse = lse;
+    p.seq = d.seq;
+    p.nh = d.nh;
+    p.nkv = d.nkv;
+    p.hd = d.hd;
+    p.group = d.nh / d.nkv;
+    p.hpw = tu.fwd_heads_per_wg > 0 ? pick_hpw(p.group, tu.fwd_heads_per_wg) : pick_hpw(p.group, 4);
+    p.tpw = tu.fwd_tblocks_per_wg > 0 ? tu.fwd_tblocks_per_wg : (4 / p.hpw > 0 ? 4 / p.hpw : 1);
+    if (p.hpw * p.tpw > 4) p.tpw = 4 / p.hpw > 0 ? 4 / p.hpw : 1;
+    p.n_sub = p.group / p.hpw;
+    p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
+    long n_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+    if (n_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    p.n_wg = (int)n_wg;
+    const float scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:62
+    p.sl2 = scale * kLog2e;
+    p.q_bs = (long)d.seq * d.nh * d.hd;
+    p.kv_bs = (long)d.seq * d.nkv * d.hd;
+    const int ch = dt == kBF16 ? 8 : 4;
+    const size_t al = 16;
+    p.vec_ok = (d.hd % ch == 0) && ((uintptr_t)q % al == 0) && ((uintptr_t)k % al == 0) && ((uintptr_t)v % al == 0);
+    p.o_vec_ok = (d.hd % 4 == 0) && ((uintptr_t)o % al == 0);
+    p.xcd = tu.xcd_remap;
+    const int nwaves = p.hpw * p.tpw;
+    const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;
+    if (dt == kBF16) {
+        switch (dp) {
+            case 32: return fwd_dp<bf16_bits, 32>(d, p, st, nwaves);
+            case 64: return fwd_dp<bf16_bits, 64>(d, p, st, nwaves);
+            case 128: return fwd_dp<bf16_bits, 128>(d, p, st, nwaves);
+            default: return fwd_dp<bf16_bits, 256>(d, p, st, nwaves);
+        }
+    }
+    switch (dp) {
+        case 32: return fwd_dp<float, 32>(d, p, st, nwaves);
+        case 64: return fwd_dp<float, 64>(d, p, st, nwaves);
+        case 128: return fwd_dp<float, 128>(d, p, st, nwaves);
+        default: return fwd_dp<float, 256>(d, p, st, nwaves);
+    }
+}
+
+}  // namespace cfattn

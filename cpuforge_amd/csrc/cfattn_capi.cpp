@@ -1,0 +1,545 @@
+// C ABI of libcfattn.so (declared in include/cfattn.h).
+//
+// Host-side plumbing only: argument checks that mirror the reference's
+// asserts, a per-context stream and grow-only device buffer pool, host<->device
+// copies for the host-slice entry points, and dispatch to the gfx950 kernels.
+// There is no CPU compute path: every result comes from the HIP kernels.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "cfattn.h"
+#include "cfattn_kernels.hpp"
+
+struct cfattn_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int mode = CFATTN_F32;
+    std::string err;
+    std::mutex mu;
+    enum Slot { Q, K, V, O, LSE, DO_, DQ, DK, DV, QB, KB, VB, DOB, DELTA, PARTIAL, DQROT, DKROT, NSLOT };
+    void* buf[NSLOT] = {};
+    size_t cap[NSLOT] = {};
+};
+
+namespace {
+
+using cfattn::Dims;
+using cfattn::Dtype;
+
+int fail(cfattn_ctx* c, int code, const char* fmt, ...) {
+    char msg[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+    if (c) c->err = msg;
+    return code;
+}
+
+int hip_fail(cfattn_ctx* c, hipError_t e, const char* what) {
+    return fail(c, CFATTN_ERR_HIP, "%s: %s (%s)", what, hipGetErrorName(e), hipGetErrorString(e));
+}
+
+// Makes the context's device current for the duration of a call and restores
+// the caller's device afterwards.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+// Grow-only device buffer of a pool slot.
+void* slot(cfattn_ctx* c, int s, size_t bytes, int* rc) {
+    if (bytes == 0) bytes = 256;
+    if (c->cap[s] >= bytes) return c->buf[s];
+    if (c->buf[s]) {
+        (void)hipFree(c->buf[s]);
+        c->buf[s] = nullptr;
+        c->cap[s] = 0;
+    }
+    size_t want = (bytes + 4095) & ~(size_t)4095;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        *rc = fail(c, CFATTN_ERR_NOMEM, "hipMalloc of %zu bytes failed: %s", want, hipGetErrorString(e));
+        return nullptr;
+    }
+    c->buf[s] = p;
+    c->cap[s] = want;
+    return p;
+}
+
+// AttnShape::check plus the head-dim / size limits of the kernels
+// (core/src/ops/attention.rs:35-38).
+int check_shape(cfattn_ctx* c, const cfattn_shape& s) {
+    if (!(s.n_kv > 0 && s.n_heads % s.n_kv == 0))
+        return fail(c, CFATTN_ERR_SHAPE, "n_heads must be a multiple of n_kv (n_heads=%zu, n_kv=%zu)", s.n_heads,
+                    s.n_kv);
+    if (s.head_dim == 0 || s.head_dim > (size_t)cfattn::kMaxHeadDim)
+        return fail(c, CFATTN_ERR_UNSUPPORTED, "head_dim=%zu outside 1..=%d", s.head_dim, cfattn::kMaxHeadDim);
+    const size_t lim = (size_t)1 << 31;
+    if (s.seq >= lim || s.n_heads >= lim || s.seq * s.n_heads >= lim || s.seq * s.n_heads * s.head_dim >= lim)
+        return fail(c, CFATTN_ERR_UNSUPPORTED, "shape too large (seq=%zu, n_heads=%zu, head_dim=%zu)", s.seq,
+                    s.n_heads, s.head_dim);
+    return CFATTN_OK;
+}
+
+int check_len(cfattn_ctx* c, const char* name, size_t got, size_t want) {
+    if (got != want)
+        return fail(c, CFATTN_ERR_SHAPE, "assertion `left == right` failed: %s.len() = %zu, expected %zu", name, got,
+                    want);
+    return CFATTN_OK;
+}
+
+int check_dtype(cfattn_ctx* c, int dt) {
+    if (dt != CFATTN_F32 && dt != CFATTN_BF16) return fail(c, CFATTN_ERR_ARG, "unknown dtype %d", dt);
+    return CFATTN_OK;
+}
+
+Dims dims_of(const cfattn_shape& s, size_t batch) {
+    return Dims{(int)batch, (int)s.seq, (int)s.n_heads, (int)s.n_kv, (int)s.head_dim};
+}
+
+hipStream_t pick_stream(cfattn_ctx* c, void* st) { return st ? static_cast<hipStream_t>(st) : c->stream; }
+
+#define CF_TRY(expr)                 \
+    do {                             \
+        int _rc = (expr);            \
+        if (_rc != CFATTN_OK) return _rc; \
+    } while (0)
+
+#define CF_HIP(c, expr, what)                                    \
+    do {                                                         \
+        hipError_t _e = (expr);                                  \
+        if (_e != hipSuccess) return hip_fail((c), _e, (what));  \
+    } while (0)
+
+// Uploads an f32 host slice into a pool slot; with bf16 compute also rounds
+// it into the matching bf16 slot.  Returns the device pointer the kernels read.
+const void* upload(cfattn_ctx* c, int s32, int s16, const float* host, size_t n, bool bf16, int* rc) {
+    float* d = static_cast<float*>(slot(c, s32, n * 4, rc));
+    if (!d) return nullptr;
+    hipError_t e = hipMemcpyAsync(d, host, n * 4, hipMemcpyHostToDevice, c->stream);
+    if (e != hipSuccess) {
+        *rc = hip_fail(c, e, "hipMemcpyAsync H2D");
+        return nullptr;
+    }
+    if (!bf16) return d;
+    uint16_t* b = static_cast<uint16_t*>(slot(c, s16, n * 2, rc));
+    if (!b) return nullptr;
+    e = cfattn::launch_f32_to_bf16(d, b, n, c->stream);
+    if (e != hipSuccess) {
+        *rc = hip_fail(c, e, "f32_to_bf16 launch");
+        return nullptr;
+    }
+    return b;
+}
+
+int forward_host(cfattn_ctx* c, const float* q, size_t q_len, const float* k, size_t k_len, const float* v,
+                 size_t v_len, float* o, size_t o_len, float* lse, size_t lse_len, cfattn_shape s, size_t q_block) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    // attention.rs:55-58 order: shape check, then v, o and lse lengths.
+    if (!(s.n_kv > 0 && s.n_heads % s.n_kv == 0)) CF_TRY(check_shape(c, s));
+    CF_TRY(check_len(c, "q", q_len, s.seq * s.n_heads * s.head_dim));
+    CF_TRY(check_len(c, "k", k_len, s.seq * s.n_kv * s.head_dim));
+    CF_TRY(check_len(c, "v", v_len, k_len));
+    CF_TRY(check_len(c, "o", o_len, q_len));
+    CF_TRY(check_len(c, "lse", lse_len, s.n_heads * s.seq));
+    if (q_block == 0) return fail(c, CFATTN_ERR_ARG, "q_block must be positive");
+    if (s.seq == 0 || s.n_heads == 0) return CFATTN_OK;
+    CF_TRY(check_shape(c, s));
+    if (!q || !k || !v || !o || !lse) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    DeviceGuard dg(c->device);
+    if (!dg.ok) return fail(c, CFATTN_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+    const bool bf = c->mode == CFATTN_BF16;
+    int rc = CFATTN_OK;
+    const void* dq = upload(c, cfattn_ctx::Q, cfattn_ctx::QB, q, q_len, bf, &rc);
+    if (!dq) return rc;
+    const void* dk = upload(c, cfattn_ctx::K, cfattn_ctx::KB, k, k_len, bf, &rc);
+    if (!dk) return rc;
+    const void* dv = upload(c, cfattn_ctx::V, cfattn_ctx::VB, v, v_len, bf, &rc);
+    if (!dv) return rc;
+    float* dout = static_cast<float*>(slot(c, cfattn_ctx::O, o_len * 4, &rc));
+    if (!dout) return rc;
+    float* dlse = static_cast<float*>(slot(c, cfattn_ctx::LSE, lse_len * 4, &rc));
+    if (!dlse) return rc;
+    CF_HIP(c, cfattn::launch_attn_fwd(bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), dq, dk, dv, dout, dlse,
+                                      c->stream, cfattn::Tuning{}),
+           "attention forward launch");
+    CF_HIP(c, hipMemcpyAsync(o, dout, o_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H o");
+    CF_HIP(c, hipMemcpyAsync(lse, dlse, lse_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H lse");
+    CF_HIP(c, hipStreamSynchronize(c->stream), "attention forward");
+    return CFATTN_OK;
+}
+
+int backward_host(cfattn_ctx* c, const float* d_o, size_t d_o_len, const float* q, size_t q_len, const float* k,
+                  size_t k_len, const float* v, size_t v_len, const float* o, size_t o_len, const float* lse,
+                  size_t lse_len, float* dq, size_t dq_len, float* dk, size_t dk_len, float* dv, size_t dv_len,
+                  cfattn_shape s, size_t q_block) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    // attention.rs:155-158 order.
+    if (!(s.n_kv > 0 && s.n_heads % s.n_kv == 0)) CF_TRY(check_shape(c, s));
+    CF_TRY(check_len(c, "q", q_len, s.seq * s.n_heads * s.head_dim));
+    CF_TRY(check_len(c, "k", k_len, s.seq * s.n_kv * s.head_dim));
+    CF_TRY(check_len(c, "v", v_len, k_len));
+    CF_TRY(check_len(c, "dk", dk_len, k_len));
+    CF_TRY(check_len(c, "dv", dv_len, k_len));
+    CF_TRY(check_len(c, "d_o", d_o_len, q_len));
+    CF_TRY(check_len(c, "o", o_len, q_len));
+    CF_TRY(check_len(c, "dq", dq_len, q_len));
+    CF_TRY(check_len(c, "lse", lse_len, s.n_heads * s.seq));
+    if (q_block == 0) return fail(c, CFATTN_ERR_ARG, "q_block must be positive");
+    if (s.seq == 0 || s.n_heads == 0) return CFATTN_OK;
+    CF_TRY(check_shape(c, s));
+    if (!d_o || !q || !k || !v || !o || !lse || !dq || !dk || !dv) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    DeviceGuard dg(c->device);
+    if (!dg.ok) return fail(c, CFATTN_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+    const bool bf = c->mode == CFATTN_BF16;
+    int rc = CFATTN_OK;
+    const void* ddo = upload(c, cfattn_ctx::DO_, cfattn_ctx::DOB, d_o, d_o_len, bf, &rc);
+    if (!ddo) return rc;
+    const void* dq_in = upload(c, cfattn_ctx::Q, cfattn_ctx::QB, q, q_len, bf, &rc);
+    if (!dq_in) return rc;
+    const void* dk_in = upload(c, cfattn_ctx::K, cfattn_ctx::KB, k, k_len, bf, &rc);
+    if (!dk_in) return rc;
+    const void* dv_in = upload(c, cfattn_ctx::V, cfattn_ctx::VB, v, v_len, bf, &rc);
+    if (!dv_in) return rc;
+    const float* d_out = static_cast<const float*>(upload(c, cfattn_ctx::O, -1, o, o_len, false, &rc));
+    if (!d_out) return rc;
+    const float* d_lse = static_cast<const float*>(upload(c, cfattn_ctx::LSE, -1, lse, lse_len, false, &rc));
+    if (!d_lse) return rc;
+    float* g_q = static_cast<float*>(slot(c, cfattn_ctx::DQ, dq_len * 4, &rc));
+    float* g_k = g_q ? static_cast<float*>(slot(c, cfattn_ctx::DK, dk_len * 4, &rc)) : nullptr;
+    float* g_v = g_k ? static_cast<float*>(slot(c, cfattn_ctx::DV, dv_len * 4, &rc)) : nullptr;
+    float* delta = g_v ? static_cast<float*>(slot(c, cfattn_ctx::DELTA, s.n_heads * s.seq * 4, &rc)) : nullptr;
+    if (!delta) return rc;
+    CF_HIP(c, hipMemcpyAsync(g_q, dq, dq_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dq");
+    CF_HIP(c, hipMemcpyAsync(g_k, dk, dk_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dk");
+    CF_HIP(c, hipMemcpyAsync(g_v, dv, dv_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dv");
+    CF_HIP(c, cfattn::launch_attn_bwd(bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), ddo, dq_in, dk_in, dv_in,
+                                      d_out, d_lse, delta, g_q, g_k, g_v, c->stream, cfattn::Tuning{}),
+           "attention backward launch");
+    CF_HIP(c, hipMemcpyAsync(dq, g_q, dq_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H dq");
+    CF_HIP(c, hipMemcpyAsync(dk, g_k, dk_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H dk");
+    CF_HIP(c, hipMemcpyAsync(dv, g_v, dv_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H dv");
+    CF_HIP(c, hipStreamSynchronize(c->stream), "attention backward");
+    return CFATTN_OK;
+}
+
+int check_prologue(cfattn_ctx* c, const cfattn_shape& s, const cfattn_prologue* pr) {
+    if (!pr || !pr->cos || !pr->sin) return fail(c, CFATTN_ERR_ARG, "prologue needs a cos/sin table");
+    if (s.head_dim % 2 != 0) return fail(c, CFATTN_ERR_SHAPE, "head_dim must be even");  // rope.rs:47
+    if (pr->pos0 + s.seq > pr->max_pos)
+        return fail(c, CFATTN_ERR_SHAPE, "position %zu exceeds cache size %zu", pr->pos0 + s.seq,
+                    pr->max_pos);  // rope.rs:73
+    if ((pr->q_norm == nullptr) != (pr->k_norm == nullptr))
+        return fail(c, CFATTN_ERR_ARG, "q_norm and k_norm must both be given or both be NULL");
+    if (pr->max_pos >= ((size_t)1 << 31)) return fail(c, CFATTN_ERR_UNSUPPORTED, "max_pos too large");
+    return CFATTN_OK;
+}
+
+cfattn::Prologue to_prologue(const cfattn_prologue* pr) {
+    cfattn::Prologue p;
+    p.cos = pr->cos;
+    p.sin = pr->sin;
+    p.max_pos = (int)pr->max_pos;
+    p.pos0 = (int)pr->pos0;
+    p.qw = pr->q_norm;
+    p.kw = pr->k_norm;
+    p.eps = pr->eps;
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cfattn_create(int device, cfattn_ctx** out) {
+    if (!out) return CFATTN_ERR_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return CFATTN_ERR_HIP;
+    cfattn_ctx* c = new cfattn_ctx();
+    c->device = device;
+    DeviceGuard dg(device);
+    if (!dg.ok || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return CFATTN_ERR_HIP;
+    }
+    *out = c;
+    return CFATTN_OK;
+}
+
+int cfattn_destroy(cfattn_ctx* c) {
+    if (!c) return CFATTN_ERR_ARG;
+    {
+        DeviceGuard dg(c->device);
+        if (c->stream) {
+            (void)hipStreamSynchronize(c->stream);
+            (void)hipStreamDestroy(c->stream);
+        }
+        for (int i = 0; i < cfattn_ctx::NSLOT; i++)
+            if (c->buf[i]) (void)hipFree(c->buf[i]);
+    }
+    delete c;
+    return CFATTN_OK;
+}
+
+const char* cfattn_last_error(const cfattn_ctx* c) { return c ? c->err.c_str() : "null context"; }
+
+int cfattn_set_mode(cfattn_ctx* c, int dtype) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    CF_TRY(check_dtype(c, dtype));
+    c->mode = dtype;
+    return CFATTN_OK;
+}
+
+int cfattn_get_mode(const cfattn_ctx* c) { return c ? c->mode : -1; }
+
+int cfattn_synchronize(cfattn_ctx* c) {
+    if (!c) return CFATTN_ERR_ARG;
+    DeviceGuard dg(c->device);
+    CF_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return CFATTN_OK;
+}
+
+void* cfattn_stream(cfattn_ctx* c) { return c ? static_cast<void*>(c->stream) : nullptr; }
+
+int cfattn_attention_forward(cfattn_ctx* c, const float* q, size_t q_len, const float* k, size_t k_len,
+                             const float* v, size_t v_len, float* o, size_t o_len, float* lse, size_t lse_len,
+                             cfattn_shape s) {
+    return forward_host(c, q, q_len, k, k_len, v, v_len, o, o_len, lse, lse_len, s, 128);
+}
+
+int cfattn_attention_forward_blocked(cfattn_ctx* c, const float* q, size_t q_len, const float* k, size_t k_len,
+                                     const float* v, size_t v_len, float* o, size_t o_len, float* lse,
+                                     size_t lse_len, cfattn_shape s, size_t q_block) {
+    return forward_host(c, q, q_len, k, k_len, v, v_len, o, o_len, lse, lse_len, s, q_block);
+}
+
+int cfattn_attention_backward(cfattn_ctx* c, const float* d_o, size_t d_o_len, const float* q, size_t q_len,
+                              const float* k, size_t k_len, const float* v, size_t v_len, const float* o,
+                              size_t o_len, const float* lse, size_t lse_len, float* dq, size_t dq_len, float* dk,
+                              size_t dk_len, float* dv, size_t dv_len, cfattn_shape s) {
+    return backward_host(c, d_o, d_o_len, q, q_len, k, k_len, v, v_len, o, o_len, lse, lse_len, dq, dq_len, dk,
+                         dk_len, dv, dv_len, s, 128);
+}
+
+int cfattn_attention_backward_blocked(cfattn_ctx* c, const float* d_o, size_t d_o_len, const float* q,
+                                      size_t q_len, const float* k, size_t k_len, const float* v, size_t v_len,
+                                      const float* o, size_t o_len, const float* lse, size_t lse_len, float* dq,
+                                      size_t dq_len, float* dk, size_t dk_len, float* dv, size_t dv_len,
+                                      cfattn_shape s, size_t q_block) {
+    return backward_host(c, d_o, d_o_len, q, q_len, k, k_len, v, v_len, o, o_len, lse, lse_len, dq, dq_len, dk,
+                         dk_len, dv, dv_len, s, q_block);
+}
+
+static int cfattn_fwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const void* q, const void* k, const void* v,
+               float* o, float* lse, void* stream) {
+    CF_TRY(check_dtype(c, dtype));
+    if (batch == 0 || s.seq == 0) return CFATTN_OK;
+    CF_TRY(check_shape(c, s));
+    if (batch * s.seq * s.n_heads >= ((size_t)1 << 31))
+        return fail(c, CFATTN_ERR_UNSUPPORTED, "batch*seq*n_heads too large");
+    if (!q || !k || !v || !o || !lse) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    DeviceGuard dg(c->device);
+    CF_HIP(c, cfattn::launch_attn_fwd((Dtype)dtype, dims_of(s, batch), q, k, v, o, lse, pick_stream(c, stream),
+                                      cfattn::Tuning{}),
+           "attention forward launch");
+    return CFATTN_OK;
+}
+
+int cfattn_fwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const void* q, const void* k, const void* v,
+               float* o, float* lse, void* stream) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    return cfattn_fwd_locked(c, s, batch, dtype, q, k, v, o, lse, stream);
+}
+
+static int cfattn_bwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const void* d_o, const void* q, const void* k,
+               const void* v, const float* o, const float* lse, float* dq, float* dk, float* dv, void* stream) {
+    CF_TRY(check_dtype(c, dtype));
+    if (batch == 0 || s.seq == 0) return CFATTN_OK;
+    CF_TRY(check_shape(c, s));
+    if (batch * s.seq * s.n_heads >= ((size_t)1 << 31))
+        return fail(c, CFATTN_ERR_UNSUPPORTED, "batch*seq*n_heads too large");
+    if (!d_o || !q || !k || !v || !o || !lse || !dq || !dk || !dv) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    DeviceGuard dg(c->device);
+    int rc = CFATTN_OK;
+    float* delta = static_cast<float*>(slot(c, cfattn_ctx::DELTA, batch * s.n_heads * s.seq * 4, &rc));
+    if (!delta) return rc;
+    CF_HIP(c, cfattn::launch_attn_bwd((Dtype)dtype, dims_of(s, batch), d_o, q, k, v, o, lse, delta, dq, dk, dv,
+                                      pick_stream(c, stream), cfattn::Tuning{}),
+           "attention backward launch");
+    return CFATTN_OK;
+}
+
+int cfattn_bwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const void* d_o, const void* q, const void* k,
+               const void* v, const float* o, const float* lse, float* dq, float* dk, float* dv, void* stream) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    return cfattn_bwd_locked(c, s, batch, dtype, d_o, q, k, v, o, lse, dq, dk, dv, stream);
+}
+
+static int cfattn_prologue_fwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const cfattn_prologue* pr,
+                        const float* q_pre, const float* k_pre, void* q_out, void* k_out, float* q_rstd,
+                        float* k_rstd, void* stream) {
+    CF_TRY(check_dtype(c, dtype));
+    if (batch == 0 || s.seq == 0) return CFATTN_OK;
+    CF_TRY(check_shape(c, s));
+    CF_TRY(check_prologue(c, s, pr));
+    if (!q_pre || !k_pre || !q_out || !k_out) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (pr->q_norm && (!q_rstd || !k_rstd)) return fail(c, CFATTN_ERR_ARG, "q/k norm needs rstd outputs");
+    DeviceGuard dg(c->device);
+    CF_HIP(c, cfattn::launch_prologue_fwd((Dtype)dtype, dims_of(s, batch), to_prologue(pr), q_pre, k_pre, q_out,
+                                          k_out, q_rstd, k_rstd, pick_stream(c, stream)),
+           "prologue forward launch");
+    return CFATTN_OK;
+}
+
+int cfattn_prologue_fwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const cfattn_prologue* pr,
+                        const float* q_pre, const float* k_pre, void* q_out, void* k_out, float* q_rstd,
+                        float* k_rstd, void* stream) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    return cfattn_prologue_fwd_locked(c, s, batch, dtype, pr, q_pre, k_pre, q_out, k_out, q_rstd, k_rstd, stream);
+}
+
+static int cfattn_prologue_bwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, const cfattn_prologue* pr, const float* dq,
+                        const float* dk, const float* q_pre, const float* k_pre, const float* q_rstd,
+                        const float* k_rstd, float* dq_pre, float* dk_pre, float* dq_norm, float* dk_norm,
+                        void* stream) {
+    if (batch == 0 || s.seq == 0) return CFATTN_OK;
+    CF_TRY(check_shape(c, s));
+    CF_TRY(check_prologue(c, s, pr));
+    if (!dq || !dk || !dq_pre || !dk_pre) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (pr->q_norm && (!q_pre || !k_pre || !q_rstd || !k_rstd || !dq_norm || !dk_norm))
+        return fail(c, CFATTN_ERR_ARG, "q/k norm backward needs q_pre, k_pre, rstd and gain-gradient buffers");
+    DeviceGuard dg(c->device);
+    const Dims d = dims_of(s, batch);
+    int rc = CFATTN_OK;
+    float* partial = nullptr;
+    if (pr->q_norm) {
+        partial = static_cast<float*>(slot(c, cfattn_ctx::PARTIAL, cfattn::prologue_bwd_scratch_floats(d) * 4, &rc));
+        if (!partial) return rc;
+    }
+    CF_HIP(c, cfattn::launch_prologue_bwd(d, to_prologue(pr), dq, dk, q_pre, k_pre, q_rstd, k_rstd, dq_pre, dk_pre,
+                                          dq_norm, dk_norm, partial, pick_stream(c, stream)),
+           "prologue backward launch");
+    return CFATTN_OK;
+}
+
+int cfattn_prologue_bwd(cfattn_ctx* c, cfattn_shape s, size_t batch, const cfattn_prologue* pr, const float* dq,
+                        const float* dk, const float* q_pre, const float* k_pre, const float* q_rstd,
+                        const float* k_rstd, float* dq_pre, float* dk_pre, float* dq_norm, float* dk_norm,
+                        void* stream) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    return cfattn_prologue_bwd_locked(c, s, batch, pr, dq, dk, q_pre, k_pre, q_rstd, k_rstd, dq_pre, dk_pre, dq_norm, dk_norm, stream);
+}
+
+int cfattn_fused_fwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const cfattn_prologue* pr,
+                     const float* q_pre, const float* k_pre, const void* v, void* q_out, void* k_out, float* q_rstd,
+                     float* k_rstd, float* o, float* lse, void* stream) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    CF_TRY(cfattn_prologue_fwd_locked(c, s, batch, dtype, pr, q_pre, k_pre, q_out, k_out, q_rstd, k_rstd, stream));
+    return cfattn_fwd_locked(c, s, batch, dtype, q_out, k_out, v, o, lse, stream);
+}
+
+int cfattn_fused_bwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const cfattn_prologue* pr,
+                     const void* d_o, const float* q_pre, const float* k_pre, const void* q, const void* k,
+                     const void* v, const float* o, const float* lse, const float* q_rstd, const float* k_rstd,
+                     float* dq_pre, float* dk_pre, float* dv, float* dq_norm, float* dk_norm, void* stream) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    CF_TRY(check_dtype(c, dtype));
+    if (batch == 0 || s.seq == 0) return CFATTN_OK;
+    CF_TRY(check_shape(c, s));
+    CF_TRY(check_prologue(c, s, pr));
+    DeviceGuard dg(c->device);
+    int rc = CFATTN_OK;
+    const size_t nq = batch * s.seq * s.n_heads * s.head_dim, nk = batch * s.seq * s.n_kv * s.head_dim;
+    float* dq_rot = static_cast<float*>(slot(c, cfattn_ctx::DQROT, nq * 4, &rc));
+    if (!dq_rot) return rc;
+    float* dk_rot = static_cast<float*>(slot(c, cfattn_ctx::DKROT, nk * 4, &rc));
+    if (!dk_rot) return rc;
+    hipStream_t st = pick_stream(c, stream);
+    // Layer::backward starts from zeroed dq/dk (layer.rs:183-185).
+    CF_HIP(c, cfattn::launch_fill_zero(dq_rot, nq, st), "zero dq");
+    CF_HIP(c, cfattn::launch_fill_zero(dk_rot, nk, st), "zero dk");
+    CF_TRY(cfattn_bwd_locked(c, s, batch, dtype, d_o, q, k, v, o, lse, dq_rot, dk_rot, dv, stream));
+    return cfattn_prologue_bwd_locked(c, s, batch, pr, dq_rot, dk_rot, q_pre, k_pre, q_rstd, k_rstd, dq_pre, dk_pre,
+                                      dq_norm, dk_norm, stream);
+}
+
+double cfattn_llama3_scale(const cfattn_llama3_scaling* sc, double inv_freq) {
+    if (!sc) return inv_freq;
+    const double pi = 3.14159265358979323846;
+    const double wavelen = 2.0 * pi / inv_freq;
+    const double low_wavelen = sc->original_max_position / sc->low_freq_factor;
+    const double high_wavelen = sc->original_max_position / sc->high_freq_factor;
+    if (wavelen < high_wavelen) return inv_freq;
+    if (wavelen > low_wavelen) return inv_freq / sc->factor;
+    const double smooth =
+        (sc->original_max_position / wavelen - sc->low_freq_factor) / (sc->high_freq_factor - sc->low_freq_factor);
+    return (1.0 - smooth) * inv_freq / sc->factor + smooth * inv_freq;
+}
+
+int cfattn_rope_table(size_t head_dim, size_t max_pos, double theta, const cfattn_llama3_scaling* scaling,
+                      float* cos_out, float* sin_out) {
+    if (head_dim % 2 != 0) return CFATTN_ERR_SHAPE;  // "head_dim must be even" (rope.rs:47)
+    if ((!cos_out || !sin_out) && max_pos * head_dim > 0) return CFATTN_ERR_ARG;
+    const size_t half = head_dim / 2;
+    for (size_t pos = 0; pos < max_pos; pos++) {
+        for (size_t i = 0; i < half; i++) {
+            double inv_freq = std::pow(theta, -(2.0 * (double)i) / (double)head_dim);
+            if (scaling) inv_freq = cfattn_llama3_scale(scaling, inv_freq);
+            const double angle = (double)pos * inv_freq;
+            cos_out[pos * half + i] = (float)std::cos(angle);
+            sin_out[pos * half + i] = (float)std::sin(angle);
+        }
+    }
+    return CFATTN_OK;
+}
+
+int cfattn_f32_to_bf16(cfattn_ctx* c, const float* src, uint16_t* dst, size_t n, void* stream) {
+    if (!c) return CFATTN_ERR_ARG;
+    if (n == 0) return CFATTN_OK;
+    if (!src || !dst) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    DeviceGuard dg(c->device);
+    CF_HIP(c, cfattn::launch_f32_to_bf16(src, dst, n, pick_stream(c, stream)), "f32_to_bf16 launch");
+    return CFATTN_OK;
+}
+
+double cfattn_flops_fwd_bwd(cfattn_shape s, size_t batch) {
+    return 7.0 * (double)batch * (double)s.n_heads * (double)s.head_dim * (double)s.seq * ((double)s.seq + 1.0);
+}
+
+const char* cfattn_version(void) { return "cfattn 0.1.0 (gfx950)"; }
+
+}  // extern "C"

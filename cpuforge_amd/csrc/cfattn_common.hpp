@@ -1,0 +1,235 @@
+// Shared device code for the cfattn gfx950 kernels: types, MFMA wrappers,
+// bf16 rounding, workgroup-id remapping and LDS tile staging.
+//
+// MFMA lane layouts used throughout (checked on gfx950 for all four builtins):
+//   v_mfma_f32_32x32x16_bf16: lane l holds A[l%32][8*(l/32)+0..7] and
+//       B[8*(l/32)+0..7][l%32]; the 16 accumulators of lane l are
+//       C[8*(r/4) + 4*(l/32) + r%4][l%32], r = 0..15.
+//   v_mfma_f32_32x32x2f32:    lane l holds A[l%32][l/32], B[l/32][l%32];
+//       same accumulator layout.
+// The k-index inside one MFMA may be permuted freely as long as A and B use
+// the same permutation; the kernels use that to feed accumulator registers
+// of one MFMA straight into the next one as operands.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cfattn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint16_t bf16_bits;  // bf16 values live in memory as raw 16-bit patterns
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ----------------------------------------------------------------- modes
+// Mode<float>: fp32 parity mode (v_mfma_f32_32x32x2f32, one element per lane
+// per MFMA).  Mode<bf16_bits>: bf16 inputs, fp32 accumulation
+// (v_mfma_f32_32x32x16_bf16, eight elements per lane per MFMA).
+template <typename T>
+struct Mode;
+
+template <>
+struct Mode<float> {
+    static constexpr int EPL = 1;  // operand elements per lane per MFMA
+    static constexpr int CH = 4;   // elements per 16-byte chunk
+    using frag = float;
+};
+
+template <>
+struct Mode<bf16_bits> {
+    static constexpr int EPL = 8;
+    static constexpr int CH = 8;
+    using frag = bf16x8;
+};
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(float a, float b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+    f32x16 z;
+#pragma unroll
+    for (int i = 0; i < 16; i++) z[i] = 0.0f;
+    return z;
+}
+
+// Round-to-nearest-even f32 -> bf16 bit pattern (finite inputs and inf; NaN
+// is kept a quiet NaN).
+__host__ __device__ __forceinline__ bf16_bits f32_to_bf16(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_bits)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16_bits)(u >> 16);
+}
+__host__ __device__ __forceinline__ float bf16_to_f32(bf16_bits b) {
+    return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T x);
+template <>
+__device__ __forceinline__ float to_f32<float>(float x) {
+    return x;
+}
+template <>
+__device__ __forceinline__ float to_f32<bf16_bits>(bf16_bits x) {
+    return bf16_to_f32(x);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) {
+    return x;
+}
+template <>
+__device__ __forceinline__ bf16_bits from_f32<bf16_bits>(float x) {
+    return f32_to_bf16(x);
+}
+
+// Eight consecutive bf16 from 16-byte-aligned memory as an MFMA operand.
+__device__ __forceinline__ bf16x8 load_bf16x8(const bf16_bits* p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+}
+// Two groups of four consecutive bf16 (each 8-byte aligned) as one operand.
+__device__ __forceinline__ bf16x8 load_bf16x4x2(const bf16_bits* p0, const bf16_bits* p1) {
+    uint2 a = *reinterpret_cast<const uint2*>(p0);
+    uint2 b = *reinterpret_cast<const uint2*>(p1);
+    uint4 v = make_uint4(a.x, a.y, b.x, b.y);
+    return __builtin_bit_cast(bf16x8, v);
+}
+// Eight f32 accumulator values rounded to bf16 as one operand.
+__device__ __forceinline__ bf16x8 pack_bf16x8(const float* v) {
+    uint4 u;
+    u.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+    u.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+    u.z = (uint32_t)f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
+    u.w = (uint32_t)f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+    return __builtin_bit_cast(bf16x8, u);
+}
+
+// --------------------------------------------------------- XCD remapping
+// MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs,
+// each with its own L2.  Remap so that XCD x runs one contiguous range of
+// logical ids; the kernels order logical ids so that a range shares K/V
+// heads, which then stay resident in that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int hw_id, int n, int enable) {
+    if (!enable || n < 8) return hw_id;
+    const int q = n / 8, r = n % 8;
+    const int xcd = hw_id % 8, local = hw_id / 8;
+    const int start = xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q;
+    return start + local;
+}
+
+// ------------------------------------------------------------ LDS staging
+template <typename T>
+union Chunk {
+    uint4 u;
+    T e[16 / sizeof(T)];
+};
+
+// Copy rows [0, ROWS) x columns [0, DP) of a strided global tile into LDS,
+// row-major with leading dimension LD (elements).  Rows at or past `nrows`
+// and columns at or past `hd` are written as zero, so padded rows and
+// head-dim padding contribute nothing to any contraction.
+template <typename T, int ROWS, int DP, int LD>
+__device__ __forceinline__ void stage_rows(T* __restrict__ s, const T* __restrict__ g, long row_stride, int nrows,
+                                           int hd, bool vec_ok, int nthreads) {
+    constexpr int CH = Mode<T>::CH;
+    constexpr int CPR = DP / CH;  // 16-byte chunks per row
+    constexpr int TOTAL = ROWS * CPR;
+    for (int c = threadIdx.x; c < TOTAL; c += nthreads) {
+        const int row = c / CPR;
+        const int col = (c % CPR) * CH;
+        Chunk<T> v;
+        if (row < nrows && vec_ok && col + CH <= hd) {
+            v.u = *reinterpret_cast<const uint4*>(g + (long)row * row_stride + col);
+        } else {
+#pragma unroll
+            for (int i = 0; i < CH; i++)
+                v.e[i] = (row < nrows && col + i < hd) ? g[(long)row * row_stride + col + i] : T(0);
+        }
+        *reinterpret_cast<uint4*>(s + row * LD + col) = v.u;
+    }
+}
+
+// The same tile transposed: LDS holds element (row, d) at s[d * LD + row].
+// Each thread moves four rows x one 16-byte column chunk and writes the four
+// rows of each d with one store.
+template <typename T, int ROWS, int DP, int LD>
+__device__ __forceinline__ void stage_rows_t(T* __restrict__ s, const T* __restrict__ g, long row_stride, int nrows,
+                                             int hd, bool vec_ok, int nthreads) {
+    constexpr int CH = Mode<T>::CH;
+    constexpr int RG = ROWS / 4;  // groups of four rows
+    constexpr int TOTAL = RG * (DP / CH);
+    static_assert(ROWS % 4 == 0, "row tile must be a multiple of 4");
+    for (int c = threadIdx.x; c < TOTAL; c += nthreads) {
+        const int r0 = (c % RG) * 4;
+        const int col = (c / RG) * CH;
+        Chunk<T> v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = r0 + j;
+            if (row < nrows && vec_ok && col + CH <= hd) {
+                v[j].u = *reinterpret_cast<const uint4*>(g + (long)row * row_stride + col);
+            } else {
+#pragma unroll
+                for (int i = 0; i < CH; i++)
+                    v[j].e[i] = (row < nrows && col + i < hd) ? g[(long)row * row_stride + col + i] : T(0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            if constexpr (sizeof(T) == 2) {
+                uint2 w;
+                w.x = (uint32_t)v[0].e[i] | ((uint32_t)v[1].e[i] << 16);
+                w.y = (uint32_t)v[2].e[i] | ((uint32_t)v[3].e[i] << 16);
+                *reinterpret_cast<uint2*>(s + (col + i) * LD + r0) = w;
+            } else {
+                float4 w = make_float4(v[0].e[i], v[1].e[i], v[2].e[i], v[3].e[i]);
+                *reinterpret_cast<float4*>(s + (col + i) * LD + r0) = w;
+            }
+        }
+    }
+}
+
+// Load one lane's operand row: elements [d0, d0 + N) of a global row into N
+// registers (zero past hd or for an invalid row).
+template <typename T, int N>
+__device__ __forceinline__ void load_row_frag(T (&dst)[N], const T* __restrict__ row, int d0, int hd, bool valid,
+                                              bool vec_ok) {
+    constexpr int CH = Mode<T>::CH;
+    static_assert(N % CH == 0, "fragment must be whole chunks");
+#pragma unroll
+    for (int c = 0; c < N / CH; c++) {
+        const int d = d0 + c * CH;
+        Chunk<T> v;
+        if (valid && vec_ok && d + CH <= hd) {
+            v.u = *reinterpret_cast<const uint4*>(row + d);
+        } else {
+#pragma unroll
+            for (int i = 0; i < CH; i++) v.e[i] = (valid && d + i < hd) ? row[d + i] : T(0);
+        }
+#pragma unroll
+        for (int i = 0; i < CH; i++) dst[c * CH + i] = v.e[i];
+    }
+}
+
+// Leading dimensions with padding chosen so that the MFMA operand reads
+// (16-byte row reads for row-major tiles, 8/16-byte reads of four
+// consecutive rows for transposed tiles) spread over all LDS banks.
+template <typename T, int DP>
+struct RowLD {
+    static constexpr int value = DP + 16 / (int)sizeof(T);
+};
+template <typename T, int ROWS>
+struct TLD {
+    static constexpr int value = ROWS + (sizeof(T) == 2 ? 4 : 4);
+};
+
+}  // namespace cfattn

@@ -1,0 +1,67 @@
+// Internal launch interface between the C ABI (cfattn_capi.cpp) and the
+// gfx950 kernel files.  Plain structs of device pointers and sizes; all
+// tensors are row-major and contiguous:
+//   q, o, d_o, dq : [batch][seq][n_heads][head_dim]
+//   k, v, dk, dv  : [batch][seq][n_kv][head_dim]
+//   lse, delta    : [batch][n_heads][seq]
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace cfattn {
+
+enum Dtype { kF32 = 0, kBF16 = 1 };
+
+struct Dims {
+    int batch, seq, nh, nkv, hd;
+};
+
+// Tuning knobs of one launch; defaults are chosen by the launchers.
+struct Tuning {
+    int xcd_remap = 1;  // XCD-aware workgroup ordering
+    int fwd_heads_per_wg = 0;  // 0 = automatic
+    int fwd_tblocks_per_wg = 0;
+    int bwd_kv_waves = 0;
+};
+
+hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k, const void* v, float* o,
+                           float* lse, hipStream_t st, const Tuning& tu);
+
+// Backward.  `delta` is caller-provided scratch of batch*n_heads*seq floats.
+// dq, dk, dv are accumulated (+=).
+hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
+                           const float* o, const float* lse, float* delta, float* dq, float* dk, float* dv,
+                           hipStream_t st, const Tuning& tu);
+
+// Attention prologue: optional per-head RMSNorm of q_pre/k_pre (when qw/kw
+// are non-null) followed by rotate-half RoPE at positions pos0+t, written in
+// the compute dtype.  rstd outputs are written only with the norm.
+struct Prologue {
+    const float* cos;  // [max_pos][head_dim/2]
+    const float* sin;
+    int max_pos;
+    int pos0;
+    const float* qw;  // [head_dim] or null
+    const float* kw;
+    float eps;
+};
+hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, const float* q_pre, const float* k_pre,
+                               void* q_out, void* k_out, float* q_rstd, float* k_rstd, hipStream_t st);
+
+// Prologue backward: inverse RoPE of dq/dk, then (with the norm) RMSNorm
+// backward.  dq_pre/dk_pre and dqw/dkw are accumulated.  `partial` is
+// scratch of prologue_bwd_scratch_floats(d) floats (unused without norm).
+size_t prologue_bwd_scratch_floats(const Dims& d);
+hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* dq, const float* dk,
+                               const float* q_pre, const float* k_pre, const float* q_rstd, const float* k_rstd,
+                               float* dq_pre, float* dk_pre, float* dqw, float* dkw, float* partial, hipStream_t st);
+
+// Elementwise helpers.
+hipError_t launch_f32_to_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t st);
+hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t st);
+
+// Largest head_dim the kernels take.
+constexpr int kMaxHeadDim = 256;
+
+}  // namespace cfattn

@@ -1,0 +1,52 @@
+/* cpuforge attention oracle -- TEST INFRASTRUCTURE ONLY (see cforge_oracle.c). */
+#ifndef CFORGE_ORACLE_H
+#define CFORGE_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+uint64_t orc_rng_seed(uint64_t seed);
+uint64_t orc_rng_next_u64(uint64_t* state);
+float orc_rng_uniform(uint64_t* state);
+float orc_rng_normal(uint64_t* state);
+void orc_fill_normal(uint64_t seed, float* out, size_t n, float std);
+
+void orc_gemm_strided(const float* a, long a_rs, long a_cs, const float* b, long b_rs, long b_cs, float* c,
+                      long c_rs, long c_cs, size_t m, size_t k, size_t n, int acc);
+int orc_gemm_threads(void);
+
+int orc_attention_forward_blocked(const float* q, const float* k, const float* v, float* o, float* lse,
+                                  size_t seq, size_t nh, size_t nkv, size_t hd, size_t q_block);
+int orc_attention_forward_heads(const float* q, const float* k, const float* v, float* o, float* lse,
+                                size_t seq, size_t nh, size_t nkv, size_t hd, size_t q_block,
+                                size_t h_begin, size_t h_end);
+int orc_attention_backward_blocked(const float* d_o, const float* q, const float* k, const float* v,
+                                   const float* o, const float* lse, float* dq, float* dk, float* dv,
+                                   size_t seq, size_t nh, size_t nkv, size_t hd, size_t q_block);
+int orc_attention_backward_heads(const float* d_o, const float* q, const float* k, const float* v,
+                                 const float* o, const float* lse, float* dq, float* dk, float* dv,
+                                 size_t seq, size_t nh, size_t nkv, size_t hd, size_t q_block,
+                                 size_t h_begin, size_t h_end);
+void orc_attn_ref_f64(const double* q, const double* k, const double* v, double* o, double* lse,
+                      size_t seq, size_t nh, size_t nkv, size_t hd, const uint8_t* row_mask);
+void orc_attn_bwd_ref_f64(const double* d_o, const double* q, const double* k, const double* v,
+                          double* dq, double* dk, double* dv, size_t seq, size_t nh, size_t nkv, size_t hd,
+                          size_t h_begin, size_t h_end);
+
+double orc_llama3_scale(double inv_freq, double factor, double low_freq_factor, double high_freq_factor,
+                        double original_max_position);
+int orc_rope_table(size_t head_dim, size_t max_pos, double theta, const double* scaling, float* cos_out,
+                   float* sin_out);
+int orc_rope_apply(const float* cos_t, const float* sin_t, size_t max_pos, size_t head_dim, float* x, size_t seq,
+                   size_t heads, size_t pos0, int inverse);
+void orc_rmsnorm_forward(const float* x, const float* w, float* y, float* rstd, size_t rows, size_t dim, float eps);
+void orc_rmsnorm_backward(const float* dy, const float* x, const float* w, const float* rstd, float* dx, float* dw,
+                          size_t rows, size_t dim);
+uint16_t orc_f32_to_bf16(float f);
+void orc_round_bf16(const float* src, float* dst, size_t n);
+double orc_grad_close_metric(const float* a, const double* n, size_t len, size_t* worst_i);
+#ifdef __cplusplus
+}
+#endif
+#endif

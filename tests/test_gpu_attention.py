@@ -1,0 +1,212 @@
+"""GPU parity of the HIP attention kernels against the oracle.
+
+The first four tests restate the reference's own attention tests
+(crates/core/src/ops/attention.rs:324-393) with the GPU op in place of the
+Rust one; the rest run the benchmark configurations through the batched
+device entry points and compare with the oracle's f32 restatement of the
+reference algorithm (fp32 mode: max abs error <= 1e-4 on O, lse, dQ, dK, dV;
+bf16 mode: max|a-r|/max|r| <= 2e-2, oracle fed the same bf16-rounded inputs).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.cases import CASES, CONFIGS, case, max_abs, rel_err, rope_tables, seq_inputs
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-4  # fp32 parity bar (max abs)
+BF16_TOL = 2e-2  # bf16 parity bar (max relative)
+
+
+@pytest.fixture(scope="module")
+def cf():
+    import cpuforge_amd
+    ctx = cpuforge_amd.Context(0)
+    yield cpuforge_amd, ctx
+    ctx.close()
+
+
+def _fwd(cf, q, k, v, s, qb=128):
+    mod, ctx = cf
+    o = np.zeros(s.seq * s.n_heads * s.head_dim, np.float32)
+    lse = np.zeros(s.n_heads * s.seq, np.float32)
+    mod.attention_forward_blocked(q, k, v, o, lse, s, qb, ctx)
+    return o, lse
+
+
+def test_forward_matches_f64_reference(cf):
+    mod, _ = cf
+    for i, (seq, h, kv, hd, qb) in enumerate(CASES):
+        print(f"case {i}: seq={seq} h={h} kv={kv} hd={hd} qb={qb}", flush=True)
+        q, k, v = case(seq, h, kv, hd, 10 + i)
+        s = mod.AttnShape(seq, h, kv, hd)
+        o, lse = _fwd(cf, q, k, v, s, qb)
+        want, want_lse = O.attn_ref_f64(q, k, v, seq, h, kv, hd)
+        err, _ = O.grad_close_metric(o, want)
+        assert err <= 1e-4, f"attn fwd case {i}: {err}"
+        assert O.grad_close_metric(lse, want_lse)[0] <= 1e-4
+        # and against the f32 restatement of attention_forward_blocked
+        o_ref = np.zeros_like(o)
+        l_ref = np.zeros_like(lse)
+        O.attention_forward_blocked(q, k, v, o_ref, l_ref, seq, h, kv, hd, qb)
+        assert max_abs(o, o_ref) <= F32_TOL and max_abs(lse, l_ref) <= F32_TOL
+
+
+def test_block_size_does_not_change_result(cf):
+    mod, _ = cf
+    q, k, v = case(37, 4, 2, 8, 30)
+    s = mod.AttnShape(37, 4, 2, 8)
+    runs = [_fwd(cf, q, k, v, s, qb) for qb in (1, 16, 1000)]
+    for o, lse in runs[1:]:
+        assert np.abs(o - runs[0][0]).max() < 1e-5
+        assert np.abs(lse - runs[0][1]).max() < 1e-5
+
+
+def test_first_token_attends_only_to_itself(cf):
+    mod, _ = cf
+    q, k, v = case(5, 2, 1, 4, 40)
+    o, _ = _fwd(cf, q, k, v, mod.AttnShape(5, 2, 1, 4))
+    for h in range(2):
+        assert np.abs(o[h * 4:(h + 1) * 4] - v[0:4]).max() < 1e-6
+
+
+def test_backward_matches_f64_gradients_and_finite_differences(cf):
+    mod, ctx = cf
+    for i, (seq, h, kv, hd, qb) in enumerate(CASES):
+        print(f"case {i}", flush=True)
+        q, k, v = case(seq, h, kv, hd, 50 + i)
+        g = O.rand(seq * h * hd, 70 + i, 1.0)
+        s = mod.AttnShape(seq, h, kv, hd)
+        o, lse = _fwd(cf, q, k, v, s, qb)
+        dq = np.zeros_like(q)
+        dk = np.zeros_like(k)
+        dv = np.zeros_like(v)
+        mod.attention_backward_blocked(g, q, k, v, o, lse, dq, dk, dv, s, qb, ctx)
+        wq, wk, wv = O.attn_bwd_ref_f64(g, q, k, v, seq, h, kv, hd)
+        for name, a, w in (("dq", dq, wq), ("dk", dk, wk), ("dv", dv, wv)):
+            assert max_abs(a, w) <= F32_TOL, f"{name} case {i}: {max_abs(a, w)}"
+        # finite differences of the f64 reference forward (attention.rs:378-392)
+        q64, k64, v64, g64 = (x.astype(np.float64) for x in (q, k, v, g))
+
+        def loss(qq, kk, vv):
+            return float(np.dot(O.attn_ref_f64(qq, kk, vv, seq, h, kv, hd)[0], g64))
+
+        for name, a, x, which in (("dq", dq, q64, 0), ("dk", dk, k64, 1), ("dv", dv, v64, 2)):
+            num = np.zeros_like(x)
+            for j in range(x.size):
+                xp = x.copy()
+                xm = x.copy()
+                xp[j] += 1e-6
+                xm[j] -= 1e-6
+                args_p = [q64, k64, v64]
+                args_m = [q64, k64, v64]
+                args_p[which] = xp
+                args_m[which] = xm
+                num[j] = (loss(*args_p) - loss(*args_m)) / 2e-6
+            assert O.grad_close_metric(a, num)[0] <= 1e-3, f"attn {name} case {i} vs finite differences"
+
+
+def test_backward_accumulates(cf):
+    mod, ctx = cf
+    q, k, v = case(40, 6, 2, 16, 5)
+    g = O.rand(q.size, 6, 1.0)
+    s = mod.AttnShape(40, 6, 2, 16)
+    o, lse = _fwd(cf, q, k, v, s)
+    grads = [np.zeros_like(x) for x in (q, k, v)]
+    mod.attention_backward(g, q, k, v, o, lse, *grads, s, ctx)
+    once = [x.copy() for x in grads]
+    mod.attention_backward(g, q, k, v, o, lse, *grads, s, ctx)
+    for a, b in zip(grads, once):
+        assert np.abs(a - 2 * b).max() <= 1e-6 * (1 + np.abs(b).max())
+
+
+def _prologue_cpu(cfg, qp, kp):
+    cos, sin = rope_tables(cfg)
+    q, k, _, _ = O.layer_prologue_forward(qp, kp, cfg.seq, cfg.n_heads, cfg.n_kv, cfg.head_dim, cos, sin, cfg.seq)
+    return q, k
+
+
+def test_c1_f32_parity(cf):
+    """C1: SmolLM-135M layer, f32, RoPE theta 1e4; the host-slice drop-in."""
+    mod, ctx = cf
+    cfg = CONFIGS["C1"]
+    qp, kp, v, g = seq_inputs(cfg, 0)
+    q, k = _prologue_cpu(cfg, qp, kp)
+    s = mod.AttnShape(cfg.seq, cfg.n_heads, cfg.n_kv, cfg.head_dim)
+    o, lse = _fwd(cf, q, k, v, s)
+    dq, dk, dv = (np.zeros_like(x) for x in (q, k, v))
+    mod.attention_backward(g, q, k, v, o, lse, dq, dk, dv, s, ctx)
+    ro, rl = np.zeros_like(o), np.zeros_like(lse)
+    O.attention_forward_blocked(q, k, v, ro, rl, *s.__dict__.values(), 128)
+    rq, rk, rv = (np.zeros_like(x) for x in (q, k, v))
+    O.attention_backward_blocked(g, q, k, v, ro, rl, rq, rk, rv, *s.__dict__.values(), 128)
+    for name, a, r in (("o", o, ro), ("lse", lse, rl), ("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        e = max_abs(a, r)
+        print(f"C1 f32 {name}: max abs {e:.3e}", flush=True)
+        assert e <= F32_TOL, name
+
+
+def _device_check(cf, cfg, mode, seqs, head_groups):
+    """Run the whole batch on the GPU; check the listed sequences and KV
+    groups against the oracle's f32 restatement."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    B, S, Hq, Hk, Dh = cfg.batch, cfg.seq, cfg.n_heads, cfg.n_kv, cfg.head_dim
+    grp = cfg.group
+    cos, sin = rope_tables(cfg)
+    host = []
+    for b in range(B):
+        qp, kp, v, g = seq_inputs(cfg, b)
+        q, k, _, _ = O.layer_prologue_forward(qp, kp, S, Hq, Hk, Dh, cos, sin, S)
+        if mode == "bf16":
+            q, k, v, g = (O.round_bf16(x) for x in (q, k, v, g))
+        host.append((q, k, v, g))
+    tdt = torch.bfloat16 if mode == "bf16" else torch.float32
+
+    def dev(i, heads):
+        return torch.from_numpy(np.stack([h[i] for h in host])).view(B, S, heads, Dh).to("cuda").to(tdt)
+
+    q, k, v, g = dev(0, Hq), dev(1, Hk), dev(2, Hk), dev(3, Hq)
+    o, lse = D.fwd(q, k, v, ctx=ctx)
+    dq, dk, dv = D.bwd(g, q, k, v, o, lse, ctx=ctx)
+    torch.cuda.synchronize()
+    o, lse, dq, dk, dv = (x.cpu().numpy() for x in (o, lse, dq, dk, dv))
+    worst = {}
+    for b in seqs:
+        hq, hk, hv, hg = host[b]
+        for grp_i in head_groups:
+            h0, h1 = grp_i * grp, (grp_i + 1) * grp
+            ro = np.zeros(S * Hq * Dh, np.float32)
+            rl = np.zeros(Hq * S, np.float32)
+            O.attention_forward_blocked(hq, hk, hv, ro, rl, S, Hq, Hk, Dh, 128, heads=(h0, h1))
+            rq = np.zeros_like(ro)
+            rk = np.zeros(S * Hk * Dh, np.float32)
+            rv = np.zeros_like(rk)
+            O.attention_backward_blocked(hg, hq, hk, hv, ro, rl, rq, rk, rv, S, Hq, Hk, Dh, 128, heads=(h0, h1))
+            sel_q = lambda x: x.reshape(S, Hq, Dh)[:, h0:h1]  # noqa: E731
+            sel_k = lambda x: x.reshape(S, Hk, Dh)[:, grp_i]  # noqa: E731
+            pairs = {
+                "o": (sel_q(o[b]), sel_q(ro)),
+                "lse": (lse[b][h0:h1], rl.reshape(Hq, S)[h0:h1]),
+                "dq": (sel_q(dq[b]), sel_q(rq)),
+                "dk": (sel_k(dk[b]), sel_k(rk)),
+                "dv": (sel_k(dv[b]), sel_k(rv)),
+            }
+            for name, (a, r) in pairs.items():
+                e = max_abs(a, r) if mode == "f32" else rel_err(a, r)
+                worst[name] = max(worst.get(name, 0.0), e)
+    print(f"{cfg.name} {mode}: " + ", ".join(f"{n} {e:.3e}" for n, e in worst.items()), flush=True)
+    tol = F32_TOL if mode == "f32" else BF16_TOL
+    for name, e in worst.items():
+        assert e <= tol, f"{cfg.name} {mode} {name}: {e}"
+
+
+@pytest.mark.parametrize("mode", ["f32", "bf16"])
+def test_c2_parity(cf, mode):
+    _device_check(cf, CONFIGS["C2"], mode, seqs=(0, 7), head_groups=(0, 2))
+
+
+def test_c5_bf16_parity(cf):
+    _device_check(cf, CONFIGS["C5"], "bf16", seqs=(0,), head_groups=(0, 7))
