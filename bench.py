@@ -1,0 +1,230 @@
+"""Benchmark of the causal GQA attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C5] [--mode bf16]
+
+One step is one forward + backward of cpuforge's attention op
+(crates/core/src/ops/attention.rs:42-262) over one batch of the configuration:
+cfattn_fwd (O, lse overwritten) then cfattn_bwd (dQ, dK, dV accumulated), on
+device-resident inputs.  The default workload is BASELINE.json's Llama-3-8B
+layer shape (batch 1, seq 8192, 32 query / 8 KV heads, head_dim 128, bf16
+inputs with fp32 accumulation), the configuration the target figure is
+quoted on.  Q and K are produced once, before timing, by the library's RoPE
+prologue (theta 500000) from synthetic N(0,1) data.
+
+Printed: one JSON line with the whole-step throughput (algorithmic TFLOP/s,
+7*B*Hq*D*S*(S+1) per step), a `roofline` object for the kernel that takes the
+most time (its algorithmic FLOPs per launch / its mean launch time, measured
+with hipEvents on its stream over the timed steps) and a `cpu_baseline`
+object: the oracle's restatement of the reference CPU algorithm timed on a
+bounded sample of the same workload on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+# MI355X published dense peaks (TFLOP/s) and HBM bandwidth (GB/s).
+PEAK_TFLOPS = {"bf16": 2516.6, "f32": 157.3}
+PEAK_HBM_GBS = 8000.0
+
+# name: (batch, seq, n_heads, n_kv, head_dim, theta, llama3 scaling, qk norm)
+CONFIGS = {
+    "C1": (1, 512, 9, 3, 64, 1e4, None, False),
+    "C2": (8, 2048, 9, 3, 64, 1e4, None, False),
+    "C3": (4, 4096, 32, 8, 64, 5e5, (32.0, 1.0, 4.0, 8192.0), False),
+    "C4": (4, 4096, 16, 8, 128, 1e6, None, True),
+    "C5": (1, 8192, 32, 8, 128, 5e5, None, False),
+}
+WORKLOAD = {
+    "C1": "SmolLM-135M attention layer (B1 S512 9q/3kv D64)",
+    "C2": "SmolLM-135M attention, training batch (B8 S2048 9q/3kv D64)",
+    "C3": "Llama-3.2-1B attention layer (B4 S4096 32q/8kv D64, llama3 rope)",
+    "C4": "Qwen3-0.6B attention layer (B4 S4096 16q/8kv D128, q/k rmsnorm)",
+    "C5": "Llama-3-8B attention layer (B1 S8192 32q/8kv D128)",
+}
+
+# Contractions each kernel performs that the algorithmic count includes
+# (units of B*Hq*D*S*(S+1) FLOPs): forward QK^T and PV; dK/dV kernel the
+# recomputed QK^T, dP = dO V^T, dV and dK; dQ kernel dQ only (it also
+# recomputes QK^T and dP, which the algorithmic count does not credit).
+ALGO_UNITS = {"attn_fwd": 2.0, "attn_bwd_dkdv": 4.0, "attn_bwd_dq": 1.0}
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C5", choices=sorted(CONFIGS))
+    ap.add_argument("--mode", default=None, choices=["bf16", "f32"], help="default: bf16 (f32 for C1)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--cpu-heads", type=int, default=16, help="query heads of sequence 0 in the CPU sample")
+    ap.add_argument("--traffic-file", default=None,
+                    help="rocprofv3 traffic summary to read `traffic` from (default: profiles/ match)")
+    return ap.parse_args()
+
+
+def cpu_baseline(cfg_name, mode, heads):
+    """The oracle (a C restatement of attention_forward_blocked /
+    attention_backward_blocked with an OpenMP GEMM) timed on query heads
+    [0, heads) of one sequence of the workload.  Runs on the host only."""
+    import numpy as np
+
+    from oracle import oracle as O
+    B, S, Hq, Hk, D = CONFIGS[cfg_name][:5]
+    heads = max(Hq // Hk, min(heads, Hq))
+    heads -= heads % (Hq // Hk)  # whole GQA groups
+    q = O.rand(S * Hq * D, 1, 1.0)
+    k = O.rand(S * Hk * D, 2, 1.0)
+    v = O.rand(S * Hk * D, 3, 1.0)
+    g = O.rand(S * Hq * D, 4, 1.0)
+    if mode == "bf16":
+        q, k, v, g = (O.round_bf16(x) for x in (q, k, v, g))
+    o = np.zeros_like(q)
+    lse = np.zeros(Hq * S, np.float32)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    t0 = time.perf_counter()
+    O.attention_forward_blocked(q, k, v, o, lse, S, Hq, Hk, D, 128, heads=(0, heads))
+    O.attention_backward_blocked(g, q, k, v, o, lse, dq, dk, dv, S, Hq, Hk, D, 128, heads=(0, heads))
+    dt = time.perf_counter() - t0
+    flops = 7.0 * heads * D * S * (S + 1)
+    return {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": O.gemm_threads(),
+        "kind": "port",
+        "sample": (f"oracle fwd+bwd (q_block 128, f32 arithmetic) over query heads 0..{heads} of one sequence "
+                   f"of {cfg_name} (S={S}, D={D}); {dt:.2f} s for {flops / 1e9:.1f} GFLOP"),
+    }
+
+
+def read_traffic(path, kernel, workload_key):
+    """HBM bytes per launch of `kernel` from a committed rocprofv3 summary:
+    a line `traffic_bytes <kernel> <workload_key> <bytes>`."""
+    if not path or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) == 4 and parts[0] == "traffic_bytes" and parts[1] == kernel and parts[2] == workload_key:
+                return float(parts[3])
+    return None
+
+
+def main():
+    a = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the attention op runs on a single MI355X here and this build has no "
+              f"multi-GPU path (asked for --gpus {a.gpus}, WORLD_SIZE={world}).", file=sys.stderr)
+        sys.exit(2)
+    mode = a.mode or ("f32" if a.config == "C1" else "bf16")
+    B, S, Hq, Hk, D, theta, scaling, qk_norm = CONFIGS[a.config]
+
+    import torch
+
+    import cpuforge_amd as cf
+    from cpuforge_amd import device as dev
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
+        sys.exit(1)
+    ctx = cf.Context(0)
+    torch.manual_seed(1234)
+    dt = torch.bfloat16 if mode == "bf16" else torch.float32
+    # Synthetic pre-RoPE q/k, v and upstream gradient, N(0,1).
+    q_pre = torch.randn(B, S, Hq, D, device="cuda", dtype=torch.float32)
+    k_pre = torch.randn(B, S, Hk, D, device="cuda", dtype=torch.float32)
+    v = torch.randn(B, S, Hk, D, device="cuda", dtype=torch.float32).to(dt)
+    d_o = torch.randn(B, S, Hq, D, device="cuda", dtype=torch.float32).to(dt)
+    sc = cf.Llama3Scaling(*scaling) if scaling else None
+    rope = cf.RopeCache(D, S, theta, sc)
+    qn = kn = None
+    if qk_norm:
+        qn = (1.0 + 0.02 * torch.randn(D, device="cuda")).float()
+        kn = (1.0 + 0.02 * torch.randn(D, device="cuda")).float()
+    pr = dev.DeviceRope(rope, "cuda", 0, qn, kn, 1e-6)
+    q, k, _, _ = dev.prologue_fwd(q_pre, k_pre, pr, dtype=dt, ctx=ctx)
+    del q_pre, k_pre
+    o = torch.empty(B, S, Hq, D, device="cuda", dtype=torch.float32)
+    lse = torch.empty(B, Hq, S, device="cuda", dtype=torch.float32)
+    dq = torch.zeros(B, S, Hq, D, device="cuda", dtype=torch.float32)
+    dk = torch.zeros(B, S, Hk, D, device="cuda", dtype=torch.float32)
+    dv = torch.zeros(B, S, Hk, D, device="cuda", dtype=torch.float32)
+
+    def step():
+        dev.fwd(q, k, v, o, lse, ctx=ctx)
+        dev.bwd(d_o, q, k, v, o, lse, dq, dk, dv, ctx=ctx)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    print(f"bench: {a.config} {mode} warmup done ({a.warmup} steps)", file=sys.stderr, flush=True)
+
+    ctx.profile_enable(True)
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(a.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    prof = ctx.profile_read()
+    ctx.profile_enable(False)
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = max(gpu_ms, wall * 1e3) / a.steps
+    flops = 7.0 * B * Hq * D * S * (S + 1)
+    tflops = flops / (ms_per_step * 1e-3) / 1e12
+    print(f"bench: timed {a.steps} steps, {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
+
+    kernels = {n: (t / c if c else 0.0, c) for n, (t, c) in prof.items() if c}
+    dom = max((n for n in kernels if n in ALGO_UNITS), key=lambda n: kernels[n][0] * kernels[n][1])
+    dom_ms = kernels[dom][0]
+    dom_flops = ALGO_UNITS[dom] * B * Hq * D * S * (S + 1)
+    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    peak = PEAK_TFLOPS[mode]
+    tpath = a.traffic_file or os.path.join(ROOT, "profiles", "traffic.txt")
+    traffic = read_traffic(tpath, dom, f"{a.config}-{mode}")
+
+    out = {
+        "metric": "attention fwd+bwd TFLOP/s + % MFMA peak at 1 MI355X; SmolLM-135M train tok/s",
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": mode,
+        "data": "synthetic (torch.randn N(0,1), RoPE prologue applied before timing)",
+        "config": {"workload": WORKLOAD[a.config], "config": a.config, "batch": B, "seq": S, "n_heads": Hq,
+                   "n_kv": Hk, "head_dim": D, "mode": mode, "causal": True},
+        "pct_peak": round(100.0 * tflops / peak, 2),
+        "kernels_ms": {n: round(m, 4) for n, (m, _) in kernels.items()},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 3), "peak": peak,
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic},
+    }
+    if not a.no_cpu:
+        print("bench: cpu baseline ...", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(a.config, mode, a.cpu_heads)
+    else:
+        out["cpu_baseline"] = None
+    ctx.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -79,6 +79,21 @@ class Context:
     def stream(self) -> int:
         return self._lib.cfattn_stream(self.handle) or 0
 
+    def profile_enable(self, on: bool = True) -> None:
+        """Bracket every kernel this context queues with hipEvents on its
+        stream (enabling again resets the totals)."""
+        _lib.check(self._lib.cfattn_profile_enable(self.handle, int(bool(on))), self.handle)
+
+    def profile_read(self) -> dict:
+        """{kernel name: (total ms, launches)} since profiling was enabled."""
+        out = {}
+        for kid in range(self._lib.cfattn_kernel_count()):
+            ms = C.c_double()
+            n = C.c_longlong()
+            _lib.check(self._lib.cfattn_profile_read(self.handle, kid, C.byref(ms), C.byref(n)), self.handle)
+            out[self._lib.cfattn_kernel_name(kid).decode()] = (ms.value, n.value)
+        return out
+
 
 def _dtype_code(mode) -> int:
     if mode in ("f32", "fp32", "float32", _lib.F32):

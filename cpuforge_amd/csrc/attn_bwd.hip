@@ -429,16 +429,24 @@ static int pick_hpw_b(int group, int cap) {
 }
 
 template <typename T, int DP>
-static hipError_t bwd_dp(const BwdParams& p, hipStream_t st, int kv_waves, int q_waves) {
+static hipError_t bwd_dp(const BwdParams& p, hipStream_t st, int kv_waves, int q_waves, KernelTimer* tm) {
     const long rows = (long)p.batch * p.seq * p.nh;
-    hipLaunchKernelGGL((attn_bwd_delta_kernel<T>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, p);
-    hipError_t e = hipGetLastError();
+    hipError_t e;
+    {
+        TimedLaunch tl(tm, kKernBwdDelta, st);
+        hipLaunchKernelGGL((attn_bwd_delta_kernel<T>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, p);
+        e = hipGetLastError();
+    }
     if (e != hipSuccess) return e;
     constexpr int BM = sizeof(T) == 2 ? 64 : 32;
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, DP, BM>), dim3(p.n_wg_kv), dim3(64 * kv_waves), 0, st, p);
-    e = hipGetLastError();
+    {
+        TimedLaunch tl(tm, kKernBwdDkdv, st);
+        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, DP, BM>), dim3(p.n_wg_kv), dim3(64 * kv_waves), 0, st, p);
+        e = hipGetLastError();
+    }
     if (e != hipSuccess) return e;
     constexpr int BN = sizeof(T) == 2 ? 64 : 32;
+    TimedLaunch tl(tm, kKernBwdDq, st);
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, DP, BN>), dim3(p.n_wg_q), dim3(64 * q_waves), 0, st, p);
     return hipGetLastError();
 }
@@ -490,17 +498,17 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
     const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;
     if (dt == kBF16) {
         switch (dp) {
-            case 32: return bwd_dp<bf16_bits, 32>(p, st, kv_waves, q_waves);
-            case 64: return bwd_dp<bf16_bits, 64>(p, st, kv_waves, q_waves);
-            case 128: return bwd_dp<bf16_bits, 128>(p, st, kv_waves, q_waves);
-            default: return bwd_dp<bf16_bits, 256>(p, st, kv_waves, q_waves);
+            case 32: return bwd_dp<bf16_bits, 32>(p, st, kv_waves, q_waves, tu.timer);
+            case 64: return bwd_dp<bf16_bits, 64>(p, st, kv_waves, q_waves, tu.timer);
+            case 128: return bwd_dp<bf16_bits, 128>(p, st, kv_waves, q_waves, tu.timer);
+            default: return bwd_dp<bf16_bits, 256>(p, st, kv_waves, q_waves, tu.timer);
         }
     }
     switch (dp) {
-        case 32: return bwd_dp<float, 32>(p, st, kv_waves, q_waves);
-        case 64: return bwd_dp<float, 64>(p, st, kv_waves, q_waves);
-        case 128: return bwd_dp<float, 128>(p, st, kv_waves, q_waves);
-        default: return bwd_dp<float, 256>(p, st, kv_waves, q_waves);
+        case 32: return bwd_dp<float, 32>(p, st, kv_waves, q_waves, tu.timer);
+        case 64: return bwd_dp<float, 64>(p, st, kv_waves, q_waves, tu.timer);
+        case 128: return bwd_dp<float, 128>(p, st, kv_waves, q_waves, tu.timer);
+        default: return bwd_dp<float, 256>(p, st, kv_waves, q_waves, tu.timer);
     }
 }
 

@@ -230,18 +230,19 @@ static int pick_hpw(int group, int cap) {
 }
 
 template <typename T, int DP, int BN>
-static hipError_t fwd_dispatch(const Dims& d, FwdParams p, hipStream_t st, int nwaves) {
+static hipError_t fwd_dispatch(const Dims& d, FwdParams p, hipStream_t st, int nwaves, KernelTimer* tm) {
+    TimedLaunch tl(tm, kKernFwd, st);
     hipLaunchKernelGGL((attn_fwd_kernel<T, DP, BN>), dim3(p.n_wg), dim3(64 * nwaves), 0, st, p);
     return hipGetLastError();
 }
 
 template <typename T, int DP>
-static hipError_t fwd_dp(const Dims& d, FwdParams p, hipStream_t st, int nwaves) {
+static hipError_t fwd_dp(const Dims& d, FwdParams p, hipStream_t st, int nwaves, KernelTimer* tm) {
     // fp32 tiles are twice the bytes: keep them to 32 keys.
     if constexpr (sizeof(T) == 2)
-        return fwd_dispatch<T, DP, 64>(d, p, st, nwaves);
+        return fwd_dispatch<T, DP, 64>(d, p, st, nwaves, tm);
     else
-        return fwd_dispatch<T, DP, 32>(d, p, st, nwaves);
+        return fwd_dispatch<T, DP, 32>(d, p, st, nwaves, tm);
 }
 
 hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k, const void* v, float* o,
@@ -279,17 +280,17 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
     const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;
     if (dt == kBF16) {
         switch (dp) {
-            case 32: return fwd_dp<bf16_bits, 32>(d, p, st, nwaves);
-            case 64: return fwd_dp<bf16_bits, 64>(d, p, st, nwaves);
-            case 128: return fwd_dp<bf16_bits, 128>(d, p, st, nwaves);
-            default: return fwd_dp<bf16_bits, 256>(d, p, st, nwaves);
+            case 32: return fwd_dp<bf16_bits, 32>(d, p, st, nwaves, tu.timer);
+            case 64: return fwd_dp<bf16_bits, 64>(d, p, st, nwaves, tu.timer);
+            case 128: return fwd_dp<bf16_bits, 128>(d, p, st, nwaves, tu.timer);
+            default: return fwd_dp<bf16_bits, 256>(d, p, st, nwaves, tu.timer);
         }
     }
     switch (dp) {
-        case 32: return fwd_dp<float, 32>(d, p, st, nwaves);
-        case 64: return fwd_dp<float, 64>(d, p, st, nwaves);
-        case 128: return fwd_dp<float, 128>(d, p, st, nwaves);
-        default: return fwd_dp<float, 256>(d, p, st, nwaves);
+        case 32: return fwd_dp<float, 32>(d, p, st, nwaves, tu.timer);
+        case 64: return fwd_dp<float, 64>(d, p, st, nwaves, tu.timer);
+        case 128: return fwd_dp<float, 128>(d, p, st, nwaves, tu.timer);
+        default: return fwd_dp<float, 256>(d, p, st, nwaves, tu.timer);
     }
 }
 

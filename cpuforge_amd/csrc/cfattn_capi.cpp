@@ -12,9 +12,89 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "cfattn.h"
 #include "cfattn_kernels.hpp"
+
+// Per-kernel timing for cfattn_profile_*: every launch a timed call queues is
+// bracketed by two hipEvents recorded on the launch's stream; the elapsed
+// times are summed when the caller reads them.
+struct EventTimer final : cfattn::KernelTimer {
+    struct Rec {
+        int kernel;
+        hipEvent_t a, b;
+    };
+    std::vector<hipEvent_t> pool;
+    std::vector<Rec> pending;
+    hipEvent_t open_ev = nullptr;
+    int open_kernel = -1;
+    double total_ms[cfattn::kNumKernels] = {};
+    long long launches[cfattn::kNumKernels] = {};
+    hipError_t err = hipSuccess;
+
+    hipEvent_t take() {
+        if (!pool.empty()) {
+            hipEvent_t e = pool.back();
+            pool.pop_back();
+            return e;
+        }
+        hipEvent_t e = nullptr;
+        hipError_t r = hipEventCreate(&e);
+        if (r != hipSuccess && err == hipSuccess) err = r;
+        return r == hipSuccess ? e : nullptr;
+    }
+    void begin(int kernel, hipStream_t st) override {
+        open_ev = take();
+        open_kernel = kernel;
+        if (open_ev) {
+            hipError_t r = hipEventRecord(open_ev, st);
+            if (r != hipSuccess && err == hipSuccess) err = r;
+        }
+    }
+    void end(int kernel, hipStream_t st) override {
+        hipEvent_t b = take();
+        if (!open_ev || !b || kernel != open_kernel) {
+            if (b) pool.push_back(b);
+            return;
+        }
+        hipError_t r = hipEventRecord(b, st);
+        if (r != hipSuccess && err == hipSuccess) err = r;
+        pending.push_back(Rec{kernel, open_ev, b});
+        open_ev = nullptr;
+    }
+    // Waits for every pending pair and folds it into the totals.
+    hipError_t collect() {
+        for (const Rec& r : pending) {
+            hipError_t e = hipEventSynchronize(r.b);
+            float ms = 0.0f;
+            if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.a, r.b);
+            if (e != hipSuccess && err == hipSuccess) err = e;
+            total_ms[r.kernel] += ms;
+            launches[r.kernel] += 1;
+            pool.push_back(r.a);
+            pool.push_back(r.b);
+        }
+        pending.clear();
+        hipError_t e = err;
+        err = hipSuccess;
+        return e;
+    }
+    void reset() {
+        for (int i = 0; i < cfattn::kNumKernels; i++) {
+            total_ms[i] = 0.0;
+            launches[i] = 0;
+        }
+    }
+    ~EventTimer() override {
+        for (const Rec& r : pending) {
+            (void)hipEventSynchronize(r.b);
+            pool.push_back(r.a);
+            pool.push_back(r.b);
+        }
+        for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+    }
+};
 
 struct cfattn_ctx {
     int device = 0;
@@ -25,6 +105,13 @@ struct cfattn_ctx {
     enum Slot { Q, K, V, O, LSE, DO_, DQ, DK, DV, QB, KB, VB, DOB, DELTA, PARTIAL, DQROT, DKROT, NSLOT };
     void* buf[NSLOT] = {};
     size_t cap[NSLOT] = {};
+    EventTimer* timer = nullptr;  // non-null while profiling is on
+
+    cfattn::Tuning tuning() const {
+        cfattn::Tuning t;
+        t.timer = timer;
+        return t;
+    }
 };
 
 namespace {
@@ -179,7 +266,7 @@ int forward_host(cfattn_ctx* c, const float* q, size_t q_len, const float* k, si
     float* dlse = static_cast<float*>(slot(c, cfattn_ctx::LSE, lse_len * 4, &rc));
     if (!dlse) return rc;
     CF_HIP(c, cfattn::launch_attn_fwd(bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), dq, dk, dv, dout, dlse,
-                                      c->stream, cfattn::Tuning{}),
+                                      c->stream, c->tuning()),
            "attention forward launch");
     CF_HIP(c, hipMemcpyAsync(o, dout, o_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H o");
     CF_HIP(c, hipMemcpyAsync(lse, dlse, lse_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H lse");
@@ -234,7 +321,7 @@ int backward_host(cfattn_ctx* c, const float* d_o, size_t d_o_len, const float* 
     CF_HIP(c, hipMemcpyAsync(g_k, dk, dk_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dk");
     CF_HIP(c, hipMemcpyAsync(g_v, dv, dv_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dv");
     CF_HIP(c, cfattn::launch_attn_bwd(bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), ddo, dq_in, dk_in, dv_in,
-                                      d_out, d_lse, delta, g_q, g_k, g_v, c->stream, cfattn::Tuning{}),
+                                      d_out, d_lse, delta, g_q, g_k, g_v, c->stream, c->tuning()),
            "attention backward launch");
     CF_HIP(c, hipMemcpyAsync(dq, g_q, dq_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H dq");
     CF_HIP(c, hipMemcpyAsync(dk, g_k, dk_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H dk");
@@ -295,6 +382,8 @@ int cfattn_destroy(cfattn_ctx* c) {
             (void)hipStreamSynchronize(c->stream);
             (void)hipStreamDestroy(c->stream);
         }
+        delete c->timer;
+        c->timer = nullptr;
         for (int i = 0; i < cfattn_ctx::NSLOT; i++)
             if (c->buf[i]) (void)hipFree(c->buf[i]);
     }
@@ -362,7 +451,7 @@ static int cfattn_fwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dt
     if (!q || !k || !v || !o || !lse) return fail(c, CFATTN_ERR_ARG, "null buffer");
     DeviceGuard dg(c->device);
     CF_HIP(c, cfattn::launch_attn_fwd((Dtype)dtype, dims_of(s, batch), q, k, v, o, lse, pick_stream(c, stream),
-                                      cfattn::Tuning{}),
+                                      c->tuning()),
            "attention forward launch");
     return CFATTN_OK;
 }
@@ -388,7 +477,7 @@ static int cfattn_bwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dt
     float* delta = static_cast<float*>(slot(c, cfattn_ctx::DELTA, batch * s.n_heads * s.seq * 4, &rc));
     if (!delta) return rc;
     CF_HIP(c, cfattn::launch_attn_bwd((Dtype)dtype, dims_of(s, batch), d_o, q, k, v, o, lse, delta, dq, dk, dv,
-                                      pick_stream(c, stream), cfattn::Tuning{}),
+                                      pick_stream(c, stream), c->tuning()),
            "attention backward launch");
     return CFATTN_OK;
 }
@@ -412,7 +501,7 @@ static int cfattn_prologue_fwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batc
     if (pr->q_norm && (!q_rstd || !k_rstd)) return fail(c, CFATTN_ERR_ARG, "q/k norm needs rstd outputs");
     DeviceGuard dg(c->device);
     CF_HIP(c, cfattn::launch_prologue_fwd((Dtype)dtype, dims_of(s, batch), to_prologue(pr), q_pre, k_pre, q_out,
-                                          k_out, q_rstd, k_rstd, pick_stream(c, stream)),
+                                          k_out, q_rstd, k_rstd, pick_stream(c, stream), c->timer),
            "prologue forward launch");
     return CFATTN_OK;
 }
@@ -445,7 +534,7 @@ static int cfattn_prologue_bwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batc
         if (!partial) return rc;
     }
     CF_HIP(c, cfattn::launch_prologue_bwd(d, to_prologue(pr), dq, dk, q_pre, k_pre, q_rstd, k_rstd, dq_pre, dk_pre,
-                                          dq_norm, dk_norm, partial, pick_stream(c, stream)),
+                                          dq_norm, dk_norm, partial, pick_stream(c, stream), c->timer),
            "prologue backward launch");
     return CFATTN_OK;
 }
@@ -535,6 +624,43 @@ int cfattn_f32_to_bf16(cfattn_ctx* c, const float* src, uint16_t* dst, size_t n,
     CF_HIP(c, cfattn::launch_f32_to_bf16(src, dst, n, pick_stream(c, stream)), "f32_to_bf16 launch");
     return CFATTN_OK;
 }
+
+int cfattn_profile_enable(cfattn_ctx* c, int on) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    DeviceGuard dg(c->device);
+    if (on) {
+        if (!c->timer) c->timer = new EventTimer();
+        (void)c->timer->collect();
+        c->timer->reset();
+    } else if (c->timer) {
+        delete c->timer;
+        c->timer = nullptr;
+    }
+    return CFATTN_OK;
+}
+
+int cfattn_profile_read(cfattn_ctx* c, int kernel, double* total_ms, long long* launches) {
+    if (!c || !total_ms || !launches) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    if (kernel < 0 || kernel >= cfattn::kNumKernels) return fail(c, CFATTN_ERR_ARG, "unknown kernel id %d", kernel);
+    if (!c->timer) return fail(c, CFATTN_ERR_ARG, "profiling is not enabled");
+    DeviceGuard dg(c->device);
+    CF_HIP(c, c->timer->collect(), "profile event");
+    *total_ms = c->timer->total_ms[kernel];
+    *launches = c->timer->launches[kernel];
+    return CFATTN_OK;
+}
+
+const char* cfattn_kernel_name(int kernel) {
+    static const char* names[cfattn::kNumKernels] = {"attn_fwd", "attn_bwd_delta", "attn_bwd_dkdv", "attn_bwd_dq",
+                                                      "prologue_fwd", "prologue_bwd"};
+    return kernel >= 0 && kernel < cfattn::kNumKernels ? names[kernel] : nullptr;
+}
+
+int cfattn_kernel_count(void) { return cfattn::kNumKernels; }
 
 double cfattn_flops_fwd_bwd(cfattn_shape s, size_t batch) {
     return 7.0 * (double)batch * (double)s.n_heads * (double)s.head_dim * (double)s.seq * ((double)s.seq + 1.0);

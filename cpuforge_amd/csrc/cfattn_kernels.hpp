@@ -17,12 +17,45 @@ struct Dims {
     int batch, seq, nh, nkv, hd;
 };
 
+// Kernels a launcher may time (ids are part of the C ABI: cfattn_kernel_name).
+enum KernelId {
+    kKernFwd = 0,
+    kKernBwdDelta = 1,
+    kKernBwdDkdv = 2,
+    kKernBwdDq = 3,
+    kKernProFwd = 4,
+    kKernProBwd = 5,
+    kNumKernels = 6
+};
+
+// Optional per-kernel timing: a launcher brackets each kernel it queues with
+// begin/end on the kernel's own stream (the C ABI records hipEvents there).
+struct KernelTimer {
+    virtual void begin(int kernel, hipStream_t st) = 0;
+    virtual void end(int kernel, hipStream_t st) = 0;
+    virtual ~KernelTimer() = default;
+};
+
 // Tuning knobs of one launch; defaults are chosen by the launchers.
 struct Tuning {
     int xcd_remap = 1;  // XCD-aware workgroup ordering
     int fwd_heads_per_wg = 0;  // 0 = automatic
     int fwd_tblocks_per_wg = 0;
     int bwd_kv_waves = 0;
+    KernelTimer* timer = nullptr;
+};
+
+// RAII bracket used by the launchers.
+struct TimedLaunch {
+    KernelTimer* t;
+    int k;
+    hipStream_t st;
+    TimedLaunch(KernelTimer* t_, int k_, hipStream_t st_) : t(t_), k(k_), st(st_) {
+        if (t) t->begin(k, st);
+    }
+    ~TimedLaunch() {
+        if (t) t->end(k, st);
+    }
 };
 
 hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k, const void* v, float* o,
@@ -47,7 +80,8 @@ struct Prologue {
     float eps;
 };
 hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, const float* q_pre, const float* k_pre,
-                               void* q_out, void* k_out, float* q_rstd, float* k_rstd, hipStream_t st);
+                               void* q_out, void* k_out, float* q_rstd, float* k_rstd, hipStream_t st,
+                               KernelTimer* timer = nullptr);
 
 // Prologue backward: inverse RoPE of dq/dk, then (with the norm) RMSNorm
 // backward.  dq_pre/dk_pre and dqw/dkw are accumulated.  `partial` is
@@ -55,7 +89,8 @@ hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, cons
 size_t prologue_bwd_scratch_floats(const Dims& d);
 hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* dq, const float* dk,
                                const float* q_pre, const float* k_pre, const float* q_rstd, const float* k_rstd,
-                               float* dq_pre, float* dk_pre, float* dqw, float* dkw, float* partial, hipStream_t st);
+                               float* dq_pre, float* dk_pre, float* dqw, float* dkw, float* partial, hipStream_t st,
+                               KernelTimer* timer = nullptr);
 
 // Elementwise helpers.
 hipError_t launch_f32_to_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t st);

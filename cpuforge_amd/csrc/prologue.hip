@@ -193,7 +193,8 @@ static unsigned grid_for(size_t n) {
 }
 
 hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, const float* q_pre, const float* k_pre,
-                               void* q_out, void* k_out, float* q_rstd, float* k_rstd, hipStream_t st) {
+                               void* q_out, void* k_out, float* q_rstd, float* k_rstd, hipStream_t st,
+                               KernelTimer* timer) {
     ProParams p{};
     p.q_pre = q_pre;
     p.k_pre = k_pre;
@@ -217,6 +218,7 @@ hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, cons
     const long rows = p.rows_q + p.rows_k;
     if (rows == 0) return hipSuccess;
     const unsigned grid = (unsigned)((rows + 255) / 256);
+    TimedLaunch tl(timer, kKernProFwd, st);
     if (dt == kBF16)
         hipLaunchKernelGGL(prologue_fwd_kernel<bf16_bits>, dim3(grid), dim3(256), 0, st, p);
     else
@@ -234,7 +236,8 @@ size_t prologue_bwd_scratch_floats(const Dims& d) {
 
 hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* dq, const float* dk,
                                const float* q_pre, const float* k_pre, const float* q_rstd, const float* k_rstd,
-                               float* dq_pre, float* dk_pre, float* dqw, float* dkw, float* partial, hipStream_t st) {
+                               float* dq_pre, float* dk_pre, float* dqw, float* dkw, float* partial, hipStream_t st,
+                               KernelTimer* timer) {
     ProBwdParams p{};
     p.dq = dq;
     p.dk = dk;
@@ -264,6 +267,7 @@ hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* d
     p.n_chunks_k = (int)((p.rows_k + kChunkRows - 1) / kChunkRows);
     const long rows = p.rows_q + p.rows_k;
     if (rows == 0) return hipSuccess;
+    TimedLaunch tl(timer, kKernProBwd, st);
     hipLaunchKernelGGL(prologue_bwd_rows_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !pr.qw) return e;

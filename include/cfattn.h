@@ -175,6 +175,19 @@ int cfattn_rope_table(size_t head_dim, size_t max_pos, double theta, const cfatt
 double cfattn_llama3_scale(const cfattn_llama3_scaling* scaling, double inv_freq);
 /* Device f32 -> bf16 (round to nearest even) conversion on `stream`. */
 int cfattn_f32_to_bf16(cfattn_ctx* ctx, const float* src, uint16_t* dst, size_t n, void* stream);
+/* ---- measurement ----------------------------------------------------------- */
+/* No reference counterpart: the reference times whole steps with a wall clock
+ * (cli/src/cmd_bench.rs:13-22).  While enabled, every kernel this context
+ * queues is bracketed by two hipEvents on the kernel's stream; enabling
+ * again resets the totals.  Disable with on = 0. */
+int cfattn_profile_enable(cfattn_ctx* ctx, int on);
+/* Waits for the recorded launches and returns, for kernel id `kernel`
+ * (0 .. cfattn_kernel_count()-1), the summed event time in milliseconds and
+ * the number of launches since profiling was enabled. */
+int cfattn_profile_read(cfattn_ctx* ctx, int kernel, double* total_ms, long long* launches);
+/* Name of kernel id `kernel` ("attn_fwd", "attn_bwd_dkdv", ...), or NULL. */
+const char* cfattn_kernel_name(int kernel);
+int cfattn_kernel_count(void);
 /* Algorithmic FLOPs of one fwd+bwd over the causal triangle:
  * 7 * batch * n_heads * head_dim * seq * (seq + 1). */
 double cfattn_flops_fwd_bwd(cfattn_shape s, size_t batch);
