@@ -222,6 +222,197 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams p) {
     if (hh == 0) p.lse[((long)b * p.nh + head) * p.seq + tq] = (m2 + log2f(ltot)) * kLn2;
 }
 
+// ---------------------------------------------------------------------------
+// Fast path: bf16 inputs, head_dim == DP (64 or 128), 16-byte aligned rows.
+// Four waves per workgroup, the same (tile, heads) decomposition as above.
+// K/V tiles of BN keys are prefetched into registers one tile ahead and
+// stored row-major into a double-buffered swizzled LDS tile, so each tile
+// costs one barrier.  S^T = K Q^T reads K rows with ds_read_b128; O^T +=
+// V^T P^T reads V^T straight from the row-major V tile with transposed reads
+// (ds_read_b64_tr_b16).  The running max is only moved when a tile's max
+// exceeds it by more than kLazyRescale (log2 units): exp2 of the shifted
+// scores then stays below 2^kLazyRescale, and O and the row sum are rescaled
+// only on those tiles.  O = acc / sum and lse = m + log2(sum) do not depend on
+// which shift was used.
+constexpr float kLazyRescale = 8.0f;
+
+template <int DP, int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_bf16_kernel(
+    const FwdParams p) {
+    constexpr int NT = 256;
+    constexpr int CPR = DP / 8;  // 16-byte chunks per row
+    constexpr int TILE = BN * DP;
+    constexpr int LOADS = BN * CPR / NT;
+    static_assert(BN * CPR % NT == 0, "tile must split evenly over the workgroup");
+    constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NKB = BN / 32;
+    __shared__ __attribute__((aligned(16))) bf16_bits sK[2][TILE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV[2][TILE];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
+    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;  // longest tiles first
+    int rest = id / p.n_ttiles;
+    const int sub = rest % p.n_sub;
+    rest /= p.n_sub;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+
+    const int head = g * p.group + sub * p.hpw + wave % p.hpw;
+    const int TT = 32 * p.tpw;
+    const int t_wave = tile * TT + (wave / p.hpw) * 32;
+    const int tq = t_wave + l32;
+    const int wg_end = min(p.seq, tile * TT + TT);
+    const int n_kt = (wg_end + BN - 1) / BN;
+    const bool wave_active = t_wave < p.seq;
+    const int wave_last = min(t_wave + 31, p.seq - 1);
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const bf16_bits* kg = static_cast<const bf16_bits*>(p.k) + (long)b * p.kv_bs + (long)g * DP;
+    const bf16_bits* vg = static_cast<const bf16_bits*>(p.v) + (long)b * p.kv_bs + (long)g * DP;
+
+    // Q^T operand: query tq, head dims hh*HALF + kd*8 + [0, 8).
+    bf16x8 qf[NKD];
+    {
+        const bf16_bits* qrow = static_cast<const bf16_bits*>(p.q) + (long)b * p.q_bs + (long)tq * qrs +
+                                (long)head * DP + hh * HALF;
+        const bool ok = tq < p.seq;
+#pragma unroll
+        for (int kd = 0; kd < NKD; kd++) {
+            uint4 u = ok ? *reinterpret_cast<const uint4*>(qrow + kd * 8) : make_uint4(0, 0, 0, 0);
+            qf[kd] = __builtin_bit_cast(bf16x8, u);
+        }
+    }
+
+    // Per-lane constants of the transposed V^T reads: lane 16*G + jj reads
+    // row kbase + 4*(G/2) + jj/4, head dims db*32 + 16*(G%2) + 4*(jj%4) + [0,4).
+    const int G = lane >> 4, jj = lane & 15;
+    const int tr_row = 4 * (G >> 1) + (jj >> 2);
+    const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
+    const int tr_in = 4 * (jj & 1);
+    const int tr_sw = swz(tr_row);
+    const int k_sw = swz(l32);
+
+    uint4 pk[LOADS], pv[LOADS];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
+            const int key = kt * BN + row;
+            if (key < p.seq) {
+                pk[i] = *reinterpret_cast<const uint4*>(kg + (long)key * kvrs + col * 8);
+                pv[i] = *reinterpret_cast<const uint4*>(vg + (long)key * kvrs + col * 8);
+            } else {
+                pk[i] = make_uint4(0, 0, 0, 0);
+                pv[i] = make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto lstore = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
+            *reinterpret_cast<uint4*>(&sK[st][swz_off<DP>(row, col)]) = pk[i];
+            *reinterpret_cast<uint4*>(&sV[st][swz_off<DP>(row, col)]) = pv[i];
+        }
+    };
+
+    f32x16 oacc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) oacc[i] = zero16();
+    float m2 = -INFINITY, lsum = 0.0f;
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < n_kt; kt++) {
+        const int st = kt & 1;
+        const bool more = kt + 1 < n_kt;
+        if (more) gload(kt + 1);
+        const int k0 = kt * BN;
+        if (wave_active && k0 <= wave_last) {
+            const bf16_bits* Ks = sK[st];
+            const bf16_bits* Vs = sV[st];
+#pragma unroll
+            for (int kb = 0; kb < NKB; kb++) {
+                const int kb0 = k0 + kb * 32;
+                if (kb0 > wave_last) break;
+                // S^T block: keys kb0 + [0,32) x this wave's 32 queries.
+                f32x16 s = zero16();
+                {
+                    bf16x8 kf[NKD];
+                    const bf16_bits* krow = Ks + (kb * 32 + l32) * DP;
+#pragma unroll
+                    for (int kd = 0; kd < NKD; kd++)
+                        kf[kd] = __builtin_bit_cast(
+                            bf16x8, *reinterpret_cast<const uint4*>(krow + (((hh * NKD + kd) ^ k_sw) << 3)));
+#pragma unroll
+                    for (int kd = 0; kd < NKD; kd++) s = mfma32(kf[kd], qf[kd], s);
+                }
+                float mx = -INFINITY;
+                if (kb0 + 31 > t_wave) {  // diagonal block: causal mask
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int key = kb0 + (r >> 2) * 8 + hh * 4 + (r & 3);
+                        if (key > tq) s[r] = -INFINITY;
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[r]);
+                mx = fmaxf(mx, __shfl_xor(mx, 32)) * p.sl2;
+                // Keys 0..31 are unmasked for every row, so mx is finite on the
+                // first block and m2 from then on.
+                const float mnew = mx > m2 + kLazyRescale ? mx : m2;
+                if (__any(mnew != m2)) {
+                    const float alpha = __builtin_amdgcn_exp2f(m2 - mnew);
+                    lsum *= alpha;
+#pragma unroll
+                    for (int i = 0; i < NDB; i++) oacc[i] *= alpha;
+                    m2 = mnew;
+                }
+                float pr[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], p.sl2, -m2));
+                    lsum += pr[r];
+                }
+                const bf16x8 p0 = cvt_bf16x8(&pr[0]), p1 = cvt_bf16x8(&pr[8]);
+                // O^T += V^T P^T over the block's two 16-key halves.
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    const int cofs = (((db * 4 + tr_cb) ^ tr_sw) << 3) + tr_in;
+                    const bf16_bits* v0 = Vs + (kb * 32 + tr_row) * DP + cofs;
+                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(v0), ds_read_tr16(v0 + 8 * DP));
+                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(v0 + 16 * DP), ds_read_tr16(v0 + 24 * DP));
+                    oacc[db] = mfma32(a0, p0, oacc[db]);
+                    oacc[db] = mfma32(a1, p1, oacc[db]);
+                }
+            }
+        }
+        if (more) lstore(st ^ 1);
+        __syncthreads();
+    }
+
+    if (!wave_active) return;
+    const float ltot = lsum + __shfl_xor(lsum, 32);
+    if (tq >= p.seq) return;
+    const float inv = 1.0f / ltot;
+    float* orow = p.o + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
+#pragma unroll
+    for (int db = 0; db < NDB; db++) {
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            const int d0 = db * 32 + rq * 8 + hh * 4;
+            *reinterpret_cast<float4*>(orow + d0) =
+                make_float4(oacc[db][rq * 4 + 0] * inv, oacc[db][rq * 4 + 1] * inv, oacc[db][rq * 4 + 2] * inv,
+                            oacc[db][rq * 4 + 3] * inv);
+        }
+    }
+    if (hh == 0) p.lse[((long)b * p.nh + head) * p.seq + tq] = (m2 + __log2f(ltot)) * kLn2;
+}
+
 // Heads per workgroup: the largest divisor of `group` not above `cap`.
 static int pick_hpw(int group, int cap) {
     for (int h = cap < group ? cap : group; h >= 1; h--)
@@ -276,6 +467,23 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
     p.vec_ok = (d.hd % ch == 0) && ((uintptr_t)q % al == 0) && ((uintptr_t)k % al == 0) && ((uintptr_t)v % al == 0);
     p.o_vec_ok = (d.hd % 4 == 0) && ((uintptr_t)o % al == 0);
     p.xcd = tu.xcd_remap;
+    if (dt == kBF16 && p.vec_ok && p.o_vec_ok && (d.hd == 64 || d.hd == 128) && tu.fwd_heads_per_wg == 0 &&
+        tu.fwd_tblocks_per_wg == 0) {
+        // Fast path: four waves per workgroup, heads per workgroup in {4, 2, 1}.
+        p.hpw = p.group % 4 == 0 ? 4 : p.group % 2 == 0 ? 2 : 1;
+        p.tpw = 4 / p.hpw;
+        p.n_sub = p.group / p.hpw;
+        p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
+        n_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+        if (n_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
+        p.n_wg = (int)n_wg;
+        TimedLaunch tl(tu.timer, kKernFwd, st);
+        if (d.hd == 128)
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 64>), dim3(p.n_wg), dim3(256), 0, st, p);
+        else
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 128>), dim3(p.n_wg), dim3(256), 0, st, p);
+        return hipGetLastError();
+    }
     const int nwaves = p.hpw * p.tpw;
     const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;
     if (dt == kBF16) {

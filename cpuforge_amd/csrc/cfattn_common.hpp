@@ -220,6 +220,41 @@ __device__ __forceinline__ void load_row_frag(T (&dst)[N], const T* __restrict__
     }
 }
 
+// ------------------------------------------------ swizzled bf16 LDS tiles
+// Fast-path tiles hold rows of DP bf16 (DP = 64 or 128) without padding; the
+// 16-byte chunk c of row r is stored at chunk position c ^ swz(r).  swz takes
+// eight distinct values over any eight consecutive rows (so the ds_read_b128
+// of eight rows at one chunk hits eight different bank groups) and maps four
+// consecutive rows starting at a multiple of 4 to {0,2,4,6} or {1,3,5,7} (so
+// a transposed read of 4 rows x 2 adjacent chunks touches 8 positions).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+template <int DP>
+__device__ __forceinline__ int swz_off(int r, int c) {
+    return r * DP + ((c ^ swz(r)) << 3);
+}
+
+// Hardware round-to-nearest-even pack of eight f32 values into an MFMA
+// operand (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16x8 cvt_bf16x8(const float* v) {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r[i] = (__bf16)v[i];
+    return r;
+}
+
+// Transposed LDS read (ds_read_b64_tr_b16).  Within each group of 16 lanes,
+// output lane i, element k (k = 0..3) is element i % 4 of the 8-byte row whose
+// address lane 4*k + i/4 supplies.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ s16x4 ds_read_tr16(const bf16_bits* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+__device__ __forceinline__ bf16x8 join_bf16x4(s16x4 a, s16x4 b) {
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    s16x8 v = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(bf16x8, v);
+}
+
 // Leading dimensions with padding chosen so that the MFMA operand reads
 // (16-byte row reads for row-major tiles, 8/16-byte reads of four
 // consecutive rows for transposed tiles) spread over all LDS banks.

@@ -210,3 +210,43 @@ def test_c2_parity(cf, mode):
 
 def test_c5_bf16_parity(cf):
     _device_check(cf, CONFIGS["C5"], "bf16", seqs=(0,), head_groups=(0, 7))
+
+
+# Shapes that exercise the bf16 fast paths (head_dim 64/128, 16-byte rows):
+# ragged last tiles, seq 1, GQA with 4/2/1 heads per workgroup, MHA and MQA,
+# several sequences per call.  (batch, seq, n_heads, n_kv, head_dim)
+FAST_SHAPES = [(1, 1, 4, 1, 128), (2, 33, 4, 2, 64), (1, 100, 8, 2, 128), (1, 257, 6, 3, 64),
+               (2, 130, 3, 3, 128), (1, 200, 4, 1, 64), (1, 511, 2, 2, 128)]
+
+
+@pytest.mark.parametrize("shape", FAST_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_bf16_fast_path_shapes(cf, shape):
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    B, S, Hq, Hk, Dh = shape
+    print(f"fast-path shape {shape}", flush=True)
+    host = []
+    for b in range(B):
+        sd = 500 + 16 * b
+        host.append(tuple(O.round_bf16(O.rand(S * h * Dh, sd + i, 1.0)) for i, h in enumerate((Hq, Hk, Hk, Hq))))
+
+    def dev(i, heads):
+        return torch.from_numpy(np.stack([h[i] for h in host])).view(B, S, heads, Dh).to("cuda").to(torch.bfloat16)
+
+    q, k, v, g = dev(0, Hq), dev(1, Hk), dev(2, Hk), dev(3, Hq)
+    o, lse = D.fwd(q, k, v, ctx=ctx)
+    dq, dk, dv = D.bwd(g, q, k, v, o, lse, ctx=ctx)
+    torch.cuda.synchronize()
+    o, lse, dq, dk, dv = (x.cpu().numpy() for x in (o, lse, dq, dk, dv))
+    for b in range(B):
+        hq, hk, hv, hg = host[b]
+        ro = np.zeros(S * Hq * Dh, np.float32)
+        rl = np.zeros(Hq * S, np.float32)
+        O.attention_forward_blocked(hq, hk, hv, ro, rl, S, Hq, Hk, Dh, 128)
+        rq, rk, rv = np.zeros_like(ro), np.zeros(S * Hk * Dh, np.float32), np.zeros(S * Hk * Dh, np.float32)
+        O.attention_backward_blocked(hg, hq, hk, hv, ro, rl, rq, rk, rv, S, Hq, Hk, Dh, 128)
+        for name, a, r in (("o", o[b], ro), ("lse", lse[b], rl), ("dq", dq[b], rq), ("dk", dk[b], rk),
+                           ("dv", dv[b], rv)):
+            e = rel_err(a.reshape(-1), r)
+            assert e <= BF16_TOL, f"{shape} seq {b} {name}: {e}"
