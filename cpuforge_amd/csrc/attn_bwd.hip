@@ -422,6 +422,358 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams p) {
     for (int db = 0; db < NDB; db++) add_row_block(dqrow, dqt[db], db * 32, hh, p.hd, p.g_vec_ok);
 }
 
+// ---------------------------------------------------------------------------
+// Fast paths: bf16 inputs, head_dim == DP (64 or 128), 16-byte aligned rows.
+// Tiles are staged row-major into double-buffered swizzled LDS (prefetched
+// into registers one step ahead, one barrier per step); every transposed
+// operand (dO^T, Q^T, K^T) is read from the row-major tile with
+// ds_read_b64_tr_b16.  The contraction order over heads and tiles is fixed,
+// so results stay bitwise reproducible.
+
+// dK/dV: four waves, each owning 32 keys of one KV head; steps run over
+// (query head of the group, query tile of BM rows) in a fixed order.
+template <int DP, int BM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_bwd_dkdv_bf16_kernel(
+    const BwdParams p) {
+    constexpr int NT = 256;
+    constexpr int CPR = DP / 8;
+    constexpr int TILE = BM * DP;
+    constexpr int LOADS = BM * CPR / NT;
+    static_assert(BM * CPR % NT == 0 && BM <= NT / 2, "tile must split evenly over the workgroup");
+    constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NQB = BM / 32;
+    __shared__ __attribute__((aligned(16))) bf16_bits sQ[2][TILE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sO[2][TILE];  // dO rows
+    __shared__ __attribute__((aligned(16))) float sL[2][BM];        // lse * log2(e)
+    __shared__ __attribute__((aligned(16))) float sD[2][BM];        // delta
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
+    const int kvt = id % p.n_kvtiles;  // low key tiles see the most queries: first
+    const int rest = id / p.n_kvtiles;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+    const int wg_key0 = kvt * p.kv_tile;
+    const int key0 = wg_key0 + wave * 32;
+    const int kw = key0 + l32;
+    const bool wave_active = key0 < p.seq;
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const bf16_bits* qg = static_cast<const bf16_bits*>(p.q) + (long)b * p.q_bs;
+    const bf16_bits* og = static_cast<const bf16_bits*>(p.d_o) + (long)b * p.q_bs;
+
+    // K^T and V^T operands: key kw, head dims hh*HALF + kd*8 + [0, 8).
+    bf16x8 kf[NKD], vf[NKD];
+    {
+        const long off = (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP + hh * HALF;
+        const bf16_bits* kr = static_cast<const bf16_bits*>(p.k) + off;
+        const bf16_bits* vr = static_cast<const bf16_bits*>(p.v) + off;
+        const bool ok = kw < p.seq;
+#pragma unroll
+        for (int kd = 0; kd < NKD; kd++) {
+            kf[kd] = __builtin_bit_cast(bf16x8, ok ? *reinterpret_cast<const uint4*>(kr + kd * 8) : make_uint4(0, 0, 0, 0));
+            vf[kd] = __builtin_bit_cast(bf16x8, ok ? *reinterpret_cast<const uint4*>(vr + kd * 8) : make_uint4(0, 0, 0, 0));
+        }
+    }
+
+    const int G = lane >> 4, jj = lane & 15;
+    const int tr_row = 4 * (G >> 1) + (jj >> 2);
+    const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
+    const int tr_in = 4 * (jj & 1);
+    const int tr_sw = swz(tr_row);
+    const int r_sw = swz(l32);
+
+    const int n_qt = (p.seq + BM - 1) / BM;
+    const int qt_begin = wg_key0 / BM;
+    const int nq = n_qt - qt_begin;
+    const int n_steps = p.group * nq;
+
+    uint4 pq[LOADS], po[LOADS];
+    float pl = 0.0f;
+    auto gload = [&](int s) {
+        const int h = g * p.group + s / nq;
+        const int q0 = (qt_begin + s % nq) * BM;
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
+            const int t = q0 + row;
+            if (t < p.seq) {
+                const long off = (long)t * qrs + (long)h * DP + col * 8;
+                pq[i] = *reinterpret_cast<const uint4*>(qg + off);
+                po[i] = *reinterpret_cast<const uint4*>(og + off);
+            } else {
+                pq[i] = make_uint4(0, 0, 0, 0);
+                po[i] = make_uint4(0, 0, 0, 0);
+            }
+        }
+        if (tid < 2 * BM) {
+            const int t = q0 + (tid % BM);
+            const long li = ((long)b * p.nh + h) * p.seq + t;
+            if (tid < BM)
+                pl = t < p.seq ? p.lse[li] * kLog2e : INFINITY;  // rows past the end: P = 0
+            else
+                pl = t < p.seq ? p.delta[li] : 0.0f;
+        }
+    };
+    auto lstore = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
+            *reinterpret_cast<uint4*>(&sQ[st][swz_off<DP>(row, col)]) = pq[i];
+            *reinterpret_cast<uint4*>(&sO[st][swz_off<DP>(row, col)]) = po[i];
+        }
+        if (tid < BM)
+            sL[st][tid] = pl;
+        else if (tid < 2 * BM)
+            sD[st][tid - BM] = pl;
+    };
+
+    f32x16 dkt[NDB], dvt[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) {
+        dkt[i] = zero16();
+        dvt[i] = zero16();
+    }
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int s = 0; s < n_steps; s++) {
+        const int st = s & 1;
+        const bool more = s + 1 < n_steps;
+        if (more) gload(s + 1);
+        const int q0 = (qt_begin + s % nq) * BM;
+        if (wave_active && q0 + BM - 1 >= key0) {
+            const bf16_bits* Qs = sQ[st];
+            const bf16_bits* Os = sO[st];
+#pragma unroll
+            for (int qb = 0; qb < NQB; qb++) {
+                const int tq0 = q0 + qb * 32;
+                if (tq0 >= p.seq) break;
+                if (tq0 + 31 < key0) continue;
+                // S and dP: rows = queries tq0 + [0,32), columns = this wave's keys.
+                f32x16 sc = zero16(), dp = zero16();
+                {
+                    const bf16_bits* qrow = Qs + (qb * 32 + l32) * DP;
+                    const bf16_bits* orow = Os + (qb * 32 + l32) * DP;
+                    bf16x8 qa[NKD], oa[NKD];
+#pragma unroll
+                    for (int kd = 0; kd < NKD; kd++) {
+                        const int co = ((hh * NKD + kd) ^ r_sw) << 3;
+                        qa[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + co));
+                        oa[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(orow + co));
+                    }
+#pragma unroll
+                    for (int kd = 0; kd < NKD; kd++) {
+                        sc = mfma32(qa[kd], kf[kd], sc);
+                        dp = mfma32(oa[kd], vf[kd], dp);
+                    }
+                }
+                const bool need_mask = tq0 < key0 + 31;
+                float pr[16], ds[16];
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const int qi = qb * 32 + g4 * 8 + hh * 4;
+                    const float4 l4 = *reinterpret_cast<const float4*>(&sL[st][qi]);
+                    const float4 d4 = *reinterpret_cast<const float4*>(&sD[st][qi]);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                    const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int r = g4 * 4 + i;
+                        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lv[i]));
+                        if (need_mask && kw > q0 + qi + i) pv = 0.0f;
+                        pr[r] = pv;
+                        ds[r] = pv * (dp[r] - dv[i]) * p.scale;
+                    }
+                }
+                const bf16x8 p0 = cvt_bf16x8(&pr[0]), p1 = cvt_bf16x8(&pr[8]);
+                const bf16x8 d0 = cvt_bf16x8(&ds[0]), d1 = cvt_bf16x8(&ds[8]);
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    const int cofs = (((db * 4 + tr_cb) ^ tr_sw) << 3) + tr_in;
+                    const bf16_bits* o0 = Os + (qb * 32 + tr_row) * DP + cofs;
+                    const bf16_bits* q0p = Qs + (qb * 32 + tr_row) * DP + cofs;
+                    const bf16x8 oa0 = join_bf16x4(ds_read_tr16(o0), ds_read_tr16(o0 + 8 * DP));
+                    const bf16x8 oa1 = join_bf16x4(ds_read_tr16(o0 + 16 * DP), ds_read_tr16(o0 + 24 * DP));
+                    const bf16x8 qa0 = join_bf16x4(ds_read_tr16(q0p), ds_read_tr16(q0p + 8 * DP));
+                    const bf16x8 qa1 = join_bf16x4(ds_read_tr16(q0p + 16 * DP), ds_read_tr16(q0p + 24 * DP));
+                    dvt[db] = mfma32(oa0, p0, dvt[db]);
+                    dvt[db] = mfma32(oa1, p1, dvt[db]);
+                    dkt[db] = mfma32(qa0, d0, dkt[db]);
+                    dkt[db] = mfma32(qa1, d1, dkt[db]);
+                }
+            }
+        }
+        if (more) lstore(st ^ 1);
+        __syncthreads();
+    }
+
+    if (!wave_active || kw >= p.seq) return;
+    float* dkrow = p.dk + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
+    float* dvrow = p.dv + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
+#pragma unroll
+    for (int db = 0; db < NDB; db++) {
+        add_row_block(dkrow, dkt[db], db * 32, hh, DP, true);
+        add_row_block(dvrow, dvt[db], db * 32, hh, DP, true);
+    }
+}
+
+// dQ: the forward's decomposition (a wave owns 32 queries of one head, four
+// waves per workgroup); K/V tiles of BN keys are shared by the workgroup.
+template <int DP, int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq_bf16_kernel(
+    const BwdParams p) {
+    constexpr int NT = 256;
+    constexpr int CPR = DP / 8;
+    constexpr int TILE = BN * DP;
+    constexpr int LOADS = BN * CPR / NT;
+    static_assert(BN * CPR % NT == 0, "tile must split evenly over the workgroup");
+    constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NKB = BN / 32;
+    __shared__ __attribute__((aligned(16))) bf16_bits sK[2][TILE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV[2][TILE];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg_q, p.xcd);
+    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;
+    int rest = id / p.n_ttiles;
+    const int sub = rest % p.n_sub;
+    rest /= p.n_sub;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+
+    const int head = g * p.group + sub * p.hpw + wave % p.hpw;
+    const int TT = 32 * p.tpw;
+    const int t_wave = tile * TT + (wave / p.hpw) * 32;
+    const int tq = t_wave + l32;
+    const int wg_end = min(p.seq, tile * TT + TT);
+    const int n_kt = (wg_end + BN - 1) / BN;
+    const bool wave_active = t_wave < p.seq;
+    const int wave_last = min(t_wave + 31, p.seq - 1);
+    const bool row_ok = tq < p.seq;
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const long qoff = (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
+    const bf16_bits* kg = static_cast<const bf16_bits*>(p.k) + (long)b * p.kv_bs + (long)g * DP;
+    const bf16_bits* vg = static_cast<const bf16_bits*>(p.v) + (long)b * p.kv_bs + (long)g * DP;
+
+    bf16x8 qf[NKD], of[NKD];
+    {
+        const bf16_bits* qr = static_cast<const bf16_bits*>(p.q) + qoff + hh * HALF;
+        const bf16_bits* orr = static_cast<const bf16_bits*>(p.d_o) + qoff + hh * HALF;
+#pragma unroll
+        for (int kd = 0; kd < NKD; kd++) {
+            qf[kd] = __builtin_bit_cast(bf16x8, row_ok ? *reinterpret_cast<const uint4*>(qr + kd * 8) : make_uint4(0, 0, 0, 0));
+            of[kd] = __builtin_bit_cast(bf16x8, row_ok ? *reinterpret_cast<const uint4*>(orr + kd * 8) : make_uint4(0, 0, 0, 0));
+        }
+    }
+    const long lrow = ((long)b * p.nh + head) * p.seq + tq;
+    const float lse2 = row_ok ? p.lse[lrow] * kLog2e : INFINITY;
+    const float dlt = row_ok ? p.delta[lrow] : 0.0f;
+
+    const int G = lane >> 4, jj = lane & 15;
+    const int tr_row = 4 * (G >> 1) + (jj >> 2);
+    const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
+    const int tr_in = 4 * (jj & 1);
+    const int tr_sw = swz(tr_row);
+    const int k_sw = swz(l32);
+
+    uint4 pk[LOADS], pv[LOADS];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
+            const int key = kt * BN + row;
+            if (key < p.seq) {
+                pk[i] = *reinterpret_cast<const uint4*>(kg + (long)key * kvrs + col * 8);
+                pv[i] = *reinterpret_cast<const uint4*>(vg + (long)key * kvrs + col * 8);
+            } else {
+                pk[i] = make_uint4(0, 0, 0, 0);
+                pv[i] = make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto lstore = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < LOADS; i++) {
+            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
+            *reinterpret_cast<uint4*>(&sK[st][swz_off<DP>(row, col)]) = pk[i];
+            *reinterpret_cast<uint4*>(&sV[st][swz_off<DP>(row, col)]) = pv[i];
+        }
+    };
+
+    f32x16 dqt[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) dqt[i] = zero16();
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < n_kt; kt++) {
+        const int st = kt & 1;
+        const bool more = kt + 1 < n_kt;
+        if (more) gload(kt + 1);
+        const int k0 = kt * BN;
+        if (wave_active && k0 <= wave_last) {
+            const bf16_bits* Ks = sK[st];
+            const bf16_bits* Vs = sV[st];
+#pragma unroll
+            for (int kb = 0; kb < NKB; kb++) {
+                const int kb0 = k0 + kb * 32;
+                if (kb0 > wave_last) break;
+                f32x16 sc = zero16(), dp = zero16();
+                {
+                    const bf16_bits* krow = Ks + (kb * 32 + l32) * DP;
+                    const bf16_bits* vrow = Vs + (kb * 32 + l32) * DP;
+                    bf16x8 ka[NKD], va[NKD];
+#pragma unroll
+                    for (int kd = 0; kd < NKD; kd++) {
+                        const int co = ((hh * NKD + kd) ^ k_sw) << 3;
+                        ka[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(krow + co));
+                        va[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(vrow + co));
+                    }
+#pragma unroll
+                    for (int kd = 0; kd < NKD; kd++) {
+                        sc = mfma32(ka[kd], qf[kd], sc);
+                        dp = mfma32(va[kd], of[kd], dp);
+                    }
+                }
+                const bool need_mask = kb0 + 31 > t_wave;
+                float ds[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    float pv_ = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lse2));
+                    if (need_mask && kb0 + (r >> 2) * 8 + hh * 4 + (r & 3) > tq) pv_ = 0.0f;
+                    ds[r] = pv_ * (dp[r] - dlt) * p.scale;
+                }
+                const bf16x8 d0 = cvt_bf16x8(&ds[0]), d1 = cvt_bf16x8(&ds[8]);
+                // dQ^T += K^T dS^T, K^T read transposed from the K tile.
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    const int cofs = (((db * 4 + tr_cb) ^ tr_sw) << 3) + tr_in;
+                    const bf16_bits* k0p = Ks + (kb * 32 + tr_row) * DP + cofs;
+                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(k0p), ds_read_tr16(k0p + 8 * DP));
+                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(k0p + 16 * DP), ds_read_tr16(k0p + 24 * DP));
+                    dqt[db] = mfma32(a0, d0, dqt[db]);
+                    dqt[db] = mfma32(a1, d1, dqt[db]);
+                }
+            }
+        }
+        if (more) lstore(st ^ 1);
+        __syncthreads();
+    }
+
+    if (!wave_active || !row_ok) return;
+    float* dqrow = p.dq + qoff;
+#pragma unroll
+    for (int db = 0; db < NDB; db++) add_row_block(dqrow, dqt[db], db * 32, hh, DP, true);
+}
+
 static int pick_hpw_b(int group, int cap) {
     for (int h = cap < group ? cap : group; h >= 1; h--)
         if (group % h == 0) return h;
@@ -494,6 +846,40 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
                ((uintptr_t)v % al == 0) && ((uintptr_t)d_o % al == 0);
     p.g_vec_ok = (d.hd % 4 == 0) && ((uintptr_t)dq % al == 0) && ((uintptr_t)dk % al == 0) && ((uintptr_t)dv % al == 0);
     p.xcd = tu.xcd_remap;
+    if (dt == kBF16 && p.vec_ok && p.g_vec_ok && (d.hd == 64 || d.hd == 128) && tu.bwd_kv_waves == 0) {
+        // Fast paths: four waves per workgroup in both kernels.
+        p.hpw = p.group % 4 == 0 ? 4 : p.group % 2 == 0 ? 2 : 1;
+        p.tpw = 4 / p.hpw;
+        p.n_sub = p.group / p.hpw;
+        p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
+        nq_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+        if (nq_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
+        p.n_wg_q = (int)nq_wg;
+        const long rows = (long)p.batch * p.seq * p.nh;
+        hipError_t e;
+        {
+            TimedLaunch tl(tu.timer, kKernBwdDelta, st);
+            hipLaunchKernelGGL((attn_bwd_delta_kernel<bf16_bits>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0,
+                               st, p);
+            e = hipGetLastError();
+        }
+        if (e != hipSuccess) return e;
+        {
+            TimedLaunch tl(tu.timer, kKernBwdDkdv, st);
+            if (d.hd == 128)
+                hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 64>), dim3(p.n_wg_kv), dim3(256), 0, st, p);
+            else
+                hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 64>), dim3(p.n_wg_kv), dim3(256), 0, st, p);
+            e = hipGetLastError();
+        }
+        if (e != hipSuccess) return e;
+        TimedLaunch tl(tu.timer, kKernBwdDq, st);
+        if (d.hd == 128)
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 32>), dim3(p.n_wg_q), dim3(256), 0, st, p);
+        else
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, 128>), dim3(p.n_wg_q), dim3(256), 0, st, p);
+        return hipGetLastError();
+    }
     const int q_waves = p.hpw * p.tpw;
     const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;
     if (dt == kBF16) {
