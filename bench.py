@@ -66,6 +66,8 @@ def parse():
     ap.add_argument("--mode", default=None, choices=["bf16", "f32"], help="default: bf16 (f32 for C1)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--cpu-heads", type=int, default=16, help="query heads of sequence 0 in the CPU sample")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="run one plain device copy of MIB MiB before timing (calibrates rocprofv3 byte counters)")
     ap.add_argument("--traffic-file", default=None,
                     help="rocprofv3 traffic summary to read `traffic` from (default: profiles/ match)")
     return ap.parse_args()
@@ -163,6 +165,13 @@ def main():
         dev.fwd(q, k, v, o, lse, ctx=ctx)
         dev.bwd(d_o, q, k, v, o, lse, dq, dk, dv, ctx=ctx)
 
+    if a.copy_probe:
+        src = torch.empty(a.copy_probe << 18, device="cuda", dtype=torch.float32).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
@@ -194,7 +203,7 @@ def main():
     dom_flops = ALGO_UNITS[dom] * B * Hq * D * S * (S + 1)
     achieved = dom_flops / (dom_ms * 1e-3) / 1e12
     peak = PEAK_TFLOPS[mode]
-    tpath = a.traffic_file or os.path.join(ROOT, "profiles", "traffic.txt")
+    tpath = a.traffic_file or os.path.join(ROOT, "profiles", f"hbm_traffic_{a.config}_{mode}.md")
     traffic = read_traffic(tpath, dom, f"{a.config}-{mode}")
 
     out = {

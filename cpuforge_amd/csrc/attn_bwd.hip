@@ -440,6 +440,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int TILE = BM * DP;
     constexpr int LOADS = BM * CPR / NT;
     static_assert(BM * CPR % NT == 0 && BM <= NT / 2, "tile must split evenly over the workgroup");
+    static_assert(BM % 32 == 0, "query tile must be whole 32-row blocks");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NQB = BM / 32;
     __shared__ __attribute__((aligned(16))) bf16_bits sQ[2][TILE];
     __shared__ __attribute__((aligned(16))) bf16_bits sO[2][TILE];  // dO rows
@@ -482,8 +483,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int tr_row = 4 * (G >> 1) + (jj >> 2);
     const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
     const int tr_in = 4 * (jj & 1);
-    const int tr_sw = swz(tr_row);
-    const int r_sw = swz(l32);
+    const int tr_sw0 = swz<DP>(tr_row), tr_sw8 = swz<DP>(tr_row + 8);
+    const int r_sw = swz<DP>(l32);
 
     const int n_qt = (p.seq + BM - 1) / BM;
     const int qt_begin = wg_key0 / BM;
@@ -492,6 +493,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     uint4 pq[LOADS], po[LOADS];
     float pl = 0.0f;
+    // Step s covers query tile qt_begin + s % nq of query head s / nq.
     auto gload = [&](int s) {
         const int h = g * p.group + s / nq;
         const int q0 = (qt_begin + s % nq) * BM;
@@ -548,43 +550,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         if (wave_active && q0 + BM - 1 >= key0) {
             const bf16_bits* Qs = sQ[st];
             const bf16_bits* Os = sO[st];
+            const float* Ls = sL[st];
+            const float* Ds = sD[st];
+            // S and dP for query block qb: rows = queries q0 + qb*32 + [0,32),
+            // columns = this wave's keys.
+            auto scores = [&](int qb, f32x16& sc, f32x16& dp) {
+                sc = zero16();
+                dp = zero16();
+                const bf16_bits* qrow = Qs + (qb * 32 + l32) * DP;
+                const bf16_bits* orow = Os + (qb * 32 + l32) * DP;
+                bf16x8 qa[NKD], oa[NKD];
 #pragma unroll
-            for (int qb = 0; qb < NQB; qb++) {
-                const int tq0 = q0 + qb * 32;
-                if (tq0 >= p.seq) break;
-                if (tq0 + 31 < key0) continue;
-                // S and dP: rows = queries tq0 + [0,32), columns = this wave's keys.
-                f32x16 sc = zero16(), dp = zero16();
-                {
-                    const bf16_bits* qrow = Qs + (qb * 32 + l32) * DP;
-                    const bf16_bits* orow = Os + (qb * 32 + l32) * DP;
-                    bf16x8 qa[NKD], oa[NKD];
-#pragma unroll
-                    for (int kd = 0; kd < NKD; kd++) {
-                        const int co = ((hh * NKD + kd) ^ r_sw) << 3;
-                        qa[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + co));
-                        oa[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(orow + co));
-                    }
-#pragma unroll
-                    for (int kd = 0; kd < NKD; kd++) {
-                        sc = mfma32(qa[kd], kf[kd], sc);
-                        dp = mfma32(oa[kd], vf[kd], dp);
-                    }
+                for (int kd = 0; kd < NKD; kd++) {
+                    const int co = ((hh * NKD + kd) ^ r_sw) << 3;
+                    qa[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + co));
+                    oa[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(orow + co));
                 }
-                const bool need_mask = tq0 < key0 + 31;
+#pragma unroll
+                for (int kd = 0; kd < NKD; kd++) {
+                    sc = mfma32(qa[kd], kf[kd], sc);
+                    dp = mfma32(oa[kd], vf[kd], dp);
+                }
+            };
+            // P = exp2(S*scale*log2e - lse*log2e), dS = P (dP - delta) scale;
+            // dV^T += dO^T P and dK^T += Q^T dS with dO^T and Q^T read
+            // transposed from the row-major tiles.
+            auto accumulate = [&](int qb, const f32x16& sc, const f32x16& dp, bool masked) {
                 float pr[16], ds[16];
 #pragma unroll
                 for (int g4 = 0; g4 < 4; g4++) {
                     const int qi = qb * 32 + g4 * 8 + hh * 4;
-                    const float4 l4 = *reinterpret_cast<const float4*>(&sL[st][qi]);
-                    const float4 d4 = *reinterpret_cast<const float4*>(&sD[st][qi]);
+                    const float4 l4 = *reinterpret_cast<const float4*>(&Ls[qi]);
+                    const float4 d4 = *reinterpret_cast<const float4*>(&Ds[qi]);
                     const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
                     const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const int r = g4 * 4 + i;
                         float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lv[i]));
-                        if (need_mask && kw > q0 + qi + i) pv = 0.0f;
+                        if (masked && kw > q0 + qi + i) pv = 0.0f;
                         pr[r] = pv;
                         ds[r] = pv * (dp[r] - dv[i]) * p.scale;
                     }
@@ -593,17 +597,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 const bf16x8 d0 = cvt_bf16x8(&ds[0]), d1 = cvt_bf16x8(&ds[8]);
 #pragma unroll
                 for (int db = 0; db < NDB; db++) {
-                    const int cofs = (((db * 4 + tr_cb) ^ tr_sw) << 3) + tr_in;
-                    const bf16_bits* o0 = Os + (qb * 32 + tr_row) * DP + cofs;
-                    const bf16_bits* q0p = Qs + (qb * 32 + tr_row) * DP + cofs;
-                    const bf16x8 oa0 = join_bf16x4(ds_read_tr16(o0), ds_read_tr16(o0 + 8 * DP));
-                    const bf16x8 oa1 = join_bf16x4(ds_read_tr16(o0 + 16 * DP), ds_read_tr16(o0 + 24 * DP));
-                    const bf16x8 qa0 = join_bf16x4(ds_read_tr16(q0p), ds_read_tr16(q0p + 8 * DP));
-                    const bf16x8 qa1 = join_bf16x4(ds_read_tr16(q0p + 16 * DP), ds_read_tr16(q0p + 24 * DP));
+                    const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
+                    const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
+                    const bf16_bits* o0 = Os + (qb * 32 + tr_row) * DP;
+                    const bf16_bits* q0p = Qs + (qb * 32 + tr_row) * DP;
+                    const bf16x8 oa0 = join_bf16x4(ds_read_tr16(o0 + c0), ds_read_tr16(o0 + 8 * DP + c8));
+                    const bf16x8 oa1 = join_bf16x4(ds_read_tr16(o0 + 16 * DP + c0), ds_read_tr16(o0 + 24 * DP + c8));
+                    const bf16x8 qa0 = join_bf16x4(ds_read_tr16(q0p + c0), ds_read_tr16(q0p + 8 * DP + c8));
+                    const bf16x8 qa1 = join_bf16x4(ds_read_tr16(q0p + 16 * DP + c0), ds_read_tr16(q0p + 24 * DP + c8));
                     dvt[db] = mfma32(oa0, p0, dvt[db]);
                     dvt[db] = mfma32(oa1, p1, dvt[db]);
                     dkt[db] = mfma32(qa0, d0, dkt[db]);
                     dkt[db] = mfma32(qa1, d1, dkt[db]);
+                }
+            };
+            if (q0 >= wg_key0 + p.kv_tile) {
+                // Interior step: every query of the tile follows every key of
+                // the workgroup, so the blocks need no mask and no branch and
+                // the scheduler can overlap one block's softmax with another
+                // block's matrix work.
+#pragma unroll
+                for (int qb = 0; qb < NQB; qb++) {
+                    f32x16 sc, dp;
+                    scores(qb, sc, dp);
+                    accumulate(qb, sc, dp, false);
+                }
+            } else {
+#pragma unroll
+                for (int qb = 0; qb < NQB; qb++) {
+                    const int tq0 = q0 + qb * 32;
+                    if (tq0 >= p.seq) break;
+                    if (tq0 + 31 < key0) continue;
+                    f32x16 sc, dp;
+                    scores(qb, sc, dp);
+                    accumulate(qb, sc, dp, tq0 < key0 + 31);
                 }
             }
         }
@@ -680,8 +707,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int tr_row = 4 * (G >> 1) + (jj >> 2);
     const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
     const int tr_in = 4 * (jj & 1);
-    const int tr_sw = swz(tr_row);
-    const int k_sw = swz(l32);
+    const int tr_sw0 = swz<DP>(tr_row), tr_sw8 = swz<DP>(tr_row + 8);
+    const int k_sw = swz<DP>(l32);
 
     uint4 pk[LOADS], pv[LOADS];
     auto gload = [&](int kt) {
@@ -755,10 +782,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 // dQ^T += K^T dS^T, K^T read transposed from the K tile.
 #pragma unroll
                 for (int db = 0; db < NDB; db++) {
-                    const int cofs = (((db * 4 + tr_cb) ^ tr_sw) << 3) + tr_in;
-                    const bf16_bits* k0p = Ks + (kb * 32 + tr_row) * DP + cofs;
-                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(k0p), ds_read_tr16(k0p + 8 * DP));
-                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(k0p + 16 * DP), ds_read_tr16(k0p + 24 * DP));
+                    const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
+                    const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
+                    const bf16_bits* k0p = Ks + (kb * 32 + tr_row) * DP;
+                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(k0p + c0), ds_read_tr16(k0p + 8 * DP + c8));
+                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(k0p + 16 * DP + c0), ds_read_tr16(k0p + 24 * DP + c8));
                     dqt[db] = mfma32(a0, d0, dqt[db]);
                     dqt[db] = mfma32(a1, d1, dqt[db]);
                 }

@@ -292,8 +292,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int tr_row = 4 * (G >> 1) + (jj >> 2);
     const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
     const int tr_in = 4 * (jj & 1);
-    const int tr_sw = swz(tr_row);
-    const int k_sw = swz(l32);
+    const int tr_sw0 = swz<DP>(tr_row), tr_sw8 = swz<DP>(tr_row + 8);
+    const int k_sw = swz<DP>(l32);
 
     uint4 pk[LOADS], pv[LOADS];
     auto gload = [&](int kt) {
@@ -335,35 +335,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (wave_active && k0 <= wave_last) {
             const bf16_bits* Ks = sK[st];
             const bf16_bits* Vs = sV[st];
+            // S^T block kb: keys k0 + kb*32 + [0,32) x this wave's 32 queries.
+            auto scores = [&](int kb) {
+                f32x16 sc = zero16();
+                bf16x8 kf[NKD];
+                const bf16_bits* krow = Ks + (kb * 32 + l32) * DP;
 #pragma unroll
-            for (int kb = 0; kb < NKB; kb++) {
-                const int kb0 = k0 + kb * 32;
-                if (kb0 > wave_last) break;
-                // S^T block: keys kb0 + [0,32) x this wave's 32 queries.
-                f32x16 s = zero16();
-                {
-                    bf16x8 kf[NKD];
-                    const bf16_bits* krow = Ks + (kb * 32 + l32) * DP;
+                for (int kd = 0; kd < NKD; kd++)
+                    kf[kd] = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const uint4*>(krow + (((hh * NKD + kd) ^ k_sw) << 3)));
 #pragma unroll
-                    for (int kd = 0; kd < NKD; kd++)
-                        kf[kd] = __builtin_bit_cast(
-                            bf16x8, *reinterpret_cast<const uint4*>(krow + (((hh * NKD + kd) ^ k_sw) << 3)));
-#pragma unroll
-                    for (int kd = 0; kd < NKD; kd++) s = mfma32(kf[kd], qf[kd], s);
-                }
-                float mx = -INFINITY;
-                if (kb0 + 31 > t_wave) {  // diagonal block: causal mask
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int key = kb0 + (r >> 2) * 8 + hh * 4 + (r & 3);
-                        if (key > tq) s[r] = -INFINITY;
-                    }
-                }
-#pragma unroll
-                for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[r]);
+                for (int kd = 0; kd < NKD; kd++) sc = mfma32(kf[kd], qf[kd], sc);
+                return sc;
+            };
+            // Move the running max to m (log2 units) when the block max exceeds
+            // it by more than kLazyRescale; rescale O and the row sum then.
+            auto update_max = [&](float mx) {
                 mx = fmaxf(mx, __shfl_xor(mx, 32)) * p.sl2;
-                // Keys 0..31 are unmasked for every row, so mx is finite on the
-                // first block and m2 from then on.
                 const float mnew = mx > m2 + kLazyRescale ? mx : m2;
                 if (__any(mnew != m2)) {
                     const float alpha = __builtin_amdgcn_exp2f(m2 - mnew);
@@ -372,22 +360,64 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     for (int i = 0; i < NDB; i++) oacc[i] *= alpha;
                     m2 = mnew;
                 }
+            };
+            // P^T = exp2(S^T * scale*log2e - m), then O^T += V^T P^T over the
+            // block's two 16-key halves (V^T read transposed from the V tile).
+            auto accumulate = [&](int kb, const f32x16& sc) {
                 float pr[16];
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], p.sl2, -m2));
+                    pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -m2));
                     lsum += pr[r];
                 }
                 const bf16x8 p0 = cvt_bf16x8(&pr[0]), p1 = cvt_bf16x8(&pr[8]);
-                // O^T += V^T P^T over the block's two 16-key halves.
 #pragma unroll
                 for (int db = 0; db < NDB; db++) {
-                    const int cofs = (((db * 4 + tr_cb) ^ tr_sw) << 3) + tr_in;
-                    const bf16_bits* v0 = Vs + (kb * 32 + tr_row) * DP + cofs;
-                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(v0), ds_read_tr16(v0 + 8 * DP));
-                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(v0 + 16 * DP), ds_read_tr16(v0 + 24 * DP));
+                    const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
+                    const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
+                    const bf16_bits* v0 = Vs + (kb * 32 + tr_row) * DP;
+                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(v0 + c0), ds_read_tr16(v0 + 8 * DP + c8));
+                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(v0 + 16 * DP + c0), ds_read_tr16(v0 + 24 * DP + c8));
                     oacc[db] = mfma32(a0, p0, oacc[db]);
                     oacc[db] = mfma32(a1, p1, oacc[db]);
+                }
+            };
+            if (k0 + BN - 1 <= t_wave) {
+                // Interior tile: every key precedes every query of the wave.
+                // All score blocks are issued first so the softmax of one block
+                // overlaps the matrix work of the others.
+                f32x16 sc[NKB];
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) sc[kb] = scores(kb);
+                float mx = -INFINITY;
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) mx = fmaxf(mx, sc[kb][r]);
+                update_max(mx);
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) accumulate(kb, sc[kb]);
+            } else {
+                // Diagonal tile: causal mask, blocks past the wave's last query skipped.
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) {
+                    const int kb0 = k0 + kb * 32;
+                    if (kb0 > wave_last) break;
+                    f32x16 sc = scores(kb);
+                    if (kb0 + 31 > t_wave) {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int key = kb0 + (r >> 2) * 8 + hh * 4 + (r & 3);
+                            if (key > tq) sc[r] = -INFINITY;
+                        }
+                    }
+                    float mx = -INFINITY;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) mx = fmaxf(mx, sc[r]);
+                    // Keys 0..31 are unmasked for every row, so mx is finite on
+                    // the first block and m2 from then on.
+                    update_max(mx);
+                    accumulate(kb, sc);
                 }
             }
         }

@@ -222,15 +222,27 @@ __device__ __forceinline__ void load_row_frag(T (&dst)[N], const T* __restrict__
 
 // ------------------------------------------------ swizzled bf16 LDS tiles
 // Fast-path tiles hold rows of DP bf16 (DP = 64 or 128) without padding; the
-// 16-byte chunk c of row r is stored at chunk position c ^ swz(r).  swz takes
-// eight distinct values over any eight consecutive rows (so the ds_read_b128
-// of eight rows at one chunk hits eight different bank groups) and maps four
-// consecutive rows starting at a multiple of 4 to {0,2,4,6} or {1,3,5,7} (so
-// a transposed read of 4 rows x 2 adjacent chunks touches 8 positions).
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// 16-byte chunk c of row r is stored at chunk position c ^ swz<DP>(r).  gfx950
+// LDS serves 256 bytes per clock over 64 four-byte banks, so the patterns
+// below are chosen to be conflict-free for 16 lanes at a time:
+//   - ds_read_b128 of one chunk column by 16 consecutive rows (MFMA operand
+//     rows) lands on 16 different 16-byte bank groups;
+//   - ds_read_b64_tr_b16 by lanes 0-31 (rows r0..r0+3, r0 % 4 == 0, chunks
+//     c0..c0+3, c0 % 4 == 0) lands on 16 different bank groups;
+//   - ds_write_b128 of whole rows is a permutation within each bank row.
+// DP = 128 (one row per bank row): swz = 4*(r%4) + (r/4)%4, period 16.
+// DP = 64 (two rows per bank row): swz = 4*((r/2)%2) + (r/4)%4, values 0..7,
+// distinct over the eight rows of each parity in 16 consecutive rows.
+template <int DP>
+__device__ __forceinline__ int swz(int r) {
+    if constexpr (DP == 128)
+        return ((r & 3) << 2) | ((r >> 2) & 3);
+    else
+        return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+}
 template <int DP>
 __device__ __forceinline__ int swz_off(int r, int c) {
-    return r * DP + ((c ^ swz(r)) << 3);
+    return r * DP + ((c ^ swz<DP>(r)) << 3);
 }
 
 // Hardware round-to-nearest-even pack of eight f32 values into an MFMA
