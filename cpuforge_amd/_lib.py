@@ -55,7 +55,7 @@ SIGNATURES = {
     "cfattn_prologue_fwd": (C.c_int, [_vp, Shape, _sz, C.c_int, C.POINTER(PrologueC)] + [_vp] * 7),
     "cfattn_prologue_bwd": (C.c_int, [_vp, Shape, _sz, C.POINTER(PrologueC)] + [_vp] * 11),
     "cfattn_fused_fwd": (C.c_int, [_vp, Shape, _sz, C.c_int, C.POINTER(PrologueC)] + [_vp] * 10),
-    "cfattn_fused_bwd": (C.c_int, [_vp, Shape, _sz, C.c_int, C.POINTER(PrologueC)] + [_vp] * 15),
+    "cfattn_fused_bwd": (C.c_int, [_vp, Shape, _sz, C.c_int, C.POINTER(PrologueC)] + [_vp] * 16),
     "cfattn_rope_table": (C.c_int, [_sz, _sz, C.c_double, C.POINTER(Llama3ScalingC), _vp, _vp]),
     "cfattn_llama3_scale": (C.c_double, [C.POINTER(Llama3ScalingC), C.c_double]),
     "cfattn_f32_to_bf16": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),

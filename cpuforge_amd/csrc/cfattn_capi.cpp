@@ -200,7 +200,10 @@ Dims dims_of(const cfattn_shape& s, size_t batch) {
     return Dims{(int)batch, (int)s.seq, (int)s.n_heads, (int)s.n_kv, (int)s.head_dim};
 }
 
-hipStream_t pick_stream(cfattn_ctx* c, void* st) { return st ? static_cast<hipStream_t>(st) : c->stream; }
+// Device entry points run on the caller's stream.  NULL is the device's null
+// (default) stream, as everywhere in HIP, so work queued by other libraries
+// on that stream (PyTorch's default stream, for one) stays ordered with ours.
+hipStream_t pick_stream(cfattn_ctx*, void* st) { return static_cast<hipStream_t>(st); }
 
 #define CF_TRY(expr)                 \
     do {                             \

@@ -82,9 +82,9 @@ enum {
 };
 
 /* ---- context ------------------------------------------------------------ */
-/* Creates a context on HIP device `device`: its own stream, a grow-only pool
- * of device buffers for the host-slice entry points, and scratch.  Calls on
- * one context are serialised by a lock. */
+/* Creates a context on HIP device `device`: its own stream (used by the
+ * host-slice entry points), a grow-only pool of device buffers for them, and
+ * scratch.  Calls on one context are serialised by a lock. */
 int cfattn_create(int device, cfattn_ctx** out);
 int cfattn_destroy(cfattn_ctx* ctx);
 /* Message of the last failed call on this context (empty if none). */
@@ -124,8 +124,9 @@ int cfattn_attention_backward_blocked(cfattn_ctx* ctx, const float* d_o, size_t 
 
 /* ---- device pointers, batched, caller's stream -------------------------- */
 /* Forward on device buffers.  q, k, v are f32 or bf16 (`dtype`); o and lse
- * are f32.  `stream` is a hipStream_t (NULL = the context's stream).
- * Asynchronous: returns after queuing the kernels. */
+ * are f32.  `stream` is a hipStream_t; NULL is the device's null (default)
+ * stream, as in every HIP API (pass cfattn_stream(ctx) for the context's own
+ * stream).  Asynchronous: returns after queuing the kernels. */
 int cfattn_fwd(cfattn_ctx* ctx, cfattn_shape s, size_t batch, int dtype, const void* q, const void* k,
                const void* v, float* o, float* lse, void* stream);
 /* Backward on device buffers; accumulates into the f32 dq, dk, dv.  Uses

@@ -35,8 +35,23 @@ def test_library_exports_every_declared_symbol():
     assert not missing, f"libcfattn.so lacks {missing}"
 
 
+def declared_arities():
+    """Parameter count of every function include/cfattn.h declares."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(cfattn_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
 def test_ctypes_table_matches_header():
     assert sorted(_lib.SIGNATURES) == declared_functions()
+    arity = declared_arities()
+    assert sorted(arity) == declared_functions()
+    # a missing trailing argument would make ctypes pass a 64-bit pointer as int
+    wrong = {n: (len(args), arity[n]) for n, (_, args) in _lib.SIGNATURES.items() if len(args) != arity[n]}
+    assert not wrong, f"ctypes argument counts differ from the header: {wrong}"
 
 
 def test_rope_table_matches_oracle_bitwise():
