@@ -590,7 +590,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                         float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lv[i]));
                         if (masked && kw > q0 + qi + i) pv = 0.0f;
                         pr[r] = pv;
-                        ds[r] = pv * (dp[r] - dv[i]) * p.scale;
+                        ds[r] = pv * (dp[r] - dv[i]);  // softmax scale applied to dK at the end
                     }
                 }
                 const bf16x8 p0 = cvt_bf16x8(&pr[0]), p1 = cvt_bf16x8(&pr[8]);
@@ -612,16 +612,75 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 }
             };
             if (q0 >= wg_key0 + p.kv_tile) {
-                // Interior step: every query of the tile follows every key of
-                // the workgroup, so the blocks need no mask and no branch and
-                // the scheduler can overlap one block's softmax with another
-                // block's matrix work.
+                // Interior step: every query of the tile follows every key of the
+                // workgroup (no mask, no branch).  Both blocks' S and dP are
+                // issued before the first softmax so the scheduler can overlap
+                // one block's softmax with the other block's matrix work.
+                static_assert(NQB == 2, "the interior step is written for two query blocks");
+                auto sdp = [&](int qb, f32x16& sc, f32x16& dp) {
+                    sc = zero16();
+                    dp = zero16();
+                    const bf16_bits* qrow = Qs + (qb * 32 + l32) * DP;
+                    const bf16_bits* orow = Os + (qb * 32 + l32) * DP;
 #pragma unroll
-                for (int qb = 0; qb < NQB; qb++) {
-                    f32x16 sc, dp;
-                    scores(qb, sc, dp);
-                    accumulate(qb, sc, dp, false);
-                }
+                    for (int kd = 0; kd < NKD; kd++) {
+                        const int co = ((hh * NKD + kd) ^ r_sw) << 3;
+                        const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + co));
+                        const bf16x8 c = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(orow + co));
+                        sc = mfma32(a, kf[kd], sc);
+                        dp = mfma32(c, vf[kd], dp);
+                    }
+                };
+                auto softmax = [&](int qb, const f32x16& sc, const f32x16& dp, bf16x8& pa, bf16x8& pb, bf16x8& da,
+                                   bf16x8& dbb) {
+                    float pr[16], ds[16];
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; g4++) {
+                        const int qi = qb * 32 + g4 * 8 + hh * 4;
+                        const float4 l4 = *reinterpret_cast<const float4*>(&Ls[qi]);
+                        const float4 d4 = *reinterpret_cast<const float4*>(&Ds[qi]);
+                        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const int r = g4 * 4 + i;
+                            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lv[i]));
+                            pr[r] = pv;
+                            ds[r] = pv * (dp[r] - dv[i]);
+                        }
+                    }
+                    pa = cvt_bf16x8(&pr[0]);
+                    pb = cvt_bf16x8(&pr[8]);
+                    da = cvt_bf16x8(&ds[0]);
+                    dbb = cvt_bf16x8(&ds[8]);
+                };
+                auto dvdk = [&](int qb, const bf16x8& pa, const bf16x8& pb, const bf16x8& da, const bf16x8& dbb) {
+#pragma unroll
+                    for (int db = 0; db < NDB; db++) {
+                        const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
+                        const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
+                        const bf16_bits* o0 = Os + (qb * 32 + tr_row) * DP;
+                        const bf16_bits* q0p = Qs + (qb * 32 + tr_row) * DP;
+                        const bf16x8 oa0 = join_bf16x4(ds_read_tr16(o0 + c0), ds_read_tr16(o0 + 8 * DP + c8));
+                        const bf16x8 oa1 =
+                            join_bf16x4(ds_read_tr16(o0 + 16 * DP + c0), ds_read_tr16(o0 + 24 * DP + c8));
+                        const bf16x8 qa0 = join_bf16x4(ds_read_tr16(q0p + c0), ds_read_tr16(q0p + 8 * DP + c8));
+                        const bf16x8 qa1 =
+                            join_bf16x4(ds_read_tr16(q0p + 16 * DP + c0), ds_read_tr16(q0p + 24 * DP + c8));
+                        dvt[db] = mfma32(oa0, pa, dvt[db]);
+                        dvt[db] = mfma32(oa1, pb, dvt[db]);
+                        dkt[db] = mfma32(qa0, da, dkt[db]);
+                        dkt[db] = mfma32(qa1, dbb, dkt[db]);
+                    }
+                };
+                f32x16 sc0, dp0, sc1, dp1;
+                bf16x8 pa0, pb0, da0, db0, pa1, pb1, da1, db1;
+                sdp(0, sc0, dp0);
+                sdp(1, sc1, dp1);
+                softmax(0, sc0, dp0, pa0, pb0, da0, db0);
+                dvdk(0, pa0, pb0, da0, db0);
+                softmax(1, sc1, dp1, pa1, pb1, da1, db1);
+                dvdk(1, pa1, pb1, da1, db1);
             } else {
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++) {
@@ -643,6 +702,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     float* dvrow = p.dv + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
 #pragma unroll
     for (int db = 0; db < NDB; db++) {
+        dkt[db] *= p.scale;  // dS was accumulated without the softmax scale
         add_row_block(dkrow, dkt[db], db * 32, hh, DP, true);
         add_row_block(dvrow, dvt[db], db * 32, hh, DP, true);
     }
