@@ -66,8 +66,12 @@ def parse():
     ap.add_argument("--mode", default=None, choices=["bf16", "f32"], help="default: bf16 (f32 for C1)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--cpu-heads", type=int, default=16, help="query heads of sequence 0 in the CPU sample")
+    ap.add_argument("--no-train", action="store_true", help="skip the SmolLM-135M train tok/s leg")
+    ap.add_argument("--train-steps", type=int, default=3)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB before timing (calibrates rocprofv3 byte counters)")
+    ap.add_argument("--host-slices", action="store_true",
+                    help="time the drop-in host-slice entry points instead (PCIe-inclusive; not the headline value)")
     ap.add_argument("--traffic-file", default=None,
                     help="rocprofv3 traffic summary to read `traffic` from (default: profiles/ match)")
     return ap.parse_args()
@@ -120,6 +124,44 @@ def read_traffic(path, kernel, workload_key):
     return None
 
 
+def host_slices(a, mode):
+    """Times cfattn_attention_forward + cfattn_attention_backward on host
+    float32 buffers (the reference's calling convention: every operand crosses
+    PCIe both ways on every call).  Prints its own JSON line."""
+    import numpy as np
+
+    import cpuforge_amd as cf
+    B, S, Hq, Hk, D = CONFIGS[a.config][:5]
+    rng = np.random.default_rng(5)
+    q, g = (rng.standard_normal(S * Hq * D, dtype=np.float32) for _ in range(2))
+    k, v = (rng.standard_normal(S * Hk * D, dtype=np.float32) for _ in range(2))
+    o = np.zeros_like(q)
+    lse = np.zeros(Hq * S, np.float32)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    ctx = cf.Context(0)
+    ctx.set_mode(mode)
+    s = cf.AttnShape(S, Hq, Hk, D)
+
+    def step():
+        for _ in range(B):  # the trainer's B sequential single-sequence calls
+            cf.attention_forward(q, k, v, o, lse, s, ctx)
+            cf.attention_backward(g, q, k, v, o, lse, dq, dk, dv, s, ctx)
+
+    for _ in range(a.warmup):
+        step()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    per = (time.perf_counter() - t0) / a.steps
+    flops = 7.0 * B * Hq * D * S * (S + 1)
+    ctx.close()
+    print(json.dumps({"metric": "attention fwd+bwd TFLOP/s through the host-slice drop-in (PCIe-inclusive)",
+                      "value": round(flops / per / 1e12, 3), "unit": "TFLOP/s", "ms_per_step": round(per * 1e3, 3),
+                      "steps": a.steps, "warmup": a.warmup, "dtype": mode, "higher_is_better": True,
+                      "config": {"workload": WORKLOAD[a.config], "config": a.config, "host_buffers": "numpy float32"}}),
+          flush=True)
+
+
 def main():
     a = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -129,6 +171,9 @@ def main():
         sys.exit(2)
     mode = a.mode or ("f32" if a.config == "C1" else "bf16")
     B, S, Hq, Hk, D, theta, scaling, qk_norm = CONFIGS[a.config]
+    if a.host_slices:
+        host_slices(a, mode)
+        return
 
     import torch
 
@@ -226,6 +271,15 @@ def main():
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 3), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic},
     }
+    del q, k, v, d_o, o, lse, dq, dk, dv
+    if not a.no_train:
+        # SmolLM-135M LoRA r=16 train step (cmd_bench.rs:52-99), seq 512, batch 8,
+        # f32 like the reference, attention through the fused GPU path.
+        from cpuforge_amd.train_bench import train_tok_s
+        print("bench: SmolLM-135M train step ...", file=sys.stderr, flush=True)
+        tr = train_tok_s(batch=8, seq=512, steps=a.train_steps)
+        tr["reference_tok_s"] = 122.0  # README.md:95, 2-core CPU, batch 1, same shape and LoRA
+        out["smollm_train"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in tr.items()}
     if not a.no_cpu:
         print("bench: cpu baseline ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(a.config, mode, a.cpu_heads)

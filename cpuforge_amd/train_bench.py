@@ -1,0 +1,133 @@
+"""SmolLM-135M-shaped LoRA training step with cpuforge's attention on the GPU.
+
+This is the measurement behind "SmolLM-135M train tok/s", the second half of
+the tier's metric. It follows the reference's `cpuforge bench-train`
+(crates/cli/src/cmd_bench.rs:43-99):
+
+- **Model.** A random-init SmolLM-135M shape (`smollm_135m_config`,
+  cmd_bench.rs:43-50):
+  - 30 layers, hidden 576, FFN 1536, 9 query / 3 KV heads of 64, vocab 49152;
+  - tied embeddings, RMSNorm eps 1e-5, RoPE theta 1e4.
+- **Init** (`Model::random`, crates/model/src/model.rs:282-305): weights
+  N(0, 0.02), norm gains 1.
+- **LoRA** (`Linear::add_lora`, crates/model/src/linear.rs:44-53):
+  - rank 16, alpha 32, on q, k, v, o, gate, up, down;
+  - A uniform in ±1/sqrt(in), B zero;
+  - only the adapters train (`TrainSpec::LORA_ONLY`).
+- **Timed step.** `grads.zero()` plus one `forward_backward` (cmd_bench.rs:78-87):
+  embeddings → 30 × Layer → final norm → tied LM head → mean cross-entropy,
+  then the backward. There is no optimizer step, as in the reference.
+- **Batch.** The reference runs one sequence per call; this harness runs
+  `batch` sequences in one device pass. tok/s = batch·seq / step time.
+
+The attention of every layer is `cpuforge_amd.layer.layer_attention`, the
+fused RoPE + attention kernels. The projections and the LM head are plain
+torch matmuls (rocBLAS/hipBLASLt), because only the attention op is the path
+this library replaces.
+"""
+from __future__ import annotations
+
+import time
+
+import torch
+import torch.nn.functional as F
+
+from .layer import LayerRope, layer_attention
+from .rope import RopeCache
+
+SMOLLM_135M = dict(vocab=49152, d=576, ffn=1536, heads=9, kv_heads=3, head_dim=64, eps=1e-5, theta=1e4)
+
+
+class LoRALinear:
+    """y = x Wᵀ + (alpha/r) (x Aᵀ) Bᵀ with W frozen (linear.rs:1-3, 56-69)."""
+
+    def __init__(self, out: int, inn: int, std: float, rank: int, alpha: float, gen, dtype, device):
+        self.w = (torch.randn(out, inn, generator=gen, device=device) * std).to(dtype)
+        bound = 1.0 / inn ** 0.5
+        self.a = ((torch.rand(rank, inn, generator=gen, device=device) * 2 - 1) * bound).to(dtype).requires_grad_()
+        self.b = torch.zeros(out, rank, device=device, dtype=dtype, requires_grad=True)
+        self.scale = alpha / rank
+
+    def __call__(self, x):
+        return x @ self.w.t() + (self.scale * (x @ self.a.t())) @ self.b.t()
+
+    def params(self):
+        return [self.a, self.b]
+
+
+def rmsnorm(x, w, eps):
+    return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * w
+
+
+class SmolLM:
+    def __init__(self, layers: int = 30, seq: int = 512, rank: int = 16, dtype=torch.float32, device="cuda",
+                 seed: int = 1, attn_dtype=None):
+        c = SMOLLM_135M
+        self.c, self.dtype, self.layers_n = c, dtype, layers
+        self.attn_dtype = attn_dtype or dtype
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
+        d, f, hd = c["d"], c["ffn"], c["head_dim"]
+        qd, kvd = c["heads"] * hd, c["kv_heads"] * hd
+        lin = lambda o, i: LoRALinear(o, i, 0.02, rank, 2.0 * rank, gen, dtype, device)  # noqa: E731
+        self.layers = [dict(attn_norm=torch.ones(d, device=device, dtype=dtype), wq=lin(qd, d), wk=lin(kvd, d),
+                            wv=lin(kvd, d), wo=lin(d, qd), mlp_norm=torch.ones(d, device=device, dtype=dtype),
+                            gate=lin(f, d), up=lin(f, d), down=lin(d, f)) for _ in range(layers)]
+        self.embed = (torch.randn(c["vocab"], d, generator=gen, device=device) * 0.02).to(dtype)
+        self.final_norm = torch.ones(d, device=device, dtype=dtype)
+        self.rope = LayerRope(RopeCache(hd, seq, c["theta"]), device)
+        self.attention = layer_attention  # (q_pre, k_pre, v, LayerRope) -> o
+
+    def params(self):
+        out = []
+        for layer in self.layers:
+            for name in ("wq", "wk", "wv", "wo", "gate", "up", "down"):
+                out += layer[name].params()
+        return out
+
+    def loss(self, tokens, targets):
+        c = self.c
+        B, S = tokens.shape
+        x = self.embed[tokens]
+        for layer in self.layers:
+            n1 = rmsnorm(x, layer["attn_norm"], c["eps"])
+            q = layer["wq"](n1).view(B, S, c["heads"], c["head_dim"])
+            k = layer["wk"](n1).view(B, S, c["kv_heads"], c["head_dim"])
+            v = layer["wv"](n1).view(B, S, c["kv_heads"], c["head_dim"])
+            o = self.attention(q.float(), k.float(), v.to(self.attn_dtype), self.rope)
+            x = x + layer["wo"](o.view(B, S, -1).to(self.dtype))
+            n2 = rmsnorm(x, layer["mlp_norm"], c["eps"])
+            x = x + layer["down"](F.silu(layer["gate"](n2)) * layer["up"](n2))
+        hn = rmsnorm(x, self.final_norm, c["eps"])
+        logits = hn @ self.embed.t()
+        return F.cross_entropy(logits.view(-1, c["vocab"]).float(), targets.view(-1))
+
+
+def train_tok_s(batch: int = 8, seq: int = 512, layers: int = 30, rank: int = 16, steps: int = 3,
+                dtype=torch.float32, attn_dtype=None, device="cuda") -> dict:
+    """Build the model, warm up one step, time `steps` forward+backward
+    passes; returns tok/s and the step time."""
+    model = SmolLM(layers, seq, rank, dtype, device, attn_dtype=attn_dtype)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(7)
+    tokens = torch.randint(0, model.c["vocab"], (batch, seq), generator=gen, device=device)
+    targets = torch.randint(0, model.c["vocab"], (batch, seq), generator=gen, device=device)
+    params = model.params()
+
+    def step():
+        for p_ in params:
+            p_.grad = None
+        loss = model.loss(tokens, targets)
+        loss.backward()
+        return loss
+
+    loss0 = step().item()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    per = (time.perf_counter() - t0) / steps
+    return {"value": batch * seq / per, "unit": "tok/s", "ms_per_step": per * 1e3, "batch": batch, "seq": seq,
+            "layers": layers, "lora_rank": rank, "dtype": str(dtype).replace("torch.", ""),
+            "attn_dtype": str(attn_dtype or dtype).replace("torch.", ""), "steps": steps, "first_loss": loss0}
