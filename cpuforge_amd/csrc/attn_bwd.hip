@@ -438,12 +438,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int NT = 256;
     constexpr int CPR = DP / 8;
     constexpr int TILE = BM * DP;
-    constexpr int LOADS = BM * CPR / NT;
-    static_assert(BM * CPR % NT == 0 && BM <= NT / 2, "tile must split evenly over the workgroup");
+    constexpr int RPC = 512 / DP;             // tile rows per 1 KiB wave load (64 lanes x 16 B)
+    constexpr int CPW = TILE / 512 / 4;       // 1 KiB loads per wave per tile
+    static_assert(TILE % 2048 == 0 && BM <= NT / 2, "tile must split evenly over the four waves");
     static_assert(BM % 32 == 0, "query tile must be whole 32-row blocks");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NQB = BM / 32;
-    __shared__ __attribute__((aligned(16))) bf16_bits sQ[2][TILE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sO[2][TILE];  // dO rows
+    // Two stages as separate arrays, so the compiler can tell the stage being
+    // read from the one the direct-to-LDS loads are filling.
+    __shared__ __attribute__((aligned(16))) bf16_bits sQ0[TILE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sQ1[TILE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sO0[TILE];  // dO rows
+    __shared__ __attribute__((aligned(16))) bf16_bits sO1[TILE];
     __shared__ __attribute__((aligned(16))) float sL[2][BM];        // lse * log2(e)
     __shared__ __attribute__((aligned(16))) float sD[2][BM];        // delta
 
@@ -491,45 +496,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int nq = n_qt - qt_begin;
     const int n_steps = p.group * nq;
 
-    uint4 pq[LOADS], po[LOADS];
     float pl = 0.0f;
-    // Step s covers query tile qt_begin + s % nq of query head s / nq.
-    auto gload = [&](int s) {
+    // Step s covers query tile qt_begin + s % nq of query head s / nq.  Its
+    // Q and dO rows go straight from global memory into the swizzled LDS tile
+    // (global_load_lds_dwordx4: lane l of a wave load writes the l-th 16 bytes
+    // of a 1 KiB block, so the swizzle is applied to the source addresses).
+    // Rows past the sequence read the last row instead; their lse is +inf, so
+    // P and dS are exactly zero there.
+    auto dma = [&](int s, bf16_bits* Qd, bf16_bits* Od) {
         const int h = g * p.group + s / nq;
         const int q0 = (qt_begin + s % nq) * BM;
 #pragma unroll
-        for (int i = 0; i < LOADS; i++) {
-            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
-            const int t = q0 + row;
-            if (t < p.seq) {
-                const long off = (long)t * qrs + (long)h * DP + col * 8;
-                pq[i] = *reinterpret_cast<const uint4*>(qg + off);
-                po[i] = *reinterpret_cast<const uint4*>(og + off);
-            } else {
-                pq[i] = make_uint4(0, 0, 0, 0);
-                po[i] = make_uint4(0, 0, 0, 0);
-            }
+        for (int i = 0; i < CPW; i++) {
+            const int blk = wave * CPW + i;
+            const int r = blk * RPC + lane / CPR;
+            const int c = (lane % CPR) ^ swz<DP>(r);
+            const long off = (long)min(q0 + r, p.seq - 1) * qrs + (long)h * DP + c * 8;
+            __builtin_amdgcn_global_load_lds(qg + off, Qd + blk * 512, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(og + off, Od + blk * 512, 16, 0, 0);
         }
+        // lse and delta of the tile's rows: a plain load whose value is not
+        // touched until store_ld, so no wait for it (vmcnt is in order and
+        // would also wait for the tile loads above) lands before the compute.
         if (tid < 2 * BM) {
-            const int t = q0 + (tid % BM);
+            const int t = min(q0 + (tid % BM), p.seq - 1);
             const long li = ((long)b * p.nh + h) * p.seq + t;
-            if (tid < BM)
-                pl = t < p.seq ? p.lse[li] * kLog2e : INFINITY;  // rows past the end: P = 0
-            else
-                pl = t < p.seq ? p.delta[li] : 0.0f;
+            pl = tid < BM ? p.lse[li] : p.delta[li];
         }
     };
-    auto lstore = [&](int st) {
-#pragma unroll
-        for (int i = 0; i < LOADS; i++) {
-            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
-            *reinterpret_cast<uint4*>(&sQ[st][swz_off<DP>(row, col)]) = pq[i];
-            *reinterpret_cast<uint4*>(&sO[st][swz_off<DP>(row, col)]) = po[i];
-        }
+    auto store_ld = [&](int s, int st) {
+        const int t = (qt_begin + s % nq) * BM + (tid % BM);
         if (tid < BM)
-            sL[st][tid] = pl;
+            sL[st][tid] = t < p.seq ? pl * kLog2e : INFINITY;  // rows past the end: P = 0
         else if (tid < 2 * BM)
-            sD[st][tid - BM] = pl;
+            sD[st][tid - BM] = t < p.seq ? pl : 0.0f;
     };
 
     f32x16 dkt[NDB], dvt[NDB];
@@ -539,17 +539,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         dvt[i] = zero16();
     }
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int s = 0; s < n_steps; s++) {
+    auto step = [&](int s, const bf16_bits* Qs, const bf16_bits* Os, bf16_bits* Qn, bf16_bits* On) {
         const int st = s & 1;
         const bool more = s + 1 < n_steps;
-        if (more) gload(s + 1);
+        if (more) dma(s + 1, Qn, On);
         const int q0 = (qt_begin + s % nq) * BM;
         if (wave_active && q0 + BM - 1 >= key0) {
-            const bf16_bits* Qs = sQ[st];
-            const bf16_bits* Os = sO[st];
             const float* Ls = sL[st];
             const float* Ds = sD[st];
             // S and dP for query block qb: rows = queries q0 + qb*32 + [0,32),
@@ -572,9 +567,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     dp = mfma32(oa[kd], vf[kd], dp);
                 }
             };
-            // P = exp2(S*scale*log2e - lse*log2e), dS = P (dP - delta) scale;
-            // dV^T += dO^T P and dK^T += Q^T dS with dO^T and Q^T read
-            // transposed from the row-major tiles.
+            // P = exp2(S*scale*log2e - lse*log2e), dS = P (dP - delta) (the
+            // softmax scale is applied to dK once, at the end); dV^T += dO^T P
+            // and dK^T += Q^T dS with dO^T and Q^T read transposed from the
+            // row-major tiles.
             auto accumulate = [&](int qb, const f32x16& sc, const f32x16& dp, bool masked) {
                 float pr[16], ds[16];
 #pragma unroll
@@ -693,8 +689,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 }
             }
         }
-        if (more) lstore(st ^ 1);
+        if (more) store_ld(s + 1, st ^ 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for step s + 1 have landed
         __syncthreads();
+    };
+
+    dma(0, sQ0, sO0);
+    store_ld(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int s = 0; s < n_steps; s += 2) {
+        step(s, sQ0, sO0, sQ1, sO1);
+        if (s + 1 < n_steps) step(s + 1, sQ1, sO1, sQ0, sO0);
     }
 
     if (!wave_active || kw >= p.seq) return;
