@@ -609,10 +609,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             };
             if (q0 >= wg_key0 + p.kv_tile) {
                 // Interior step: every query of the tile follows every key of the
-                // workgroup (no mask, no branch).  Both blocks' S and dP are
-                // issued before the first softmax so the scheduler can overlap
-                // one block's softmax with the other block's matrix work.
-                static_assert(NQB == 2, "the interior step is written for two query blocks");
+                // workgroup (no mask, no branch).  Query blocks go in pairs, both
+                // blocks' S and dP issued before the first softmax so the
+                // scheduler can overlap one block's softmax with the other
+                // block's matrix work.
+                static_assert(NQB % 2 == 0, "the interior step takes query blocks in pairs");
                 auto sdp = [&](int qb, f32x16& sc, f32x16& dp) {
                     sc = zero16();
                     dp = zero16();
@@ -669,14 +670,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                         dkt[db] = mfma32(qa1, dbb, dkt[db]);
                     }
                 };
-                f32x16 sc0, dp0, sc1, dp1;
-                bf16x8 pa0, pb0, da0, db0, pa1, pb1, da1, db1;
-                sdp(0, sc0, dp0);
-                sdp(1, sc1, dp1);
-                softmax(0, sc0, dp0, pa0, pb0, da0, db0);
-                dvdk(0, pa0, pb0, da0, db0);
-                softmax(1, sc1, dp1, pa1, pb1, da1, db1);
-                dvdk(1, pa1, pb1, da1, db1);
+#pragma unroll
+                for (int qb = 0; qb < NQB; qb += 2) {
+                    f32x16 sc0, dp0, sc1, dp1;
+                    bf16x8 pa0, pb0, da0, db0, pa1, pb1, da1, db1;
+                    sdp(qb, sc0, dp0);
+                    sdp(qb + 1, sc1, dp1);
+                    softmax(qb, sc0, dp0, pa0, pb0, da0, db0);
+                    dvdk(qb, pa0, pb0, da0, db0);
+                    softmax(qb + 1, sc1, dp1, pa1, pb1, da1, db1);
+                    dvdk(qb + 1, pa1, pb1, da1, db1);
+                    // Pairs stay apart: hoisting the next pair's loads would
+                    // run out of registers.
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             } else {
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++) {
@@ -868,6 +875,224 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int db = 0; db < NDB; db++) add_row_block(dqrow, dqt[db], db * 32, hh, DP, true);
 }
 
+// dK/dV with two specialised waves per 32-key slice: eight waves, 128 keys per
+// workgroup, the same (key tile, KV head, sequence) grid and step order as
+// attn_bwd_dkdv_bf16_kernel.
+//   P waves (0-3) hold K^T and the dV^T accumulators: S = Q K^T,
+//     P = exp2(S*scale*log2e - lse*log2e) (causally masked), P to LDS in f32,
+//     then dV^T += dO^T P.
+//   dS waves (4-7) hold V^T and the dK^T accumulators: dP = dO V^T, then with
+//     P from LDS dS = P (dP - delta) and dK^T += Q^T dS.
+// Wave w and wave w + 4 work on the same keys and share a SIMD, so the
+// softmax of one runs while the other issues matrix work, and each needs half
+// the registers of a wave doing both.  Two barriers per step: P is written
+// before the first and read after it.
+template <int DP, int BM>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dkdv_ws_kernel(
+    const BwdParams p) {
+    constexpr int NT = 512;
+    constexpr int CPR = DP / 8;
+    constexpr int TILE = BM * DP;
+    constexpr int RPC = 512 / DP;        // tile rows per 1 KiB wave load
+    constexpr int CPW = TILE / 512 / 8;  // 1 KiB loads per wave per tile
+    static_assert(TILE % 4096 == 0 && 2 * BM <= NT, "tile must split evenly over the eight waves");
+    static_assert(BM % 32 == 0, "query tile must be whole 32-row blocks");
+    constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NQB = BM / 32;
+    __shared__ __attribute__((aligned(16))) bf16_bits sQ0[TILE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sQ1[TILE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sO0[TILE];  // dO rows
+    __shared__ __attribute__((aligned(16))) bf16_bits sO1[TILE];
+    __shared__ __attribute__((aligned(16))) float sL[2][BM];  // lse * log2(e)
+    __shared__ __attribute__((aligned(16))) float sD[2][BM];  // delta
+    // P of each (key slice, query block): lane l's four values of row group g4.
+    __shared__ float4 sP[4][NQB][4][64];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int slice = wave & 3;
+    const bool pwave = wave < 4;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
+    const int kvt = id % p.n_kvtiles;  // low key tiles see the most queries: first
+    const int rest = id / p.n_kvtiles;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+    const int wg_key0 = kvt * p.kv_tile;
+    const int key0 = wg_key0 + slice * 32;
+    const int kw = key0 + l32;
+    const bool wave_active = key0 < p.seq;
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const bf16_bits* qg = static_cast<const bf16_bits*>(p.q) + (long)b * p.q_bs;
+    const bf16_bits* og = static_cast<const bf16_bits*>(p.d_o) + (long)b * p.q_bs;
+
+    // K^T (P waves) or V^T (dS waves) operand: key kw, head dims hh*HALF + kd*8 + [0, 8).
+    bf16x8 xf[NKD];
+    {
+        const long off = (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP + hh * HALF;
+        const bf16_bits* xr = static_cast<const bf16_bits*>(pwave ? p.k : p.v) + off;
+        const bool ok = kw < p.seq;
+#pragma unroll
+        for (int kd = 0; kd < NKD; kd++)
+            xf[kd] = __builtin_bit_cast(bf16x8, ok ? *reinterpret_cast<const uint4*>(xr + kd * 8) : make_uint4(0, 0, 0, 0));
+    }
+
+    const int G = lane >> 4, jj = lane & 15;
+    const int tr_row = 4 * (G >> 1) + (jj >> 2);
+    const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
+    const int tr_in = 4 * (jj & 1);
+    const int tr_sw0 = swz<DP>(tr_row), tr_sw8 = swz<DP>(tr_row + 8);
+    const int r_sw = swz<DP>(l32);
+
+    const int n_qt = (p.seq + BM - 1) / BM;
+    const int qt_begin = wg_key0 / BM;
+    const int nq = n_qt - qt_begin;
+    const int n_steps = p.group * nq;
+
+    float pl = 0.0f;
+    // Step s covers query tile qt_begin + s % nq of query head s / nq; its Q
+    // and dO rows go straight into the swizzled LDS tile (see the four-wave
+    // kernel above for the addressing and the past-the-end rows).
+    auto dma = [&](int s, bf16_bits* Qd, bf16_bits* Od) {
+        const int h = g * p.group + s / nq;
+        const int q0 = (qt_begin + s % nq) * BM;
+#pragma unroll
+        for (int i = 0; i < CPW; i++) {
+            const int blk = wave * CPW + i;
+            const int r = blk * RPC + lane / CPR;
+            const int c = (lane % CPR) ^ swz<DP>(r);
+            const long off = (long)min(q0 + r, p.seq - 1) * qrs + (long)h * DP + c * 8;
+            __builtin_amdgcn_global_load_lds(qg + off, Qd + blk * 512, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(og + off, Od + blk * 512, 16, 0, 0);
+        }
+        if (tid < 2 * BM) {
+            const int t = min(q0 + (tid % BM), p.seq - 1);
+            const long li = ((long)b * p.nh + h) * p.seq + t;
+            pl = tid < BM ? p.lse[li] : p.delta[li];
+        }
+    };
+    auto store_ld = [&](int s, int st) {
+        const int t = (qt_begin + s % nq) * BM + (tid % BM);
+        if (tid < BM)
+            sL[st][tid] = t < p.seq ? pl * kLog2e : INFINITY;  // rows past the end: P = 0
+        else if (tid < 2 * BM)
+            sD[st][tid - BM] = t < p.seq ? pl : 0.0f;
+    };
+
+    f32x16 acc[NDB];  // dV^T (P waves) or dK^T (dS waves)
+#pragma unroll
+    for (int i = 0; i < NDB; i++) acc[i] = zero16();
+
+    auto step = [&](int s, const bf16_bits* Qs, const bf16_bits* Os, bf16_bits* Qn, bf16_bits* On) {
+        const int st = s & 1;
+        const bool more = s + 1 < n_steps;
+        if (more) dma(s + 1, Qn, On);
+        const int q0 = (qt_begin + s % nq) * BM;
+        const bool act = wave_active && q0 + BM - 1 >= key0;
+        const float* Ls = sL[st];
+        const float* Ds = sD[st];
+        bf16x8 pbf[NQB][2];  // P waves: P of each block as MFMA operands
+        f32x16 dpv[NQB];     // dS waves: dP of each block
+        // Phase 1: S -> P (P waves) and dP (dS waves).
+        if (act) {
+#pragma unroll
+            for (int qb = 0; qb < NQB; qb++) {
+                const int tq0 = q0 + qb * 32;
+                if (tq0 >= p.seq || tq0 + 31 < key0) continue;
+                const bf16_bits* arow = (pwave ? Qs : Os) + (qb * 32 + l32) * DP;
+                f32x16 sc = zero16();
+#pragma unroll
+                for (int kd = 0; kd < NKD; kd++) {
+                    const bf16x8 a = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const uint4*>(arow + (((hh * NKD + kd) ^ r_sw) << 3)));
+                    sc = mfma32(a, xf[kd], sc);
+                }
+                if (pwave) {
+                    const bool masked = tq0 < key0 + 31;
+                    float pr[16];
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; g4++) {
+                        const int qi = qb * 32 + g4 * 8 + hh * 4;
+                        const float4 l4 = *reinterpret_cast<const float4*>(&Ls[qi]);
+                        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[g4 * 4 + i], p.sl2, -lv[i]));
+                            if (masked && kw > q0 + qi + i) pv = 0.0f;
+                            pr[g4 * 4 + i] = pv;
+                        }
+                        sP[slice][qb][g4][lane] = make_float4(pr[g4 * 4], pr[g4 * 4 + 1], pr[g4 * 4 + 2], pr[g4 * 4 + 3]);
+                    }
+                    pbf[qb][0] = cvt_bf16x8(&pr[0]);
+                    pbf[qb][1] = cvt_bf16x8(&pr[8]);
+                } else {
+                    dpv[qb] = sc;
+                }
+            }
+        }
+        __syncthreads();
+        // Phase 2: dV^T += dO^T P (P waves), dS -> dK^T += Q^T dS (dS waves).
+        if (act) {
+#pragma unroll
+            for (int qb = 0; qb < NQB; qb++) {
+                const int tq0 = q0 + qb * 32;
+                if (tq0 >= p.seq || tq0 + 31 < key0) continue;
+                bf16x8 b0, b1;
+                if (pwave) {
+                    b0 = pbf[qb][0];
+                    b1 = pbf[qb][1];
+                } else {
+                    float ds[16];
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; g4++) {
+                        const int qi = qb * 32 + g4 * 8 + hh * 4;
+                        const float4 d4 = *reinterpret_cast<const float4*>(&Ds[qi]);
+                        const float4 p4 = sP[slice][qb][g4][lane];
+                        ds[g4 * 4 + 0] = p4.x * (dpv[qb][g4 * 4 + 0] - d4.x);
+                        ds[g4 * 4 + 1] = p4.y * (dpv[qb][g4 * 4 + 1] - d4.y);
+                        ds[g4 * 4 + 2] = p4.z * (dpv[qb][g4 * 4 + 2] - d4.z);
+                        ds[g4 * 4 + 3] = p4.w * (dpv[qb][g4 * 4 + 3] - d4.w);
+                    }
+                    b0 = cvt_bf16x8(&ds[0]);
+                    b1 = cvt_bf16x8(&ds[8]);
+                }
+                // dO^T (P waves) or Q^T (dS waves), read transposed from the tile.
+                const bf16_bits* t0 = (pwave ? Os : Qs) + (qb * 32 + tr_row) * DP;
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
+                    const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
+                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(t0 + c0), ds_read_tr16(t0 + 8 * DP + c8));
+                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(t0 + 16 * DP + c0), ds_read_tr16(t0 + 24 * DP + c8));
+                    acc[db] = mfma32(a0, b0, acc[db]);
+                    acc[db] = mfma32(a1, b1, acc[db]);
+                }
+            }
+        }
+        if (more) store_ld(s + 1, st ^ 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for step s + 1 have landed
+        __syncthreads();
+    };
+
+    dma(0, sQ0, sO0);
+    store_ld(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int s = 0; s < n_steps; s += 2) {
+        step(s, sQ0, sO0, sQ1, sO1);
+        if (s + 1 < n_steps) step(s + 1, sQ1, sO1, sQ0, sO0);
+    }
+
+    if (!wave_active || kw >= p.seq) return;
+    float* row = (pwave ? p.dv : p.dk) + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
+#pragma unroll
+    for (int db = 0; db < NDB; db++) {
+        if (!pwave) acc[db] *= p.scale;  // dS was accumulated without the softmax scale
+        add_row_block(row, acc[db], db * 32, hh, DP, true);
+    }
+}
+
 static int pick_hpw_b(int group, int cap) {
     for (int h = cap < group ? cap : group; h >= 1; h--)
         if (group % h == 0) return h;
@@ -961,9 +1186,9 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
         {
             TimedLaunch tl(tu.timer, kKernBwdDkdv, st);
             if (d.hd == 128)
-                hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<128, 64>), dim3(p.n_wg_kv), dim3(256), 0, st, p);
+                hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
             else
-                hipLaunchKernelGGL((attn_bwd_dkdv_bf16_kernel<64, 64>), dim3(p.n_wg_kv), dim3(256), 0, st, p);
+                hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<64, 64>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
             e = hipGetLastError();
         }
         if (e != hipSuccess) return e;
