@@ -987,7 +987,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     auto step = [&](int s, const bf16_bits* Qs, const bf16_bits* Os, bf16_bits* Qn, bf16_bits* On) {
         const int st = s & 1;
         const bool more = s + 1 < n_steps;
-        if (more) dma(s + 1, Qn, On);
         const int q0 = (qt_begin + s % nq) * BM;
         const bool act = wave_active && q0 + BM - 1 >= key0;
         const float* Ls = sL[st];
@@ -1000,14 +999,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int qb = 0; qb < NQB; qb++) {
                 const int tq0 = q0 + qb * 32;
                 if (tq0 >= p.seq || tq0 + 31 < key0) continue;
-                const bf16_bits* arow = (pwave ? Qs : Os) + (qb * 32 + l32) * DP;
-                f32x16 sc = zero16();
+                // Each role reads its own tile through its own pointer: a
+                // pointer chosen by a select hides which LDS array is read, and
+                // the compiler then waits for the next step's loads first.
+                auto rows_mfma = [&](const bf16_bits* tile) {
+                    const bf16_bits* arow = tile + (qb * 32 + l32) * DP;
+                    f32x16 acc_ = zero16();
 #pragma unroll
-                for (int kd = 0; kd < NKD; kd++) {
-                    const bf16x8 a = __builtin_bit_cast(
-                        bf16x8, *reinterpret_cast<const uint4*>(arow + (((hh * NKD + kd) ^ r_sw) << 3)));
-                    sc = mfma32(a, xf[kd], sc);
-                }
+                    for (int kd = 0; kd < NKD; kd++) {
+                        const bf16x8 a = __builtin_bit_cast(
+                            bf16x8, *reinterpret_cast<const uint4*>(arow + (((hh * NKD + kd) ^ r_sw) << 3)));
+                        acc_ = mfma32(a, xf[kd], acc_);
+                    }
+                    return acc_;
+                };
+                const f32x16 sc = pwave ? rows_mfma(Qs) : rows_mfma(Os);
                 if (pwave) {
                     const bool masked = tq0 < key0 + 31;
                     float pr[16];
@@ -1031,7 +1037,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 }
             }
         }
-        __syncthreads();
+        // The next step's loads start after the P stores (the compiler cannot
+        // tell those stores from the loads' LDS destination and would wait for
+        // the loads), and overlap phase 2.  P is published with this wave's LDS
+        // writes done and a plain barrier: __syncthreads() would also wait for
+        // the loads.
+        if (more) dma(s + 1, Qn, On);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
         // Phase 2: dV^T += dO^T P (P waves), dS -> dK^T += Q^T dS (dS waves).
         if (act) {
 #pragma unroll
@@ -1058,16 +1072,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     b1 = cvt_bf16x8(&ds[8]);
                 }
                 // dO^T (P waves) or Q^T (dS waves), read transposed from the tile.
-                const bf16_bits* t0 = (pwave ? Os : Qs) + (qb * 32 + tr_row) * DP;
+                auto tr_mfma = [&](const bf16_bits* tile) {
+                    const bf16_bits* t0 = tile + (qb * 32 + tr_row) * DP;
 #pragma unroll
-                for (int db = 0; db < NDB; db++) {
-                    const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
-                    const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
-                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(t0 + c0), ds_read_tr16(t0 + 8 * DP + c8));
-                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(t0 + 16 * DP + c0), ds_read_tr16(t0 + 24 * DP + c8));
-                    acc[db] = mfma32(a0, b0, acc[db]);
-                    acc[db] = mfma32(a1, b1, acc[db]);
-                }
+                    for (int db = 0; db < NDB; db++) {
+                        const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
+                        const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
+                        const bf16x8 a0 = join_bf16x4(ds_read_tr16(t0 + c0), ds_read_tr16(t0 + 8 * DP + c8));
+                        const bf16x8 a1 =
+                            join_bf16x4(ds_read_tr16(t0 + 16 * DP + c0), ds_read_tr16(t0 + 24 * DP + c8));
+                        acc[db] = mfma32(a0, b0, acc[db]);
+                        acc[db] = mfma32(a1, b1, acc[db]);
+                    }
+                };
+                if (pwave)
+                    tr_mfma(Os);
+                else
+                    tr_mfma(Qs);
             }
         }
         if (more) store_ld(s + 1, st ^ 1);
