@@ -927,17 +927,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const bf16_bits* qg = static_cast<const bf16_bits*>(p.q) + (long)b * p.q_bs;
     const bf16_bits* og = static_cast<const bf16_bits*>(p.d_o) + (long)b * p.q_bs;
 
-    // K^T (P waves) or V^T (dS waves) operand: key kw, head dims hh*HALF + kd*8 + [0, 8).
-    bf16x8 xf[NKD];
-    {
-        const long off = (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP + hh * HALF;
-        const bf16_bits* xr = static_cast<const bf16_bits*>(pwave ? p.k : p.v) + off;
-        const bool ok = kw < p.seq;
-#pragma unroll
-        for (int kd = 0; kd < NKD; kd++)
-            xf[kd] = __builtin_bit_cast(bf16x8, ok ? *reinterpret_cast<const uint4*>(xr + kd * 8) : make_uint4(0, 0, 0, 0));
-    }
-
     const int G = lane >> 4, jj = lane & 15;
     const int tr_row = 4 * (G >> 1) + (jj >> 2);
     const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
@@ -980,80 +969,110 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             sD[st][tid - BM] = t < p.seq ? pl : 0.0f;
     };
 
-    f32x16 acc[NDB];  // dV^T (P waves) or dK^T (dS waves)
+    // Each role runs its own copy of the step loop: the registers one role
+    // needs are then not held live across the other role's code.  Both
+    // copies pass the same barriers in the same order.
+    auto run = [&](auto role) {
+        constexpr bool PW = decltype(role)::value;
+        // K^T (P waves) or V^T (dS waves) operand: key kw, head dims hh*HALF + kd*8 + [0, 8).
+        bf16x8 xf[NKD];
+        {
+            const long off = (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP + hh * HALF;
+            const bf16_bits* xr = static_cast<const bf16_bits*>(PW ? p.k : p.v) + off;
+            const bool ok = kw < p.seq;
 #pragma unroll
-    for (int i = 0; i < NDB; i++) acc[i] = zero16();
+            for (int kd = 0; kd < NKD; kd++)
+                xf[kd] = __builtin_bit_cast(bf16x8,
+                                            ok ? *reinterpret_cast<const uint4*>(xr + kd * 8) : make_uint4(0, 0, 0, 0));
+        }
+        f32x16 acc[NDB];  // dV^T (P waves) or dK^T (dS waves)
+#pragma unroll
+        for (int i = 0; i < NDB; i++) acc[i] = zero16();
 
-    auto step = [&](int s, const bf16_bits* Qs, const bf16_bits* Os, bf16_bits* Qn, bf16_bits* On) {
-        const int st = s & 1;
-        const bool more = s + 1 < n_steps;
-        const int q0 = (qt_begin + s % nq) * BM;
-        const bool act = wave_active && q0 + BM - 1 >= key0;
-        const float* Ls = sL[st];
-        const float* Ds = sD[st];
-        bf16x8 pbf[NQB][2];  // P waves: P of each block as MFMA operands
-        f32x16 dpv[NQB];     // dS waves: dP of each block
-        // Phase 1: S -> P (P waves) and dP (dS waves).
-        if (act) {
+        auto step = [&](int s, const bf16_bits* Qs, const bf16_bits* Os, bf16_bits* Qn, bf16_bits* On) {
+            const int st = s & 1;
+            const bool more = s + 1 < n_steps;
+            const int q0 = (qt_begin + s % nq) * BM;
+            const bool act = wave_active && q0 + BM - 1 >= key0;
+            // Every query of the step is past every key of the slice: no mask
+            // and no per-block tests.
+            const bool full = wave_active && q0 >= key0 + 31 && q0 + BM <= p.seq;
+            const float* Ls = sL[st];
+            const float* Ds = sD[st];
+            // Phase-1 rows (Q for P waves, dO for dS waves) and the phase-2
+            // transposed tile (dO^T, Q^T); the role is a compile-time constant,
+            // so each names its LDS array directly.
+            const bf16_bits* A1 = PW ? Qs : Os;
+            const bf16_bits* A2 = PW ? Os : Qs;
+            bf16x8 pbf[NQB][2];  // P waves: P of each block as MFMA operands
+            f32x16 dpv[NQB];     // dS waves: dP of each block
+            auto row_read = [&](int qb, int kd) {
+                return __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const uint4*>(A1 + (qb * 32 + l32) * DP + (((hh * NKD + kd) ^ r_sw) << 3)));
+            };
+            // P waves: P = exp2(S*scale*log2e - lse*log2e), causally masked,
+            // to LDS in f32 for the dS waves and to registers as bf16 operands.
+            auto p_block = [&](int qb, const f32x16& sc, bool masked) {
+                float pr[16];
 #pragma unroll
-            for (int qb = 0; qb < NQB; qb++) {
-                const int tq0 = q0 + qb * 32;
-                if (tq0 >= p.seq || tq0 + 31 < key0) continue;
-                // Each role reads its own tile through its own pointer: a
-                // pointer chosen by a select hides which LDS array is read, and
-                // the compiler then waits for the next step's loads first.
-                auto rows_mfma = [&](const bf16_bits* tile) {
-                    const bf16_bits* arow = tile + (qb * 32 + l32) * DP;
-                    f32x16 acc_ = zero16();
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const int qi = qb * 32 + g4 * 8 + hh * 4;
+                    const float4 l4 = *reinterpret_cast<const float4*>(&Ls[qi]);
+                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
-                    for (int kd = 0; kd < NKD; kd++) {
-                        const bf16x8 a = __builtin_bit_cast(
-                            bf16x8, *reinterpret_cast<const uint4*>(arow + (((hh * NKD + kd) ^ r_sw) << 3)));
-                        acc_ = mfma32(a, xf[kd], acc_);
+                    for (int i = 0; i < 4; i++) {
+                        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[g4 * 4 + i], p.sl2, -lv[i]));
+                        if (masked && kw > q0 + qi + i) pv = 0.0f;
+                        pr[g4 * 4 + i] = pv;
                     }
-                    return acc_;
-                };
-                const f32x16 sc = pwave ? rows_mfma(Qs) : rows_mfma(Os);
-                if (pwave) {
-                    const bool masked = tq0 < key0 + 31;
-                    float pr[16];
+                    sP[slice][qb][g4][lane] = make_float4(pr[g4 * 4], pr[g4 * 4 + 1], pr[g4 * 4 + 2], pr[g4 * 4 + 3]);
+                }
+                pbf[qb][0] = cvt_bf16x8(&pr[0]);
+                pbf[qb][1] = cvt_bf16x8(&pr[8]);
+            };
+            // Phase 1: S -> P (P waves) and dP (dS waves).
+            if (full) {
+                f32x16 sc[NQB];
 #pragma unroll
-                    for (int g4 = 0; g4 < 4; g4++) {
-                        const int qi = qb * 32 + g4 * 8 + hh * 4;
-                        const float4 l4 = *reinterpret_cast<const float4*>(&Ls[qi]);
-                        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                for (int qb = 0; qb < NQB; qb++) sc[qb] = zero16();
 #pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[g4 * 4 + i], p.sl2, -lv[i]));
-                            if (masked && kw > q0 + qi + i) pv = 0.0f;
-                            pr[g4 * 4 + i] = pv;
-                        }
-                        sP[slice][qb][g4][lane] = make_float4(pr[g4 * 4], pr[g4 * 4 + 1], pr[g4 * 4 + 2], pr[g4 * 4 + 3]);
-                    }
-                    pbf[qb][0] = cvt_bf16x8(&pr[0]);
-                    pbf[qb][1] = cvt_bf16x8(&pr[8]);
-                } else {
-                    dpv[qb] = sc;
+                for (int kd = 0; kd < NKD; kd++)
+#pragma unroll
+                    for (int qb = 0; qb < NQB; qb++) sc[qb] = mfma32(row_read(qb, kd), xf[kd], sc[qb]);
+#pragma unroll
+                for (int qb = 0; qb < NQB; qb++) {
+                    if constexpr (PW)
+                        p_block(qb, sc[qb], false);
+                    else
+                        dpv[qb] = sc[qb];
+                }
+            } else if (act) {
+#pragma unroll
+                for (int qb = 0; qb < NQB; qb++) {
+                    const int tq0 = q0 + qb * 32;
+                    if (tq0 >= p.seq || tq0 + 31 < key0) continue;
+                    f32x16 sc = zero16();
+#pragma unroll
+                    for (int kd = 0; kd < NKD; kd++) sc = mfma32(row_read(qb, kd), xf[kd], sc);
+                    if constexpr (PW)
+                        p_block(qb, sc, tq0 < key0 + 31);
+                    else
+                        dpv[qb] = sc;
                 }
             }
-        }
-        // The next step's loads start after the P stores (the compiler cannot
-        // tell those stores from the loads' LDS destination and would wait for
-        // the loads), and overlap phase 2.  P is published with this wave's LDS
-        // writes done and a plain barrier: __syncthreads() would also wait for
-        // the loads.
-        if (more) dma(s + 1, Qn, On);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        // Phase 2: dV^T += dO^T P (P waves), dS -> dK^T += Q^T dS (dS waves).
-        if (act) {
-#pragma unroll
-            for (int qb = 0; qb < NQB; qb++) {
-                const int tq0 = q0 + qb * 32;
-                if (tq0 >= p.seq || tq0 + 31 < key0) continue;
+            // The next step's loads start after the P stores (the compiler cannot
+            // tell those stores from the loads' LDS destination and would wait for
+            // the loads), and overlap phase 2.  P is published with this wave's
+            // LDS writes done and a plain barrier: __syncthreads() would also
+            // wait for the loads.
+            if (more) dma(s + 1, Qn, On);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            // Phase 2: dV^T += dO^T P (P waves), dS -> dK^T += Q^T dS (dS waves).
+            auto phase2 = [&](int qb) {
                 bf16x8 b0, b1;
-                if (pwave) {
+                if constexpr (PW) {
                     b0 = pbf[qb][0];
                     b1 = pbf[qb][1];
                 } else {
@@ -1072,46 +1091,55 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     b1 = cvt_bf16x8(&ds[8]);
                 }
                 // dO^T (P waves) or Q^T (dS waves), read transposed from the tile.
-                auto tr_mfma = [&](const bf16_bits* tile) {
-                    const bf16_bits* t0 = tile + (qb * 32 + tr_row) * DP;
+                const bf16_bits* t0 = A2 + (qb * 32 + tr_row) * DP;
 #pragma unroll
-                    for (int db = 0; db < NDB; db++) {
-                        const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
-                        const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
-                        const bf16x8 a0 = join_bf16x4(ds_read_tr16(t0 + c0), ds_read_tr16(t0 + 8 * DP + c8));
-                        const bf16x8 a1 =
-                            join_bf16x4(ds_read_tr16(t0 + 16 * DP + c0), ds_read_tr16(t0 + 24 * DP + c8));
-                        acc[db] = mfma32(a0, b0, acc[db]);
-                        acc[db] = mfma32(a1, b1, acc[db]);
-                    }
-                };
-                if (pwave)
-                    tr_mfma(Os);
-                else
-                    tr_mfma(Qs);
+                for (int db = 0; db < NDB; db++) {
+                    const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
+                    const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
+                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(t0 + c0), ds_read_tr16(t0 + 8 * DP + c8));
+                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(t0 + 16 * DP + c0), ds_read_tr16(t0 + 24 * DP + c8));
+                    acc[db] = mfma32(a0, b0, acc[db]);
+                    acc[db] = mfma32(a1, b1, acc[db]);
+                }
+            };
+            if (full) {
+#pragma unroll
+                for (int qb = 0; qb < NQB; qb++) phase2(qb);
+            } else if (act) {
+#pragma unroll
+                for (int qb = 0; qb < NQB; qb++) {
+                    const int tq0 = q0 + qb * 32;
+                    if (tq0 >= p.seq || tq0 + 31 < key0) continue;
+                    phase2(qb);
+                }
             }
+            if (more) store_ld(s + 1, st ^ 1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for step s + 1 have landed
+            __syncthreads();
+        };
+
+        for (int s = 0; s < n_steps; s += 2) {
+            step(s, sQ0, sO0, sQ1, sO1);
+            if (s + 1 < n_steps) step(s + 1, sQ1, sO1, sQ0, sO0);
         }
-        if (more) store_ld(s + 1, st ^ 1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for step s + 1 have landed
-        __syncthreads();
+
+        if (!wave_active || kw >= p.seq) return;
+        float* row = (PW ? p.dv : p.dk) + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
+#pragma unroll
+        for (int db = 0; db < NDB; db++) {
+            if constexpr (!PW) acc[db] *= p.scale;  // dS was accumulated without the softmax scale
+            add_row_block(row, acc[db], db * 32, hh, DP, true);
+        }
     };
 
     dma(0, sQ0, sO0);
     store_ld(0, 0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    for (int s = 0; s < n_steps; s += 2) {
-        step(s, sQ0, sO0, sQ1, sO1);
-        if (s + 1 < n_steps) step(s + 1, sQ1, sO1, sQ0, sO0);
-    }
-
-    if (!wave_active || kw >= p.seq) return;
-    float* row = (pwave ? p.dv : p.dk) + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
-#pragma unroll
-    for (int db = 0; db < NDB; db++) {
-        if (!pwave) acc[db] *= p.scale;  // dS was accumulated without the softmax scale
-        add_row_block(row, acc[db], db * 32, hh, DP, true);
-    }
+    if (pwave)
+        run(RoleTag<true>{});
+    else
+        run(RoleTag<false>{});
 }
 
 static int pick_hpw_b(int group, int cap) {

@@ -51,6 +51,12 @@ __device__ __forceinline__ f32x16 mfma32(float a, float b, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// Compile-time tag selecting one code path of a kernel (a wave role).
+template <bool B>
+struct RoleTag {
+    static constexpr bool value = B;
+};
+
 __device__ __forceinline__ f32x16 zero16() {
     f32x16 z;
 #pragma unroll
