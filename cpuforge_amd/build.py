@@ -67,6 +67,12 @@ def build(verbose: bool = False) -> str:
     out = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if out.returncode != 0:
         raise RuntimeError("link failed:\n" + _filter(out.stdout))
+    # A kernel the host pass failed to emit links fine and only fails when
+    # the library is loaded (an undefined launch stub): refuse it here.
+    und = subprocess.run(["nm", "-u", tmp], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    stubs = [ln.split()[-1] for ln in und.stdout.splitlines() if "__device_stub__" in ln]
+    if stubs:
+        raise RuntimeError("kernel launch stubs missing from the host pass: " + ", ".join(stubs))
     os.replace(tmp, LIB)
     return LIB
 

@@ -424,302 +424,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams p) {
 
 // ---------------------------------------------------------------------------
 // Fast paths: bf16 inputs, head_dim == DP (64 or 128), 16-byte aligned rows.
-// Tiles are staged row-major into double-buffered swizzled LDS (prefetched
-// into registers one step ahead, one barrier per step); every transposed
-// operand (dO^T, Q^T, K^T) is read from the row-major tile with
-// ds_read_b64_tr_b16.  The contraction order over heads and tiles is fixed,
-// so results stay bitwise reproducible.
-
-// dK/dV: four waves, each owning 32 keys of one KV head; steps run over
-// (query head of the group, query tile of BM rows) in a fixed order.
-template <int DP, int BM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_bwd_dkdv_bf16_kernel(
-    const BwdParams p) {
-    constexpr int NT = 256;
-    constexpr int CPR = DP / 8;
-    constexpr int TILE = BM * DP;
-    constexpr int RPC = 512 / DP;             // tile rows per 1 KiB wave load (64 lanes x 16 B)
-    constexpr int CPW = TILE / 512 / 4;       // 1 KiB loads per wave per tile
-    static_assert(TILE % 2048 == 0 && BM <= NT / 2, "tile must split evenly over the four waves");
-    static_assert(BM % 32 == 0, "query tile must be whole 32-row blocks");
-    constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NQB = BM / 32;
-    // Two stages as separate arrays, so the compiler can tell the stage being
-    // read from the one the direct-to-LDS loads are filling.
-    __shared__ __attribute__((aligned(16))) bf16_bits sQ0[TILE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sQ1[TILE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sO0[TILE];  // dO rows
-    __shared__ __attribute__((aligned(16))) bf16_bits sO1[TILE];
-    __shared__ __attribute__((aligned(16))) float sL[2][BM];        // lse * log2(e)
-    __shared__ __attribute__((aligned(16))) float sD[2][BM];        // delta
-
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int l32 = lane & 31, hh = lane >> 5;
-
-    const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
-    const int kvt = id % p.n_kvtiles;  // low key tiles see the most queries: first
-    const int rest = id / p.n_kvtiles;
-    const int g = rest % p.nkv;
-    const int b = rest / p.nkv;
-    const int wg_key0 = kvt * p.kv_tile;
-    const int key0 = wg_key0 + wave * 32;
-    const int kw = key0 + l32;
-    const bool wave_active = key0 < p.seq;
-
-    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
-    const bf16_bits* qg = static_cast<const bf16_bits*>(p.q) + (long)b * p.q_bs;
-    const bf16_bits* og = static_cast<const bf16_bits*>(p.d_o) + (long)b * p.q_bs;
-
-    // K^T and V^T operands: key kw, head dims hh*HALF + kd*8 + [0, 8).
-    bf16x8 kf[NKD], vf[NKD];
-    {
-        const long off = (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP + hh * HALF;
-        const bf16_bits* kr = static_cast<const bf16_bits*>(p.k) + off;
-        const bf16_bits* vr = static_cast<const bf16_bits*>(p.v) + off;
-        const bool ok = kw < p.seq;
-#pragma unroll
-        for (int kd = 0; kd < NKD; kd++) {
-            kf[kd] = __builtin_bit_cast(bf16x8, ok ? *reinterpret_cast<const uint4*>(kr + kd * 8) : make_uint4(0, 0, 0, 0));
-            vf[kd] = __builtin_bit_cast(bf16x8, ok ? *reinterpret_cast<const uint4*>(vr + kd * 8) : make_uint4(0, 0, 0, 0));
-        }
-    }
-
-    const int G = lane >> 4, jj = lane & 15;
-    const int tr_row = 4 * (G >> 1) + (jj >> 2);
-    const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
-    const int tr_in = 4 * (jj & 1);
-    const int tr_sw0 = swz<DP>(tr_row), tr_sw8 = swz<DP>(tr_row + 8);
-    const int r_sw = swz<DP>(l32);
-
-    const int n_qt = (p.seq + BM - 1) / BM;
-    const int qt_begin = wg_key0 / BM;
-    const int nq = n_qt - qt_begin;
-    const int n_steps = p.group * nq;
-
-    float pl = 0.0f;
-    // Step s covers query tile qt_begin + s % nq of query head s / nq.  Its
-    // Q and dO rows go straight from global memory into the swizzled LDS tile
-    // (global_load_lds_dwordx4: lane l of a wave load writes the l-th 16 bytes
-    // of a 1 KiB block, so the swizzle is applied to the source addresses).
-    // Rows past the sequence read the last row instead; their lse is +inf, so
-    // P and dS are exactly zero there.
-    auto dma = [&](int s, bf16_bits* Qd, bf16_bits* Od) {
-        const int h = g * p.group + s / nq;
-        const int q0 = (qt_begin + s % nq) * BM;
-#pragma unroll
-        for (int i = 0; i < CPW; i++) {
-            const int blk = wave * CPW + i;
-            const int r = blk * RPC + lane / CPR;
-            const int c = (lane % CPR) ^ swz<DP>(r);
-            const long off = (long)min(q0 + r, p.seq - 1) * qrs + (long)h * DP + c * 8;
-            __builtin_amdgcn_global_load_lds(qg + off, Qd + blk * 512, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(og + off, Od + blk * 512, 16, 0, 0);
-        }
-        // lse and delta of the tile's rows: a plain load whose value is not
-        // touched until store_ld, so no wait for it (vmcnt is in order and
-        // would also wait for the tile loads above) lands before the compute.
-        if (tid < 2 * BM) {
-            const int t = min(q0 + (tid % BM), p.seq - 1);
-            const long li = ((long)b * p.nh + h) * p.seq + t;
-            pl = tid < BM ? p.lse[li] : p.delta[li];
-        }
-    };
-    auto store_ld = [&](int s, int st) {
-        const int t = (qt_begin + s % nq) * BM + (tid % BM);
-        if (tid < BM)
-            sL[st][tid] = t < p.seq ? pl * kLog2e : INFINITY;  // rows past the end: P = 0
-        else if (tid < 2 * BM)
-            sD[st][tid - BM] = t < p.seq ? pl : 0.0f;
-    };
-
-    f32x16 dkt[NDB], dvt[NDB];
-#pragma unroll
-    for (int i = 0; i < NDB; i++) {
-        dkt[i] = zero16();
-        dvt[i] = zero16();
-    }
-
-    auto step = [&](int s, const bf16_bits* Qs, const bf16_bits* Os, bf16_bits* Qn, bf16_bits* On) {
-        const int st = s & 1;
-        const bool more = s + 1 < n_steps;
-        if (more) dma(s + 1, Qn, On);
-        const int q0 = (qt_begin + s % nq) * BM;
-        if (wave_active && q0 + BM - 1 >= key0) {
-            const float* Ls = sL[st];
-            const float* Ds = sD[st];
-            // S and dP for query block qb: rows = queries q0 + qb*32 + [0,32),
-            // columns = this wave's keys.
-            auto scores = [&](int qb, f32x16& sc, f32x16& dp) {
-                sc = zero16();
-                dp = zero16();
-                const bf16_bits* qrow = Qs + (qb * 32 + l32) * DP;
-                const bf16_bits* orow = Os + (qb * 32 + l32) * DP;
-                bf16x8 qa[NKD], oa[NKD];
-#pragma unroll
-                for (int kd = 0; kd < NKD; kd++) {
-                    const int co = ((hh * NKD + kd) ^ r_sw) << 3;
-                    qa[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + co));
-                    oa[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(orow + co));
-                }
-#pragma unroll
-                for (int kd = 0; kd < NKD; kd++) {
-                    sc = mfma32(qa[kd], kf[kd], sc);
-                    dp = mfma32(oa[kd], vf[kd], dp);
-                }
-            };
-            // P = exp2(S*scale*log2e - lse*log2e), dS = P (dP - delta) (the
-            // softmax scale is applied to dK once, at the end); dV^T += dO^T P
-            // and dK^T += Q^T dS with dO^T and Q^T read transposed from the
-            // row-major tiles.
-            auto accumulate = [&](int qb, const f32x16& sc, const f32x16& dp, bool masked) {
-                float pr[16], ds[16];
-#pragma unroll
-                for (int g4 = 0; g4 < 4; g4++) {
-                    const int qi = qb * 32 + g4 * 8 + hh * 4;
-                    const float4 l4 = *reinterpret_cast<const float4*>(&Ls[qi]);
-                    const float4 d4 = *reinterpret_cast<const float4*>(&Ds[qi]);
-                    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-                    const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int r = g4 * 4 + i;
-                        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lv[i]));
-                        if (masked && kw > q0 + qi + i) pv = 0.0f;
-                        pr[r] = pv;
-                        ds[r] = pv * (dp[r] - dv[i]);  // softmax scale applied to dK at the end
-                    }
-                }
-                const bf16x8 p0 = cvt_bf16x8(&pr[0]), p1 = cvt_bf16x8(&pr[8]);
-                const bf16x8 d0 = cvt_bf16x8(&ds[0]), d1 = cvt_bf16x8(&ds[8]);
-#pragma unroll
-                for (int db = 0; db < NDB; db++) {
-                    const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
-                    const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
-                    const bf16_bits* o0 = Os + (qb * 32 + tr_row) * DP;
-                    const bf16_bits* q0p = Qs + (qb * 32 + tr_row) * DP;
-                    const bf16x8 oa0 = join_bf16x4(ds_read_tr16(o0 + c0), ds_read_tr16(o0 + 8 * DP + c8));
-                    const bf16x8 oa1 = join_bf16x4(ds_read_tr16(o0 + 16 * DP + c0), ds_read_tr16(o0 + 24 * DP + c8));
-                    const bf16x8 qa0 = join_bf16x4(ds_read_tr16(q0p + c0), ds_read_tr16(q0p + 8 * DP + c8));
-                    const bf16x8 qa1 = join_bf16x4(ds_read_tr16(q0p + 16 * DP + c0), ds_read_tr16(q0p + 24 * DP + c8));
-                    dvt[db] = mfma32(oa0, p0, dvt[db]);
-                    dvt[db] = mfma32(oa1, p1, dvt[db]);
-                    dkt[db] = mfma32(qa0, d0, dkt[db]);
-                    dkt[db] = mfma32(qa1, d1, dkt[db]);
-                }
-            };
-            if (q0 >= wg_key0 + p.kv_tile) {
-                // Interior step: every query of the tile follows every key of the
-                // workgroup (no mask, no branch).  Query blocks go in pairs, both
-                // blocks' S and dP issued before the first softmax so the
-                // scheduler can overlap one block's softmax with the other
-                // block's matrix work.
-                static_assert(NQB % 2 == 0, "the interior step takes query blocks in pairs");
-                auto sdp = [&](int qb, f32x16& sc, f32x16& dp) {
-                    sc = zero16();
-                    dp = zero16();
-                    const bf16_bits* qrow = Qs + (qb * 32 + l32) * DP;
-                    const bf16_bits* orow = Os + (qb * 32 + l32) * DP;
-#pragma unroll
-                    for (int kd = 0; kd < NKD; kd++) {
-                        const int co = ((hh * NKD + kd) ^ r_sw) << 3;
-                        const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qrow + co));
-                        const bf16x8 c = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(orow + co));
-                        sc = mfma32(a, kf[kd], sc);
-                        dp = mfma32(c, vf[kd], dp);
-                    }
-                };
-                auto softmax = [&](int qb, const f32x16& sc, const f32x16& dp, bf16x8& pa, bf16x8& pb, bf16x8& da,
-                                   bf16x8& dbb) {
-                    float pr[16], ds[16];
-#pragma unroll
-                    for (int g4 = 0; g4 < 4; g4++) {
-                        const int qi = qb * 32 + g4 * 8 + hh * 4;
-                        const float4 l4 = *reinterpret_cast<const float4*>(&Ls[qi]);
-                        const float4 d4 = *reinterpret_cast<const float4*>(&Ds[qi]);
-                        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-                        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const int r = g4 * 4 + i;
-                            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lv[i]));
-                            pr[r] = pv;
-                            ds[r] = pv * (dp[r] - dv[i]);
-                        }
-                    }
-                    pa = cvt_bf16x8(&pr[0]);
-                    pb = cvt_bf16x8(&pr[8]);
-                    da = cvt_bf16x8(&ds[0]);
-                    dbb = cvt_bf16x8(&ds[8]);
-                };
-                auto dvdk = [&](int qb, const bf16x8& pa, const bf16x8& pb, const bf16x8& da, const bf16x8& dbb) {
-#pragma unroll
-                    for (int db = 0; db < NDB; db++) {
-                        const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
-                        const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
-                        const bf16_bits* o0 = Os + (qb * 32 + tr_row) * DP;
-                        const bf16_bits* q0p = Qs + (qb * 32 + tr_row) * DP;
-                        const bf16x8 oa0 = join_bf16x4(ds_read_tr16(o0 + c0), ds_read_tr16(o0 + 8 * DP + c8));
-                        const bf16x8 oa1 =
-                            join_bf16x4(ds_read_tr16(o0 + 16 * DP + c0), ds_read_tr16(o0 + 24 * DP + c8));
-                        const bf16x8 qa0 = join_bf16x4(ds_read_tr16(q0p + c0), ds_read_tr16(q0p + 8 * DP + c8));
-                        const bf16x8 qa1 =
-                            join_bf16x4(ds_read_tr16(q0p + 16 * DP + c0), ds_read_tr16(q0p + 24 * DP + c8));
-                        dvt[db] = mfma32(oa0, pa, dvt[db]);
-                        dvt[db] = mfma32(oa1, pb, dvt[db]);
-                        dkt[db] = mfma32(qa0, da, dkt[db]);
-                        dkt[db] = mfma32(qa1, dbb, dkt[db]);
-                    }
-                };
-#pragma unroll
-                for (int qb = 0; qb < NQB; qb += 2) {
-                    f32x16 sc0, dp0, sc1, dp1;
-                    bf16x8 pa0, pb0, da0, db0, pa1, pb1, da1, db1;
-                    sdp(qb, sc0, dp0);
-                    sdp(qb + 1, sc1, dp1);
-                    softmax(qb, sc0, dp0, pa0, pb0, da0, db0);
-                    dvdk(qb, pa0, pb0, da0, db0);
-                    softmax(qb + 1, sc1, dp1, pa1, pb1, da1, db1);
-                    dvdk(qb + 1, pa1, pb1, da1, db1);
-                    // Pairs stay apart: hoisting the next pair's loads would
-                    // run out of registers.
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            } else {
-#pragma unroll
-                for (int qb = 0; qb < NQB; qb++) {
-                    const int tq0 = q0 + qb * 32;
-                    if (tq0 >= p.seq) break;
-                    if (tq0 + 31 < key0) continue;
-                    f32x16 sc, dp;
-                    scores(qb, sc, dp);
-                    accumulate(qb, sc, dp, tq0 < key0 + 31);
-                }
-            }
-        }
-        if (more) store_ld(s + 1, st ^ 1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for step s + 1 have landed
-        __syncthreads();
-    };
-
-    dma(0, sQ0, sO0);
-    store_ld(0, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    for (int s = 0; s < n_steps; s += 2) {
-        step(s, sQ0, sO0, sQ1, sO1);
-        if (s + 1 < n_steps) step(s + 1, sQ1, sO1, sQ0, sO0);
-    }
-
-    if (!wave_active || kw >= p.seq) return;
-    float* dkrow = p.dk + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
-    float* dvrow = p.dv + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
-#pragma unroll
-    for (int db = 0; db < NDB; db++) {
-        dkt[db] *= p.scale;  // dS was accumulated without the softmax scale
-        add_row_block(dkrow, dkt[db], db * 32, hh, DP, true);
-        add_row_block(dvrow, dvt[db], db * 32, hh, DP, true);
-    }
-}
+// Tiles are staged row-major in double-buffered LDS; every transposed operand
+// (dO^T, Q^T, K^T) is read from the row-major tile with ds_read_b64_tr_b16.
+// The contraction order over heads and tiles is fixed, so results stay
+// bitwise reproducible.
 
 // dQ: the forward's decomposition (a wave owns 32 queries of one head, four
 // waves per workgroup); K/V tiles of BN keys are shared by the workgroup.
@@ -876,8 +584,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // dK/dV with two specialised waves per 32-key slice: eight waves, 128 keys per
-// workgroup, the same (key tile, KV head, sequence) grid and step order as
-// attn_bwd_dkdv_bf16_kernel.
+// workgroup of one KV head; steps run over (query head of the group, query
+// tile of BM rows) in a fixed order, low key tiles (the most queries) first.
 //   P waves (0-3) hold K^T and the dV^T accumulators: S = Q K^T,
 //     P = exp2(S*scale*log2e - lse*log2e) (causally masked), P to LDS in f32,
 //     then dV^T += dO^T P.
@@ -892,18 +600,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const BwdParams p) {
     constexpr int NT = 512;
     constexpr int CPR = DP / 8;
-    constexpr int TILE = BM * DP;
-    constexpr int RPC = 512 / DP;        // tile rows per 1 KiB wave load
-    constexpr int CPW = TILE / 512 / 8;  // 1 KiB loads per wave per tile
-    static_assert(TILE % 4096 == 0 && 2 * BM <= NT, "tile must split evenly over the eight waves");
+    using L = BlkTile<DP, BM>;
+    constexpr int CPW = L::NB / 8;  // 1 KiB loads per wave per tile
+    // Local copies: hipcc's host pass drops the kernel (an undefined launch
+    // stub) when a lambda in it names these static members directly.
+    constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16;
+    static_assert(L::NB % 8 == 0 && 2 * BM <= NT, "tile must split evenly over the eight waves");
     static_assert(BM % 32 == 0, "query tile must be whole 32-row blocks");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NQB = BM / 32;
-    __shared__ __attribute__((aligned(16))) bf16_bits sQ0[TILE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sQ1[TILE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sO0[TILE];  // dO rows
-    __shared__ __attribute__((aligned(16))) bf16_bits sO1[TILE];
-    __shared__ __attribute__((aligned(16))) float sL[2][BM];  // lse * log2(e)
-    __shared__ __attribute__((aligned(16))) float sD[2][BM];  // delta
+    // Query tiles: MFMA row i of block qb is query q0 + 32*qb + qperm(i).
+    __shared__ __attribute__((aligned(16))) bf16_bits sQ0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sQ1[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sO0[L::SIZE];  // dO rows
+    __shared__ __attribute__((aligned(16))) bf16_bits sO1[L::SIZE];
+    __shared__ __attribute__((aligned(16))) float sL[2][BM];  // lse * log2(e), by MFMA row
+    __shared__ __attribute__((aligned(16))) float sD[2][BM];  // delta, by MFMA row
     // P of each (key slice, query block): lane l's four values of row group g4.
     __shared__ float4 sP[4][NQB][4][64];
 
@@ -927,12 +638,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const bf16_bits* qg = static_cast<const bf16_bits*>(p.q) + (long)b * p.q_bs;
     const bf16_bits* og = static_cast<const bf16_bits*>(p.d_o) + (long)b * p.q_bs;
 
+    // Row reads: lane (l32, hh) reads MFMA row l32, chunks hh*NKD + kd.
+    const int rrow = L::row(qperm(l32)) + hh * HALF;
+    // Transposed reads: in each 16-lane group G, lane 4k + m supplies head
+    // dims 16*(G%2) + 4m + [0, 4) of MFMA row 4*hh + k (+8, +16, +24), that
+    // is tile row 4k + hh (+2, +16, +18).
     const int G = lane >> 4, jj = lane & 15;
-    const int tr_row = 4 * (G >> 1) + (jj >> 2);
-    const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
-    const int tr_in = 4 * (jj & 1);
-    const int tr_sw0 = swz<DP>(tr_row), tr_sw8 = swz<DP>(tr_row + 8);
-    const int r_sw = swz<DP>(l32);
+    const int trow = L::row(4 * (jj >> 2) + hh) + 16 * (G & 1) + 4 * (jj & 3);
 
     const int n_qt = (p.seq + BM - 1) / BM;
     const int qt_begin = wg_key0 / BM;
@@ -940,29 +652,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int n_steps = p.group * nq;
 
     float pl = 0.0f;
+    // Query of MFMA row i (0 <= i < BM) of a tile.
+    const int lrow = (tid % BM & ~31) + qperm(tid & 31);
     // Step s covers query tile qt_begin + s % nq of query head s / nq; its Q
-    // and dO rows go straight into the swizzled LDS tile (see the four-wave
-    // kernel above for the addressing and the past-the-end rows).
+    // and dO rows go straight into the blocked LDS tile: wave w fills load
+    // blocks w*CPW.., lane l of block b loading chunk l % CPR of tile row
+    // b + NB*(l / CPR).  Rows past the end load the last row (finite values);
+    // their lse is +inf and delta 0 below, so P = dS = 0 there.
     auto dma = [&](int s, bf16_bits* Qd, bf16_bits* Od) {
         const int h = g * p.group + s / nq;
         const int q0 = (qt_begin + s % nq) * BM;
 #pragma unroll
         for (int i = 0; i < CPW; i++) {
             const int blk = wave * CPW + i;
-            const int r = blk * RPC + lane / CPR;
-            const int c = (lane % CPR) ^ swz<DP>(r);
-            const long off = (long)min(q0 + r, p.seq - 1) * qrs + (long)h * DP + c * 8;
-            __builtin_amdgcn_global_load_lds(qg + off, Qd + blk * 512, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(og + off, Od + blk * 512, 16, 0, 0);
+            const int r = blk + L::NB * (lane / CPR);
+            const long off = (long)min(q0 + r, p.seq - 1) * qrs + (long)h * DP + (lane % CPR) * 8;
+            __builtin_amdgcn_global_load_lds(qg + off, Qd + blk * BSTRIDE, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(og + off, Od + blk * BSTRIDE, 16, 0, 0);
         }
         if (tid < 2 * BM) {
-            const int t = min(q0 + (tid % BM), p.seq - 1);
+            const int t = min(q0 + lrow, p.seq - 1);
             const long li = ((long)b * p.nh + h) * p.seq + t;
             pl = tid < BM ? p.lse[li] : p.delta[li];
         }
     };
     auto store_ld = [&](int s, int st) {
-        const int t = (qt_begin + s % nq) * BM + (tid % BM);
+        const int t = (qt_begin + s % nq) * BM + lrow;
         if (tid < BM)
             sL[st][tid] = t < p.seq ? pl * kLog2e : INFINITY;  // rows past the end: P = 0
         else if (tid < 2 * BM)
@@ -1007,8 +722,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             bf16x8 pbf[NQB][2];  // P waves: P of each block as MFMA operands
             f32x16 dpv[NQB];     // dS waves: dP of each block
             auto row_read = [&](int qb, int kd) {
-                return __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const uint4*>(A1 + (qb * 32 + l32) * DP + (((hh * NKD + kd) ^ r_sw) << 3)));
+                return __builtin_bit_cast(bf16x8,
+                                          *reinterpret_cast<const uint4*>(A1 + rrow + qb * 2 * ROW16 + kd * 8));
             };
             // P waves: P = exp2(S*scale*log2e - lse*log2e), causally masked,
             // to LDS in f32 for the dS waves and to registers as bf16 operands.
@@ -1022,7 +737,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[g4 * 4 + i], p.sl2, -lv[i]));
-                        if (masked && kw > q0 + qi + i) pv = 0.0f;
+                        if (masked && kw > q0 + qb * 32 + qperm(g4 * 8 + hh * 4 + i)) pv = 0.0f;
                         pr[g4 * 4 + i] = pv;
                     }
                     sP[slice][qb][g4][lane] = make_float4(pr[g4 * 4], pr[g4 * 4 + 1], pr[g4 * 4 + 2], pr[g4 * 4 + 3]);
@@ -1090,14 +805,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     b0 = cvt_bf16x8(&ds[0]);
                     b1 = cvt_bf16x8(&ds[8]);
                 }
-                // dO^T (P waves) or Q^T (dS waves), read transposed from the tile.
-                const bf16_bits* t0 = A2 + (qb * 32 + tr_row) * DP;
+                // dO^T (P waves) or Q^T (dS waves), read transposed from the
+                // tile: MFMA rows 4hh..+3 and 8+4hh..+3 of the block for b0,
+                // 16 more for b1.
+                const bf16_bits* t0 = A2 + trow + qb * 2 * ROW16;
 #pragma unroll
                 for (int db = 0; db < NDB; db++) {
-                    const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
-                    const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
-                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(t0 + c0), ds_read_tr16(t0 + 8 * DP + c8));
-                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(t0 + 16 * DP + c0), ds_read_tr16(t0 + 24 * DP + c8));
+                    const bf16_bits* t = t0 + db * 32;
+                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(t), ds_read_tr16(t + 2 * BSTRIDE));
+                    const bf16x8 a1 =
+                        join_bf16x4(ds_read_tr16(t + ROW16), ds_read_tr16(t + ROW16 + 2 * BSTRIDE));
                     acc[db] = mfma32(a0, b0, acc[db]);
                     acc[db] = mfma32(a1, b1, acc[db]);
                 }

@@ -251,6 +251,35 @@ __device__ __forceinline__ int swz_off(int r, int c) {
     return r * DP + ((c ^ swz<DP>(r)) << 3);
 }
 
+// ------------------------------------------------- blocked bf16 LDS tiles
+// A tile of ROWS rows of DP bf16 (DP = 64 or 128) filled by direct-to-LDS
+// loads: one global_load_lds of 64 lanes x 16 bytes writes 1 KiB at
+// consecutive addresses.  Load block b (b < NB = ROWS*DP/512) holds the rows
+// b, b + NB, b + 2*NB, ... and blocks start 1040 bytes apart, so row r starts
+// at element row(r) = (r % NB) * 520 + (r / NB) * DP.  Reads are then
+// conflict-free on the 64 four-byte banks, and each lane's address is a base
+// register plus a compile-time offset:
+//   - ds_read_b128 by 16 lanes of 16 consecutive rows (one 16-byte chunk
+//     each): 1040 = 16 (mod 256), so rows with distinct r % 16 start on
+//     distinct 16-byte bank groups (DP = 64: r / NB adds 128 to the second
+//     eight);
+//   - ds_read_b64_tr_b16 by 32 lanes of four rows 4 apart, 64 bytes each:
+//     the four row starts are 64 bytes apart (mod 256).
+// The MFMA row i of a 32-row block is tile row qperm(i) of that block, which
+// makes the four rows of every transposed read (MFMA rows 4h..4h+3 of the
+// accumulator layout) 4 apart.
+template <int DP, int ROWS>
+struct BlkTile {
+    static constexpr int NB = ROWS * DP / 512;  // load blocks
+    static constexpr int STRIDE = 520;          // elements between blocks
+    static constexpr int SIZE = NB * STRIDE;
+    static constexpr int ROW16 = 16 / NB * DP;  // row(r + 16) - row(r)
+    static_assert(NB == 8 || NB == 16, "16 rows must cover every block once or twice");
+    __host__ __device__ static int row(int r) { return (r % NB) * STRIDE + (r / NB) * DP; }
+};
+// qperm(i) = 4*(i%4) + (i/4)%4 + 16*(i/16) on 0..31; qperm(qperm(i)) = i.
+__host__ __device__ __forceinline__ constexpr int qperm(int i) { return ((i & 3) << 2) | ((i >> 2) & 3) | (i & 16); }
+
 // Hardware round-to-nearest-even pack of eight f32 values into an MFMA
 // operand (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ bf16x8 cvt_bf16x8(const float* v) {
