@@ -601,11 +601,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int NT = 512;
     constexpr int CPR = DP / 8;
     using L = BlkTile<DP, BM>;
-    constexpr int CPW = L::NB / 8;  // 1 KiB loads per wave per tile
+    constexpr int CPW = L::NB / 4;  // 1 KiB loads per dS wave per tile
     // Local copies: hipcc's host pass drops the kernel (an undefined launch
     // stub) when a lambda in it names these static members directly.
     constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16;
-    static_assert(L::NB % 8 == 0 && 2 * BM <= NT, "tile must split evenly over the eight waves");
+    static_assert(L::NB % 4 == 0 && 2 * BM <= NT / 2, "tile must split evenly over the four dS waves");
     static_assert(BM % 32 == 0, "query tile must be whole 32-row blocks");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NQB = BM / 32;
     // Query tiles: MFMA row i of block qb is query q0 + 32*qb + qperm(i).
@@ -652,36 +652,41 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int n_steps = p.group * nq;
 
     float pl = 0.0f;
+    // The dS waves (threads 256..511) load the tiles, lse and delta: they
+    // would otherwise wait for the P waves' softmax at the mid-step barrier.
+    const int dt = tid - NT / 2;
     // Query of MFMA row i (0 <= i < BM) of a tile.
-    const int lrow = (tid % BM & ~31) + qperm(tid & 31);
+    const int lrow = (dt % BM & ~31) + qperm(dt & 31);
     // Step s covers query tile qt_begin + s % nq of query head s / nq; its Q
-    // and dO rows go straight into the blocked LDS tile: wave w fills load
+    // and dO rows go straight into the blocked LDS tile: dS wave w fills load
     // blocks w*CPW.., lane l of block b loading chunk l % CPR of tile row
     // b + NB*(l / CPR).  Rows past the end load the last row (finite values);
     // their lse is +inf and delta 0 below, so P = dS = 0 there.
     auto dma = [&](int s, bf16_bits* Qd, bf16_bits* Od) {
         const int h = g * p.group + s / nq;
         const int q0 = (qt_begin + s % nq) * BM;
+        if (dt < 0) return;
 #pragma unroll
         for (int i = 0; i < CPW; i++) {
-            const int blk = wave * CPW + i;
+            const int blk = (wave - 4) * CPW + i;
             const int r = blk + L::NB * (lane / CPR);
             const long off = (long)min(q0 + r, p.seq - 1) * qrs + (long)h * DP + (lane % CPR) * 8;
             __builtin_amdgcn_global_load_lds(qg + off, Qd + blk * BSTRIDE, 16, 0, 0);
             __builtin_amdgcn_global_load_lds(og + off, Od + blk * BSTRIDE, 16, 0, 0);
         }
-        if (tid < 2 * BM) {
+        if (dt >= 0 && dt < 2 * BM) {
             const int t = min(q0 + lrow, p.seq - 1);
             const long li = ((long)b * p.nh + h) * p.seq + t;
-            pl = tid < BM ? p.lse[li] : p.delta[li];
+            pl = dt < BM ? p.lse[li] : p.delta[li];
         }
     };
     auto store_ld = [&](int s, int st) {
         const int t = (qt_begin + s % nq) * BM + lrow;
-        if (tid < BM)
-            sL[st][tid] = t < p.seq ? pl * kLog2e : INFINITY;  // rows past the end: P = 0
-        else if (tid < 2 * BM)
-            sD[st][tid - BM] = t < p.seq ? pl : 0.0f;
+        if (dt < 0) return;
+        if (dt < BM)
+            sL[st][dt] = t < p.seq ? pl * kLog2e : INFINITY;  // rows past the end: P = 0
+        else if (dt < 2 * BM)
+            sD[st][dt - BM] = t < p.seq ? pl : 0.0f;
     };
 
     // Each role runs its own copy of the step loop: the registers one role
@@ -727,12 +732,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             };
             // P waves: P = exp2(S*scale*log2e - lse*log2e), causally masked,
             // to LDS in f32 for the dS waves and to registers as bf16 operands.
-            auto p_block = [&](int qb, const f32x16& sc, bool masked) {
+            // lse of MFMA rows g4*8 + hh*4 + [0, 4) of block qb.
+            auto lse4 = [&](int qb, int g4) { return *reinterpret_cast<const float4*>(&Ls[qb * 32 + g4 * 8 + hh * 4]); };
+            auto p_block = [&](int qb, const f32x16& sc, bool masked, const float4 (&l4s)[4]) {
                 float pr[16];
 #pragma unroll
                 for (int g4 = 0; g4 < 4; g4++) {
-                    const int qi = qb * 32 + g4 * 8 + hh * 4;
-                    const float4 l4 = *reinterpret_cast<const float4*>(&Ls[qi]);
+                    const float4 l4 = l4s[g4];
                     const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
@@ -747,6 +753,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             };
             // Phase 1: S -> P (P waves) and dP (dS waves).
             if (full) {
+                // The softmax's lse values are read before the products, so
+                // their latency is not paid once per group of four.
+                float4 l4s[NQB][4];
+                if constexpr (PW) {
+#pragma unroll
+                    for (int qb = 0; qb < NQB; qb++)
+#pragma unroll
+                        for (int g4 = 0; g4 < 4; g4++) l4s[qb][g4] = lse4(qb, g4);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 f32x16 sc[NQB];
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++) sc[qb] = zero16();
@@ -757,7 +773,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++) {
                     if constexpr (PW)
-                        p_block(qb, sc[qb], false);
+                        p_block(qb, sc[qb], false, l4s[qb]);
                     else
                         dpv[qb] = sc[qb];
                 }
@@ -769,23 +785,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     f32x16 sc = zero16();
 #pragma unroll
                     for (int kd = 0; kd < NKD; kd++) sc = mfma32(row_read(qb, kd), xf[kd], sc);
-                    if constexpr (PW)
-                        p_block(qb, sc, tq0 < key0 + 31);
-                    else
+                    if constexpr (PW) {
+                        float4 l4s[4];
+#pragma unroll
+                        for (int g4 = 0; g4 < 4; g4++) l4s[g4] = lse4(qb, g4);
+                        p_block(qb, sc, tq0 < key0 + 31, l4s);
+                    } else {
                         dpv[qb] = sc;
+                    }
                 }
             }
-            // The next step's loads start after the P stores (the compiler cannot
-            // tell those stores from the loads' LDS destination and would wait for
-            // the loads), and overlap phase 2.  P is published with this wave's
-            // LDS writes done and a plain barrier: __syncthreads() would also
-            // wait for the loads.
-            if (more) dma(s + 1, Qn, On);
+            // The dS waves start the next step's loads here, while the P waves
+            // finish the softmax; the loads overlap phase 2.  P is published
+            // with this wave's LDS writes done and a plain barrier:
+            // __syncthreads() would also wait for the loads.
+            if constexpr (!PW)
+                if (more) dma(s + 1, Qn, On);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
             // Phase 2: dV^T += dO^T P (P waves), dS -> dK^T += Q^T dS (dS waves).
-            auto phase2 = [&](int qb) {
+            // dS waves: P and delta of MFMA rows g4*8 + hh*4 + [0, 4) of block qb.
+            auto pd4 = [&](int qb, int g4, float4& p4, float4& d4) {
+                p4 = sP[slice][qb][g4][lane];
+                d4 = *reinterpret_cast<const float4*>(&Ds[qb * 32 + g4 * 8 + hh * 4]);
+            };
+            auto phase2 = [&](int qb, const float4 (&p4s)[4], const float4 (&d4s)[4]) {
                 bf16x8 b0, b1;
                 if constexpr (PW) {
                     b0 = pbf[qb][0];
@@ -794,9 +819,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     float ds[16];
 #pragma unroll
                     for (int g4 = 0; g4 < 4; g4++) {
-                        const int qi = qb * 32 + g4 * 8 + hh * 4;
-                        const float4 d4 = *reinterpret_cast<const float4*>(&Ds[qi]);
-                        const float4 p4 = sP[slice][qb][g4][lane];
+                        const float4 d4 = d4s[g4];
+                        const float4 p4 = p4s[g4];
                         ds[g4 * 4 + 0] = p4.x * (dpv[qb][g4 * 4 + 0] - d4.x);
                         ds[g4 * 4 + 1] = p4.y * (dpv[qb][g4 * 4 + 1] - d4.y);
                         ds[g4 * 4 + 2] = p4.z * (dpv[qb][g4 * 4 + 2] - d4.z);
@@ -820,17 +844,31 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 }
             };
             if (full) {
+                // dS waves read every P and delta value of the step first.
+                float4 p4s[NQB][4], d4s[NQB][4];
+                if constexpr (!PW) {
 #pragma unroll
-                for (int qb = 0; qb < NQB; qb++) phase2(qb);
+                    for (int qb = 0; qb < NQB; qb++)
+#pragma unroll
+                        for (int g4 = 0; g4 < 4; g4++) pd4(qb, g4, p4s[qb][g4], d4s[qb][g4]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int qb = 0; qb < NQB; qb++) phase2(qb, p4s[qb], d4s[qb]);
             } else if (act) {
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++) {
                     const int tq0 = q0 + qb * 32;
                     if (tq0 >= p.seq || tq0 + 31 < key0) continue;
-                    phase2(qb);
+                    float4 p4s[4], d4s[4];
+                    if constexpr (!PW)
+#pragma unroll
+                        for (int g4 = 0; g4 < 4; g4++) pd4(qb, g4, p4s[g4], d4s[g4]);
+                    phase2(qb, p4s, d4s);
                 }
             }
-            if (more) store_ld(s + 1, st ^ 1);
+            if constexpr (!PW)
+                if (more) store_ld(s + 1, st ^ 1);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for step s + 1 have landed
             __syncthreads();
         };
@@ -849,8 +887,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     };
 
-    dma(0, sQ0, sO0);
-    store_ld(0, 0);
+    if (!pwave) {
+        dma(0, sQ0, sO0);
+        store_ld(0, 0);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (pwave)
