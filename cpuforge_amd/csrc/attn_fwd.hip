@@ -225,28 +225,33 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams p) {
 // ---------------------------------------------------------------------------
 // Fast path: bf16 inputs, head_dim == DP (64 or 128), 16-byte aligned rows.
 // Four waves per workgroup, the same (tile, heads) decomposition as above.
-// K/V tiles of BN keys are prefetched into registers one tile ahead and
-// stored row-major into a double-buffered swizzled LDS tile, so each tile
-// costs one barrier.  S^T = K Q^T reads K rows with ds_read_b128; O^T +=
-// V^T P^T reads V^T straight from the row-major V tile with transposed reads
-// (ds_read_b64_tr_b16).  The running max is only moved when a tile's max
-// exceeds it by more than kLazyRescale (log2 units): exp2 of the shifted
-// scores then stays below 2^kLazyRescale, and O and the row sum are rescaled
-// only on those tiles.  O = acc / sum and lse = m + log2(sum) do not depend on
-// which shift was used.
+// K/V tiles of BN keys go straight from global memory into double-buffered
+// blocked LDS tiles (global_load_lds, issued one tile ahead by all four
+// waves), so each tile costs one barrier.  S^T = K Q^T reads K rows with
+// ds_read_b128; O^T += V^T P^T reads V^T straight from the V tile with
+// transposed reads (ds_read_b64_tr_b16).  MFMA row i of a 32-key block is key
+// qperm(i) of the block (see BlkTile).  The running max is only moved when a
+// tile's max exceeds it by more than kLazyRescale (log2 units): exp2 of the
+// shifted scores then stays below 2^kLazyRescale, and O and the row sum are
+// rescaled only on those tiles.  O = acc / sum and lse = m + log2(sum) do not
+// depend on which shift was used.
 constexpr float kLazyRescale = 8.0f;
 
 template <int DP, int BN>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_bf16_kernel(
     const FwdParams p) {
-    constexpr int NT = 256;
     constexpr int CPR = DP / 8;  // 16-byte chunks per row
-    constexpr int TILE = BN * DP;
-    constexpr int LOADS = BN * CPR / NT;
-    static_assert(BN * CPR % NT == 0, "tile must split evenly over the workgroup");
+    using L = BlkTile<DP, BN>;
+    constexpr int CPW = L::NB / 4;  // 1 KiB loads per wave per tile
+    // Local copies: hipcc's host pass drops the kernel (an undefined launch
+    // stub) when a lambda in it names these static members directly.
+    constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16;
+    static_assert(L::NB % 4 == 0, "tile must split evenly over the four waves");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NKB = BN / 32;
-    __shared__ __attribute__((aligned(16))) bf16_bits sK[2][TILE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sV[2][TILE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sK0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sK1[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV1[L::SIZE];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -286,36 +291,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
 
-    // Per-lane constants of the transposed V^T reads: lane 16*G + jj reads
-    // row kbase + 4*(G/2) + jj/4, head dims db*32 + 16*(G%2) + 4*(jj%4) + [0,4).
+    // Row reads: lane (l32, hh) reads MFMA row l32 (key qperm(l32)), chunks
+    // hh*NKD + kd.  Transposed reads: in each 16-lane group G, lane 4k + m
+    // supplies head dims 16*(G%2) + 4m + [0, 4) of MFMA row 4*hh + k (+8,
+    // +16, +24), that is tile row 4k + hh (+2, +16, +18).
+    const int rrow = L::row(qperm(l32)) + hh * HALF;
     const int G = lane >> 4, jj = lane & 15;
-    const int tr_row = 4 * (G >> 1) + (jj >> 2);
-    const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
-    const int tr_in = 4 * (jj & 1);
-    const int tr_sw0 = swz<DP>(tr_row), tr_sw8 = swz<DP>(tr_row + 8);
-    const int k_sw = swz<DP>(l32);
+    const int trow = L::row(4 * (jj >> 2) + hh) + 16 * (G & 1) + 4 * (jj & 3);
 
-    uint4 pk[LOADS], pv[LOADS];
-    auto gload = [&](int kt) {
+    // Tile kt's K and V rows: wave w fills load blocks w*CPW.., lane l of
+    // block b loading chunk l % CPR of tile row b + NB*(l / CPR).  Keys past
+    // the end load the last key (finite values); the causal mask removes them.
+    auto dma = [&](int kt, bf16_bits* Kd, bf16_bits* Vd) {
 #pragma unroll
-        for (int i = 0; i < LOADS; i++) {
-            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
-            const int key = kt * BN + row;
-            if (key < p.seq) {
-                pk[i] = *reinterpret_cast<const uint4*>(kg + (long)key * kvrs + col * 8);
-                pv[i] = *reinterpret_cast<const uint4*>(vg + (long)key * kvrs + col * 8);
-            } else {
-                pk[i] = make_uint4(0, 0, 0, 0);
-                pv[i] = make_uint4(0, 0, 0, 0);
-            }
-        }
-    };
-    auto lstore = [&](int st) {
-#pragma unroll
-        for (int i = 0; i < LOADS; i++) {
-            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
-            *reinterpret_cast<uint4*>(&sK[st][swz_off<DP>(row, col)]) = pk[i];
-            *reinterpret_cast<uint4*>(&sV[st][swz_off<DP>(row, col)]) = pv[i];
+        for (int i = 0; i < CPW; i++) {
+            const int blk = wave * CPW + i;
+            const int r = blk + L::NB * (lane / CPR);
+            const long off = (long)min(kt * BN + r, p.seq - 1) * kvrs + (lane % CPR) * 8;
+            __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vg + off, Vd + blk * BSTRIDE, 16, 0, 0);
         }
     };
 
@@ -324,34 +318,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int i = 0; i < NDB; i++) oacc[i] = zero16();
     float m2 = -INFINITY, lsum = 0.0f;
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < n_kt; kt++) {
-        const int st = kt & 1;
-        const bool more = kt + 1 < n_kt;
-        if (more) gload(kt + 1);
+    auto step = [&](int kt, const bf16_bits* Ks, const bf16_bits* Vs, bf16_bits* Kn, bf16_bits* Vn) {
+        if (kt + 1 < n_kt) dma(kt + 1, Kn, Vn);
         const int k0 = kt * BN;
         if (wave_active && k0 <= wave_last) {
-            const bf16_bits* Ks = sK[st];
-            const bf16_bits* Vs = sV[st];
-            // S^T block kb: keys k0 + kb*32 + [0,32) x this wave's 32 queries.
+            // S^T block kb: keys k0 + kb*32 + qperm([0,32)) x this wave's 32 queries.
             auto scores = [&](int kb) {
                 f32x16 sc = zero16();
-                bf16x8 kf[NKD];
-                const bf16_bits* krow = Ks + (kb * 32 + l32) * DP;
 #pragma unroll
                 for (int kd = 0; kd < NKD; kd++)
-                    kf[kd] = __builtin_bit_cast(
-                        bf16x8, *reinterpret_cast<const uint4*>(krow + (((hh * NKD + kd) ^ k_sw) << 3)));
-#pragma unroll
-                for (int kd = 0; kd < NKD; kd++) sc = mfma32(kf[kd], qf[kd], sc);
+                    sc = mfma32(__builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                                             Ks + rrow + kb * 2 * ROW16 + kd * 8)),
+                                qf[kd], sc);
                 return sc;
             };
             // Move the running max to m (log2 units) when the block max exceeds
             // it by more than kLazyRescale; rescale O and the row sum then.
             auto update_max = [&](float mx) {
-                mx = fmaxf(mx, __shfl_xor(mx, 32)) * p.sl2;
+                mx = max_halves(mx) * p.sl2;
                 const float mnew = mx > m2 + kLazyRescale ? mx : m2;
                 if (__any(mnew != m2)) {
                     const float alpha = __builtin_amdgcn_exp2f(m2 - mnew);
@@ -371,13 +355,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     lsum += pr[r];
                 }
                 const bf16x8 p0 = cvt_bf16x8(&pr[0]), p1 = cvt_bf16x8(&pr[8]);
+                const bf16_bits* t0 = Vs + trow + kb * 2 * ROW16;
 #pragma unroll
                 for (int db = 0; db < NDB; db++) {
-                    const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
-                    const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
-                    const bf16_bits* v0 = Vs + (kb * 32 + tr_row) * DP;
-                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(v0 + c0), ds_read_tr16(v0 + 8 * DP + c8));
-                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(v0 + 16 * DP + c0), ds_read_tr16(v0 + 24 * DP + c8));
+                    const bf16_bits* tp = t0 + db * 32;
+                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(tp), ds_read_tr16(tp + 2 * BSTRIDE));
+                    const bf16x8 a1 =
+                        join_bf16x4(ds_read_tr16(tp + ROW16), ds_read_tr16(tp + ROW16 + 2 * BSTRIDE));
                     oacc[db] = mfma32(a0, p0, oacc[db]);
                     oacc[db] = mfma32(a1, p1, oacc[db]);
                 }
@@ -407,7 +391,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     if (kb0 + 31 > t_wave) {
 #pragma unroll
                         for (int r = 0; r < 16; r++) {
-                            const int key = kb0 + (r >> 2) * 8 + hh * 4 + (r & 3);
+                            const int key = kb0 + qperm((r >> 2) * 8 + hh * 4 + (r & 3));
                             if (key > tq) sc[r] = -INFINITY;
                         }
                     }
@@ -421,12 +405,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 }
             }
         }
-        if (more) lstore(st ^ 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for tile kt + 1 have landed
         __syncthreads();
+    };
+
+    dma(0, sK0, sV0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int kt = 0; kt < n_kt; kt += 2) {
+        step(kt, sK0, sV0, sK1, sV1);
+        if (kt + 1 < n_kt) step(kt + 1, sK1, sV1, sK0, sV0);
     }
 
     if (!wave_active) return;
-    const float ltot = lsum + __shfl_xor(lsum, 32);
+    const float ltot = sum_halves(lsum);
     if (tq >= p.seq) return;
     const float inv = 1.0f / ltot;
     float* orow = p.o + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;

@@ -280,6 +280,29 @@ struct BlkTile {
 // qperm(i) = 4*(i%4) + (i/4)%4 + 16*(i/16) on 0..31; qperm(qperm(i)) = i.
 __host__ __device__ __forceinline__ constexpr int qperm(int i) { return ((i & 3) << 2) | ((i >> 2) & 3) | (i & 16); }
 
+// max / sum of x over lanes l and l ^ 32 with one v_permlane32_swap (no LDS
+// traffic, unlike a shuffle): swapping the upper half of one copy of x with
+// the lower half of another leaves x[l] in one register and x[l ^ 32] in the
+// other.  Written as inline asm: this compiler folds max(r0, r1) of the
+// builtin's two results to r0.  The s_nop covers the VALU-write to permlane
+// read hazard for the copies.
+__device__ __forceinline__ void swap_halves(float x, float& a, float& b) {
+    float u = x, w = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(u), "+v"(w));
+    a = u;
+    b = w;
+}
+__device__ __forceinline__ float max_halves(float x) {
+    float a, b;
+    swap_halves(x, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_halves(float x) {
+    float a, b;
+    swap_halves(x, a, b);
+    return a + b;
+}
+
 // Hardware round-to-nearest-even pack of eight f32 values into an MFMA
 // operand (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ bf16x8 cvt_bf16x8(const float* v) {
