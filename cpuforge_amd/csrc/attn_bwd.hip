@@ -430,18 +430,25 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams p) {
 // bitwise reproducible.
 
 // dQ: the forward's decomposition (a wave owns 32 queries of one head, four
-// waves per workgroup); K/V tiles of BN keys are shared by the workgroup.
+// waves per workgroup); K/V tiles of BN keys are shared by the workgroup and
+// go straight from global memory into double-buffered blocked LDS tiles
+// (global_load_lds, issued one tile ahead by all four waves).  MFMA row i of
+// a 32-key block is key qperm(i) of the block (see BlkTile).
 template <int DP, int BN>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq_bf16_kernel(
     const BwdParams p) {
-    constexpr int NT = 256;
     constexpr int CPR = DP / 8;
-    constexpr int TILE = BN * DP;
-    constexpr int LOADS = BN * CPR / NT;
-    static_assert(BN * CPR % NT == 0, "tile must split evenly over the workgroup");
+    using L = BlkTile<DP, BN>;
+    constexpr int CPW = L::NB / 4;  // 1 KiB loads per wave per tile
+    // Local copies: hipcc's host pass drops the kernel (an undefined launch
+    // stub) when a lambda in it names these static members directly.
+    constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16;
+    static_assert(L::NB % 4 == 0, "tile must split evenly over the four waves");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NKB = BN / 32;
-    __shared__ __attribute__((aligned(16))) bf16_bits sK[2][TILE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sV[2][TILE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sK0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sK1[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV1[L::SIZE];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -476,42 +483,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const bf16_bits* orr = static_cast<const bf16_bits*>(p.d_o) + qoff + hh * HALF;
 #pragma unroll
         for (int kd = 0; kd < NKD; kd++) {
-            qf[kd] = __builtin_bit_cast(bf16x8, row_ok ? *reinterpret_cast<const uint4*>(qr + kd * 8) : make_uint4(0, 0, 0, 0));
-            of[kd] = __builtin_bit_cast(bf16x8, row_ok ? *reinterpret_cast<const uint4*>(orr + kd * 8) : make_uint4(0, 0, 0, 0));
+            qf[kd] = __builtin_bit_cast(bf16x8,
+                                        row_ok ? *reinterpret_cast<const uint4*>(qr + kd * 8) : make_uint4(0, 0, 0, 0));
+            of[kd] = __builtin_bit_cast(bf16x8,
+                                        row_ok ? *reinterpret_cast<const uint4*>(orr + kd * 8) : make_uint4(0, 0, 0, 0));
         }
     }
     const long lrow = ((long)b * p.nh + head) * p.seq + tq;
     const float lse2 = row_ok ? p.lse[lrow] * kLog2e : INFINITY;
     const float dlt = row_ok ? p.delta[lrow] : 0.0f;
 
+    // Row reads (K and V rows, MFMA row l32 = key qperm(l32)) and transposed
+    // reads (K^T: tile rows 4k + hh (+2, +16, +18)), as in the forward.
+    const int rrow = L::row(qperm(l32)) + hh * HALF;
     const int G = lane >> 4, jj = lane & 15;
-    const int tr_row = 4 * (G >> 1) + (jj >> 2);
-    const int tr_cb = 2 * (G & 1) + ((jj & 3) >> 1);
-    const int tr_in = 4 * (jj & 1);
-    const int tr_sw0 = swz<DP>(tr_row), tr_sw8 = swz<DP>(tr_row + 8);
-    const int k_sw = swz<DP>(l32);
+    const int trow = L::row(4 * (jj >> 2) + hh) + 16 * (G & 1) + 4 * (jj & 3);
 
-    uint4 pk[LOADS], pv[LOADS];
-    auto gload = [&](int kt) {
+    // Tile kt's K and V rows: wave w fills load blocks w*CPW.., lane l of
+    // block b loading chunk l % CPR of tile row b + NB*(l / CPR).  Keys past
+    // the end load the last key (finite values); the causal mask removes them.
+    auto dma = [&](int kt, bf16_bits* Kd, bf16_bits* Vd) {
 #pragma unroll
-        for (int i = 0; i < LOADS; i++) {
-            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
-            const int key = kt * BN + row;
-            if (key < p.seq) {
-                pk[i] = *reinterpret_cast<const uint4*>(kg + (long)key * kvrs + col * 8);
-                pv[i] = *reinterpret_cast<const uint4*>(vg + (long)key * kvrs + col * 8);
-            } else {
-                pk[i] = make_uint4(0, 0, 0, 0);
-                pv[i] = make_uint4(0, 0, 0, 0);
-            }
-        }
-    };
-    auto lstore = [&](int st) {
-#pragma unroll
-        for (int i = 0; i < LOADS; i++) {
-            const int c = tid + i * NT, row = c / CPR, col = c % CPR;
-            *reinterpret_cast<uint4*>(&sK[st][swz_off<DP>(row, col)]) = pk[i];
-            *reinterpret_cast<uint4*>(&sV[st][swz_off<DP>(row, col)]) = pv[i];
+        for (int i = 0; i < CPW; i++) {
+            const int blk = wave * CPW + i;
+            const int r = blk + L::NB * (lane / CPR);
+            const long off = (long)min(kt * BN + r, p.seq - 1) * kvrs + (lane % CPR) * 8;
+            __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vg + off, Vd + blk * BSTRIDE, 16, 0, 0);
         }
     };
 
@@ -519,62 +517,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int i = 0; i < NDB; i++) dqt[i] = zero16();
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < n_kt; kt++) {
-        const int st = kt & 1;
-        const bool more = kt + 1 < n_kt;
-        if (more) gload(kt + 1);
+    auto step = [&](int kt, const bf16_bits* Ks, const bf16_bits* Vs, bf16_bits* Kn, bf16_bits* Vn) {
+        if (kt + 1 < n_kt) dma(kt + 1, Kn, Vn);
         const int k0 = kt * BN;
         if (wave_active && k0 <= wave_last) {
-            const bf16_bits* Ks = sK[st];
-            const bf16_bits* Vs = sV[st];
-#pragma unroll
-            for (int kb = 0; kb < NKB; kb++) {
-                const int kb0 = k0 + kb * 32;
-                if (kb0 > wave_last) break;
+            // Block kb: S^T = K Q^T and dP^T = V dO^T, then
+            // dS^T = P^T (dP^T - delta) * scale and dQ^T += K^T dS^T.
+            auto block = [&](int kb, bool masked) {
                 f32x16 sc = zero16(), dp = zero16();
-                {
-                    const bf16_bits* krow = Ks + (kb * 32 + l32) * DP;
-                    const bf16_bits* vrow = Vs + (kb * 32 + l32) * DP;
-                    bf16x8 ka[NKD], va[NKD];
 #pragma unroll
-                    for (int kd = 0; kd < NKD; kd++) {
-                        const int co = ((hh * NKD + kd) ^ k_sw) << 3;
-                        ka[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(krow + co));
-                        va[kd] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(vrow + co));
-                    }
-#pragma unroll
-                    for (int kd = 0; kd < NKD; kd++) {
-                        sc = mfma32(ka[kd], qf[kd], sc);
-                        dp = mfma32(va[kd], of[kd], dp);
-                    }
+                for (int kd = 0; kd < NKD; kd++) {
+                    const int o = rrow + kb * 2 * ROW16 + kd * 8;
+                    sc = mfma32(__builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Ks + o)), qf[kd], sc);
+                    dp = mfma32(__builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Vs + o)), of[kd], dp);
                 }
-                const bool need_mask = kb0 + 31 > t_wave;
+                const int kb0 = k0 + kb * 32;
                 float ds[16];
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     float pv_ = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lse2));
-                    if (need_mask && kb0 + (r >> 2) * 8 + hh * 4 + (r & 3) > tq) pv_ = 0.0f;
+                    if (masked && kb0 + qperm((r >> 2) * 8 + hh * 4 + (r & 3)) > tq) pv_ = 0.0f;
                     ds[r] = pv_ * (dp[r] - dlt) * p.scale;
                 }
                 const bf16x8 d0 = cvt_bf16x8(&ds[0]), d1 = cvt_bf16x8(&ds[8]);
-                // dQ^T += K^T dS^T, K^T read transposed from the K tile.
+                const bf16_bits* t0 = Ks + trow + kb * 2 * ROW16;
 #pragma unroll
                 for (int db = 0; db < NDB; db++) {
-                    const int c0 = (((db * 4 + tr_cb) ^ tr_sw0) << 3) + tr_in;
-                    const int c8 = (((db * 4 + tr_cb) ^ tr_sw8) << 3) + tr_in;
-                    const bf16_bits* k0p = Ks + (kb * 32 + tr_row) * DP;
-                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(k0p + c0), ds_read_tr16(k0p + 8 * DP + c8));
-                    const bf16x8 a1 = join_bf16x4(ds_read_tr16(k0p + 16 * DP + c0), ds_read_tr16(k0p + 24 * DP + c8));
+                    const bf16_bits* tp = t0 + db * 32;
+                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(tp), ds_read_tr16(tp + 2 * BSTRIDE));
+                    const bf16x8 a1 =
+                        join_bf16x4(ds_read_tr16(tp + ROW16), ds_read_tr16(tp + ROW16 + 2 * BSTRIDE));
                     dqt[db] = mfma32(a0, d0, dqt[db]);
                     dqt[db] = mfma32(a1, d1, dqt[db]);
                 }
+            };
+            if (k0 + BN - 1 <= t_wave) {
+                // Interior tile: every key precedes every query of the wave.
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) block(kb, false);
+            } else {
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) {
+                    const int kb0 = k0 + kb * 32;
+                    if (kb0 > wave_last) break;
+                    block(kb, kb0 + 31 > t_wave);
+                }
             }
         }
-        if (more) lstore(st ^ 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for tile kt + 1 have landed
         __syncthreads();
+    };
+
+    dma(0, sK0, sV0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int kt = 0; kt < n_kt; kt += 2) {
+        step(kt, sK0, sV0, sK1, sV1);
+        if (kt + 1 < n_kt) step(kt + 1, sK1, sV1, sK0, sV0);
     }
 
     if (!wave_active || !row_ok) return;
@@ -1000,7 +999,7 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
         if (e != hipSuccess) return e;
         TimedLaunch tl(tu.timer, kKernBwdDq, st);
         if (d.hd == 128)
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 32>), dim3(p.n_wg_q), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 64>), dim3(p.n_wg_q), dim3(256), 0, st, p);
         else
             hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, 128>), dim3(p.n_wg_q), dim3(256), 0, st, p);
         return hipGetLastError();
