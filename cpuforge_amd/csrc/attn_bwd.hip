@@ -524,21 +524,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             // Block kb: S^T = K Q^T and dP^T = V dO^T, then
             // dS^T = P^T (dP^T - delta) * scale and dQ^T += K^T dS^T.
             auto block = [&](int kb, bool masked) {
+                // S^T first, then dP^T: P = exp2(...) needs only S^T and runs
+                // while the dP^T products are in flight.
                 f32x16 sc = zero16(), dp = zero16();
 #pragma unroll
-                for (int kd = 0; kd < NKD; kd++) {
-                    const int o = rrow + kb * 2 * ROW16 + kd * 8;
-                    sc = mfma32(__builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Ks + o)), qf[kd], sc);
-                    dp = mfma32(__builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Vs + o)), of[kd], dp);
-                }
+                for (int kd = 0; kd < NKD; kd++)
+                    sc = mfma32(__builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                                             Ks + rrow + kb * 2 * ROW16 + kd * 8)),
+                                qf[kd], sc);
+#pragma unroll
+                for (int kd = 0; kd < NKD; kd++)
+                    dp = mfma32(__builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                                             Vs + rrow + kb * 2 * ROW16 + kd * 8)),
+                                of[kd], dp);
                 const int kb0 = k0 + kb * 32;
-                float ds[16];
+                float pr[16];
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    float pv_ = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lse2));
-                    if (masked && kb0 + qperm((r >> 2) * 8 + hh * 4 + (r & 3)) > tq) pv_ = 0.0f;
-                    ds[r] = pv_ * (dp[r] - dlt) * p.scale;
+                    pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lse2));
+                    if (masked && kb0 + qperm((r >> 2) * 8 + hh * 4 + (r & 3)) > tq) pr[r] = 0.0f;
                 }
+                // dS^T without the softmax scale (applied once to dQ).
+                float ds[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) ds[r] = pr[r] * (dp[r] - dlt);
                 const bf16x8 d0 = cvt_bf16x8(&ds[0]), d1 = cvt_bf16x8(&ds[8]);
                 const bf16_bits* t0 = Ks + trow + kb * 2 * ROW16;
 #pragma unroll
@@ -579,7 +588,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (!wave_active || !row_ok) return;
     float* dqrow = p.dq + qoff;
 #pragma unroll
-    for (int db = 0; db < NDB; db++) add_row_block(dqrow, dqt[db], db * 32, hh, DP, true);
+    for (int db = 0; db < NDB; db++) {
+        dqt[db] *= p.scale;  // dS was accumulated without the softmax scale
+        add_row_block(dqrow, dqt[db], db * 32, hh, DP, true);
+    }
 }
 
 // dK/dV with two specialised waves per 32-key slice: eight waves, 128 keys per

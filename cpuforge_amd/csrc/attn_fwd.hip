@@ -368,19 +368,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             };
             if (k0 + BN - 1 <= t_wave) {
                 // Interior tile: every key precedes every query of the wave.
-                // All score blocks are issued first so the softmax of one block
-                // overlaps the matrix work of the others.
+                // All score blocks are issued first; each block's max is taken
+                // on its own, so block kb's softmax runs while the products of
+                // block kb+1 (scores) and of block kb-1 (O^T) are in flight.
                 f32x16 sc[NKB];
 #pragma unroll
                 for (int kb = 0; kb < NKB; kb++) sc[kb] = scores(kb);
-                float mx = -INFINITY;
 #pragma unroll
-                for (int kb = 0; kb < NKB; kb++)
+                for (int kb = 0; kb < NKB; kb++) {
+                    float mx = -INFINITY;
 #pragma unroll
                     for (int r = 0; r < 16; r++) mx = fmaxf(mx, sc[kb][r]);
-                update_max(mx);
-#pragma unroll
-                for (int kb = 0; kb < NKB; kb++) accumulate(kb, sc[kb]);
+                    update_max(mx);
+                    accumulate(kb, sc[kb]);
+                }
             } else {
                 // Diagonal tile: causal mask, blocks past the wave's last query skipped.
 #pragma unroll
