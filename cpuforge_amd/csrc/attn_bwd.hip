@@ -502,14 +502,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // Tile kt's K and V rows: wave w fills load blocks w*CPW.., lane l of
     // block b loading chunk l % CPR of tile row b + NB*(l / CPR).  Keys past
     // the end load the last key (finite values); the causal mask removes them.
+    // The per-lane part of each offset does not change from tile to tile (the
+    // compiler keeps it out of the loop); a whole tile adds a scalar base.
+    const int wv = wave_uniform(wave);
+    constexpr int NBL = L::NB;
+    const int lane_off = NBL * (lane / CPR) * (int)kvrs + (lane % CPR) * 8;
     auto dma = [&](int kt, bf16_bits* Kd, bf16_bits* Vd) {
+        if ((kt + 1) * BN <= p.seq) {
+            const long base = (long)kt * BN * kvrs;
 #pragma unroll
-        for (int i = 0; i < CPW; i++) {
-            const int blk = wave * CPW + i;
-            const int r = blk + L::NB * (lane / CPR);
-            const long off = (long)min(kt * BN + r, p.seq - 1) * kvrs + (lane % CPR) * 8;
-            __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vg + off, Vd + blk * BSTRIDE, 16, 0, 0);
+            for (int i = 0; i < CPW; i++) {
+                const int blk = wv * CPW + i;
+                const long off = base + (long)blk * kvrs + lane_off;
+                __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vg + off, Vd + blk * BSTRIDE, 16, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPW; i++) {
+                const int blk = wv * CPW + i;
+                const int r = blk + L::NB * (lane / CPR);
+                const long off = (long)min(kt * BN + r, p.seq - 1) * kvrs + (lane % CPR) * 8;
+                __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vg + off, Vd + blk * BSTRIDE, 16, 0, 0);
+            }
         }
     };
 
@@ -673,17 +689,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // blocks w*CPW.., lane l of block b loading chunk l % CPR of tile row
     // b + NB*(l / CPR).  Rows past the end load the last row (finite values);
     // their lse is +inf and delta 0 below, so P = dS = 0 there.
+    // The per-lane part of each offset does not change from step to step;
+    // a step adds a scalar base (query tile and head).
+    const int wd = wave_uniform(wave) - 4;
+    constexpr int NBL = L::NB;
+    const int lane_off = NBL * (lane / CPR) * (int)qrs + (lane % CPR) * 8;
     auto dma = [&](int s, bf16_bits* Qd, bf16_bits* Od) {
         const int h = g * p.group + s / nq;
         const int q0 = (qt_begin + s % nq) * BM;
         if (dt < 0) return;
+        if (q0 + BM <= p.seq) {
+            const long base = (long)q0 * qrs + (long)h * DP;
 #pragma unroll
-        for (int i = 0; i < CPW; i++) {
-            const int blk = (wave - 4) * CPW + i;
-            const int r = blk + L::NB * (lane / CPR);
-            const long off = (long)min(q0 + r, p.seq - 1) * qrs + (long)h * DP + (lane % CPR) * 8;
-            __builtin_amdgcn_global_load_lds(qg + off, Qd + blk * BSTRIDE, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(og + off, Od + blk * BSTRIDE, 16, 0, 0);
+            for (int i = 0; i < CPW; i++) {
+                const int blk = wd * CPW + i;
+                const long off = base + (long)blk * qrs + lane_off;
+                __builtin_amdgcn_global_load_lds(qg + off, Qd + blk * BSTRIDE, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(og + off, Od + blk * BSTRIDE, 16, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPW; i++) {
+                const int blk = wd * CPW + i;
+                const int r = blk + L::NB * (lane / CPR);
+                const long off = (long)min(q0 + r, p.seq - 1) * qrs + (long)h * DP + (lane % CPR) * 8;
+                __builtin_amdgcn_global_load_lds(qg + off, Qd + blk * BSTRIDE, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(og + off, Od + blk * BSTRIDE, 16, 0, 0);
+            }
         }
         if (dt >= 0 && dt < 2 * BM) {
             const int t = min(q0 + lrow, p.seq - 1);

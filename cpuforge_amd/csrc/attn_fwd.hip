@@ -302,14 +302,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // Tile kt's K and V rows: wave w fills load blocks w*CPW.., lane l of
     // block b loading chunk l % CPR of tile row b + NB*(l / CPR).  Keys past
     // the end load the last key (finite values); the causal mask removes them.
+    // The per-lane part of each offset does not change from tile to tile (the
+    // compiler keeps it out of the loop); a whole tile adds a scalar base.
+    const int wv = wave_uniform(wave);
+    constexpr int NBL = L::NB;
+    const int lane_off = NBL * (lane / CPR) * (int)kvrs + (lane % CPR) * 8;
     auto dma = [&](int kt, bf16_bits* Kd, bf16_bits* Vd) {
+        if ((kt + 1) * BN <= p.seq) {
+            const long base = (long)kt * BN * kvrs;
 #pragma unroll
-        for (int i = 0; i < CPW; i++) {
-            const int blk = wave * CPW + i;
-            const int r = blk + L::NB * (lane / CPR);
-            const long off = (long)min(kt * BN + r, p.seq - 1) * kvrs + (lane % CPR) * 8;
-            __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vg + off, Vd + blk * BSTRIDE, 16, 0, 0);
+            for (int i = 0; i < CPW; i++) {
+                const int blk = wv * CPW + i;
+                const long off = base + (long)blk * kvrs + lane_off;
+                __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vg + off, Vd + blk * BSTRIDE, 16, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPW; i++) {
+                const int blk = wv * CPW + i;
+                const int r = blk + L::NB * (lane / CPR);
+                const long off = (long)min(kt * BN + r, p.seq - 1) * kvrs + (lane % CPR) * 8;
+                __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vg + off, Vd + blk * BSTRIDE, 16, 0, 0);
+            }
         }
     };
 
@@ -319,7 +335,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float m2 = -INFINITY, lsum = 0.0f;
 
     auto step = [&](int kt, const bf16_bits* Ks, const bf16_bits* Vs, bf16_bits* Kn, bf16_bits* Vn) {
-        if (kt + 1 < n_kt) dma(kt + 1, Kn, Vn);
+        // The next tile's loads are issued after this tile's score products:
+        // issuing stalls the wave until the load queue takes them, and the
+        // products then run meanwhile.
+        const bool more = kt + 1 < n_kt;
         const int k0 = kt * BN;
         if (wave_active && k0 <= wave_last) {
             // S^T block kb: keys k0 + kb*32 + qperm([0,32)) x this wave's 32 queries.
@@ -374,6 +393,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 f32x16 sc[NKB];
 #pragma unroll
                 for (int kb = 0; kb < NKB; kb++) sc[kb] = scores(kb);
+                if (more) dma(kt + 1, Kn, Vn);
 #pragma unroll
                 for (int kb = 0; kb < NKB; kb++) {
                     float mx = -INFINITY;
@@ -384,6 +404,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 }
             } else {
                 // Diagonal tile: causal mask, blocks past the wave's last query skipped.
+                if (more) dma(kt + 1, Kn, Vn);
 #pragma unroll
                 for (int kb = 0; kb < NKB; kb++) {
                     const int kb0 = k0 + kb * 32;
@@ -405,6 +426,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     accumulate(kb, sc);
                 }
             }
+        } else if (more) {
+            dma(kt + 1, Kn, Vn);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for tile kt + 1 have landed
         __syncthreads();

@@ -51,6 +51,11 @@ __device__ __forceinline__ f32x16 mfma32(float a, float b, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// A wave-uniform value moved to a scalar register.  Called through this
+// device function: hipcc's host pass drops a kernel (an undefined launch stub)
+// whose body names the builtin directly.
+__device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
 // Compile-time tag selecting one code path of a kernel (a wave role).
 template <bool B>
 struct RoleTag {
