@@ -429,21 +429,25 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams p) {
 // The contraction order over heads and tiles is fixed, so results stay
 // bitwise reproducible.
 
-// dQ: the forward's decomposition (a wave owns 32 queries of one head, four
+// Waves per workgroup of the fast dQ kernel.  All of them share each K/V
+// tile; four (two workgroups per CU) measured faster than eight (one).
+constexpr int kDqWaves = 4;
+
+// dQ: the forward's decomposition (a wave owns 32 queries of one head, NW
 // waves per workgroup); K/V tiles of BN keys are shared by the workgroup and
 // go straight from global memory into double-buffered blocked LDS tiles
-// (global_load_lds, issued one tile ahead by all four waves).  MFMA row i of
+// (global_load_lds, issued one tile ahead by all the waves).  MFMA row i of
 // a 32-key block is key qperm(i) of the block (see BlkTile).
-template <int DP, int BN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq_bf16_kernel(
+template <int DP, int BN, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq_bf16_kernel(
     const BwdParams p) {
     constexpr int CPR = DP / 8;
     using L = BlkTile<DP, BN>;
-    constexpr int CPW = L::NB / 4;  // 1 KiB loads per wave per tile
+    constexpr int CPW = L::NB / NW;  // 1 KiB loads per wave per tile
     // Local copies: hipcc's host pass drops the kernel (an undefined launch
     // stub) when a lambda in it names these static members directly.
     constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16;
-    static_assert(L::NB % 4 == 0, "tile must split evenly over the four waves");
+    static_assert(L::NB % NW == 0, "tile must split evenly over the waves");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NKB = BN / 32;
     __shared__ __attribute__((aligned(16))) bf16_bits sK0[L::SIZE];
     __shared__ __attribute__((aligned(16))) bf16_bits sK1[L::SIZE];
@@ -1015,9 +1019,9 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
     p.g_vec_ok = (d.hd % 4 == 0) && ((uintptr_t)dq % al == 0) && ((uintptr_t)dk % al == 0) && ((uintptr_t)dv % al == 0);
     p.xcd = tu.xcd_remap;
     if (dt == kBF16 && p.vec_ok && p.g_vec_ok && (d.hd == 64 || d.hd == 128) && tu.bwd_kv_waves == 0) {
-        // Fast paths: four waves per workgroup in both kernels.
+        // Fast paths: the dQ kernel runs kDqWaves waves per workgroup, dK/dV eight.
         p.hpw = p.group % 4 == 0 ? 4 : p.group % 2 == 0 ? 2 : 1;
-        p.tpw = 4 / p.hpw;
+        p.tpw = kDqWaves / p.hpw;
         p.n_sub = p.group / p.hpw;
         p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
         nq_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
@@ -1043,9 +1047,11 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
         if (e != hipSuccess) return e;
         TimedLaunch tl(tu.timer, kKernBwdDq, st);
         if (d.hd == 128)
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 64>), dim3(p.n_wg_q), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 64, kDqWaves>), dim3(p.n_wg_q), dim3(64 * kDqWaves), 0, st,
+                               p);
         else
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, 128>), dim3(p.n_wg_q), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, 128, kDqWaves>), dim3(p.n_wg_q), dim3(64 * kDqWaves), 0, st,
+                               p);
         return hipGetLastError();
     }
     const int q_waves = p.hpw * p.tpw;

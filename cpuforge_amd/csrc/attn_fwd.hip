@@ -224,9 +224,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams p) {
 
 // ---------------------------------------------------------------------------
 // Fast path: bf16 inputs, head_dim == DP (64 or 128), 16-byte aligned rows.
-// Four waves per workgroup, the same (tile, heads) decomposition as above.
+// NW waves per workgroup, the same (tile, heads) decomposition as above.
 // K/V tiles of BN keys go straight from global memory into double-buffered
-// blocked LDS tiles (global_load_lds, issued one tile ahead by all four
+// blocked LDS tiles (global_load_lds, issued one tile ahead by all the
 // waves), so each tile costs one barrier.  S^T = K Q^T reads K rows with
 // ds_read_b128; O^T += V^T P^T reads V^T straight from the V tile with
 // transposed reads (ds_read_b64_tr_b16).  MFMA row i of a 32-key block is key
@@ -236,17 +236,20 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams p) {
 // rescaled only on those tiles.  O = acc / sum and lse = m + log2(sum) do not
 // depend on which shift was used.
 constexpr float kLazyRescale = 8.0f;
+// Waves per workgroup of the fast forward.  All of them share each K/V tile;
+// four (two workgroups per CU) measured faster than eight (one).
+constexpr int kFastWaves = 4;
 
-template <int DP, int BN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_bf16_kernel(
+template <int DP, int BN, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_bf16_kernel(
     const FwdParams p) {
     constexpr int CPR = DP / 8;  // 16-byte chunks per row
     using L = BlkTile<DP, BN>;
-    constexpr int CPW = L::NB / 4;  // 1 KiB loads per wave per tile
+    constexpr int CPW = L::NB / NW;  // 1 KiB loads per wave per tile
     // Local copies: hipcc's host pass drops the kernel (an undefined launch
     // stub) when a lambda in it names these static members directly.
     constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16;
-    static_assert(L::NB % 4 == 0, "tile must split evenly over the four waves");
+    static_assert(L::NB % NW == 0, "tile must split evenly over the waves");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NKB = BN / 32;
     __shared__ __attribute__((aligned(16))) bf16_bits sK0[L::SIZE];
     __shared__ __attribute__((aligned(16))) bf16_bits sK1[L::SIZE];
@@ -515,9 +518,10 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
     p.xcd = tu.xcd_remap;
     if (dt == kBF16 && p.vec_ok && p.o_vec_ok && (d.hd == 64 || d.hd == 128) && tu.fwd_heads_per_wg == 0 &&
         tu.fwd_tblocks_per_wg == 0) {
-        // Fast path: four waves per workgroup, heads per workgroup in {4, 2, 1}.
+        // Fast path: kFastWaves waves per workgroup, heads per workgroup in
+        // {4, 2, 1}, the rest of the waves on further 32-query blocks.
         p.hpw = p.group % 4 == 0 ? 4 : p.group % 2 == 0 ? 2 : 1;
-        p.tpw = 4 / p.hpw;
+        p.tpw = kFastWaves / p.hpw;
         p.n_sub = p.group / p.hpw;
         p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
         n_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
@@ -525,9 +529,11 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
         p.n_wg = (int)n_wg;
         TimedLaunch tl(tu.timer, kKernFwd, st);
         if (d.hd == 128)
-            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 64>), dim3(p.n_wg), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 64, kFastWaves>), dim3(p.n_wg), dim3(64 * kFastWaves), 0, st,
+                               p);
         else
-            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 128>), dim3(p.n_wg), dim3(256), 0, st, p);
+            hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 128, kFastWaves>), dim3(p.n_wg), dim3(64 * kFastWaves), 0, st,
+                               p);
         return hipGetLastError();
     }
     const int nwaves = p.hpw * p.tpw;
