@@ -35,6 +35,7 @@ struct ProParams {
     int half, pos0;
     int seq, nh, nkv, hd;
     long rows_q, rows_k;
+    int srows;  // rows per block of the staged kernel
 };
 
 template <typename T>
@@ -71,6 +72,75 @@ __global__ __launch_bounds__(256) void prologue_fwd_kernel(const ProParams p) {
     }
 }
 
+// The same rows, restructured for bandwidth: a block of srows rows of q or k
+// (a contiguous range of memory) per workgroup of 256 threads.
+//   - Qwen3 only: the rows are staged in LDS with coalesced loads and one lane
+//     per row runs the sequential sum of squares above (LDS rows are D+1
+//     floats apart, D even, so those lanes hit distinct banks); rstd goes to
+//     LDS and to global memory.
+//   - The rotation is elementwise: each thread takes column pairs (i, i+D/2)
+//     of the block's rows, consecutive threads consecutive i, reading x (from
+//     LDS or straight from global memory) and writing y with coalesced
+//     accesses.  Every element's expression is the one above, so the result
+//     is unchanged bit for bit.
+constexpr int kStageMaxRows = 64;
+constexpr int kStageMaxD = 256;
+// Rows per block, keeping a block's LDS within 64 KiB.
+static int stage_rows(int hd, int nbuf) {
+    const int r = 65536 / (nbuf * (hd + 1) * (int)sizeof(float));
+    return r < kStageMaxRows ? r : kStageMaxRows;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void prologue_fwd_staged_kernel(const ProParams p) {
+#pragma clang fp contract(off)
+    extern __shared__ float stage[];  // Qwen3: [srows][hd + 1] rows, then [srows] rstd
+    const int tid = threadIdx.x;
+    const long nbq = (p.rows_q + p.srows - 1) / p.srows;
+    long blk = blockIdx.x;
+    const bool isq = blk < nbq;
+    if (!isq) blk -= nbq;
+    const long rows = isq ? p.rows_q : p.rows_k;
+    const long r0 = blk * p.srows;
+    const int nr = (int)min((long)p.srows, rows - r0);
+    const int D = p.hd, LD = p.hd + 1, half = p.half;
+    const int heads = isq ? p.nh : p.nkv;
+    const float* x = (isq ? p.q_pre : p.k_pre) + r0 * D;
+    const float* w = isq ? p.qw : p.kw;
+    float* srstd = stage + p.srows * LD;
+    if (w) {
+        for (int j = tid; j < nr * D; j += 256) stage[(j / D) * LD + j % D] = x[j];
+        __syncthreads();
+        if (tid < nr) {
+            const float* xr = stage + tid * LD;
+            float ss = 0.0f;
+            for (int i = 0; i < D; i++) ss += xr[i] * xr[i];
+            const float ms = ss / (float)D;
+            const float inv = 1.0f / sqrtf(ms + p.eps);
+            srstd[tid] = inv;
+            (isq ? p.q_rstd : p.k_rstd)[r0 + tid] = inv;
+        }
+        __syncthreads();
+    }
+    T* y = static_cast<T*>(isq ? p.q_out : p.k_out) + r0 * D;
+    for (int j = tid; j < nr * half; j += 256) {
+        const int row = j / half, i = j % half;
+        const int t = (int)(((r0 + row) / heads) % p.seq);
+        float x1, x2;
+        if (w) {
+            const float inv = srstd[row];
+            x1 = stage[row * LD + i] * inv * w[i];
+            x2 = stage[row * LD + i + half] * inv * w[i + half];
+        } else {
+            x1 = x[(long)row * D + i];
+            x2 = x[(long)row * D + i + half];
+        }
+        const float c = p.cos[(long)(p.pos0 + t) * half + i], sn = p.sin[(long)(p.pos0 + t) * half + i];
+        y[(long)row * D + i] = from_f32<T>(x1 * c - x2 * sn);
+        y[(long)row * D + i + half] = from_f32<T>(x2 * c + x1 * sn);
+    }
+}
+
 struct ProBwdParams {
     const float* dq;
     const float* dk;
@@ -91,6 +161,7 @@ struct ProBwdParams {
     int seq, nh, nkv, hd;
     long rows_q, rows_k;
     int chunk_rows, n_chunks_q, n_chunks_k;
+    int srows;  // rows per block of the staged kernel
 };
 
 // Inverse rotation of element i of a gradient row (sine negated, as
@@ -135,6 +206,70 @@ __global__ __launch_bounds__(256) void prologue_bwd_rows_kernel(const ProBwdPara
     }
 }
 
+// The same rows restructured like prologue_fwd_staged_kernel: Qwen3 stages
+// the gradient and input rows in LDS and runs the sequential dot product with
+// one lane per row; the rest is elementwise over column pairs (i, i+D/2),
+// with the expressions above and a coalesced += into dq_pre/dk_pre.
+__global__ __launch_bounds__(256) void prologue_bwd_rows_staged_kernel(const ProBwdParams p) {
+#pragma clang fp contract(off)
+    extern __shared__ float stage[];  // Qwen3: [srows][hd + 1] gradient rows, [srows][hd + 1] input rows, [srows] mean
+    const int tid = threadIdx.x;
+    const long nbq = (p.rows_q + p.srows - 1) / p.srows;
+    long blk = blockIdx.x;
+    const bool isq = blk < nbq;
+    if (!isq) blk -= nbq;
+    const long rows = isq ? p.rows_q : p.rows_k;
+    const long r0 = blk * p.srows;
+    const int nr = (int)min((long)p.srows, rows - r0);
+    const int D = p.hd, LD = p.hd + 1, half = p.half;
+    const int heads = isq ? p.nh : p.nkv;
+    const float* w = isq ? p.qw : p.kw;
+    const float* g = (isq ? p.dq : p.dk) + r0 * D;
+    const float* x = (isq ? p.q_pre : p.k_pre) + r0 * D;
+    const float* rstd = w ? (isq ? p.q_rstd : p.k_rstd) + r0 : nullptr;
+    float* sg = stage;
+    float* sx = stage + p.srows * LD;
+    float* smean = stage + 2 * p.srows * LD;
+    if (w) {
+        for (int j = tid; j < nr * D; j += 256) {
+            sg[(j / D) * LD + j % D] = g[j];
+            sx[(j / D) * LD + j % D] = x[j];
+        }
+        __syncthreads();
+        if (tid < nr) {
+            const long r = r0 + tid;
+            const int t = (int)((r / heads) % p.seq);
+            const float* cs = p.cos + (long)(p.pos0 + t) * half;
+            const float* sn = p.sin + (long)(p.pos0 + t) * half;
+            const float* gr = sg + tid * LD;
+            const float* xr = sx + tid * LD;
+            const float inv = rstd[tid];
+            float dot = 0.0f;
+            for (int i = 0; i < D; i++) dot += unrotate(gr, cs, sn, i, half) * w[i] * xr[i] * inv;
+            smean[tid] = dot / (float)D;
+        }
+        __syncthreads();
+    }
+    float* dx = (isq ? p.dq_pre : p.dk_pre) + r0 * D;
+    for (int j = tid; j < nr * half; j += 256) {
+        const int row = j / half, i = j % half;
+        const int t = (int)(((r0 + row) / heads) % p.seq);
+        const float* cs = p.cos + (long)(p.pos0 + t) * half;
+        const float* sn = p.sin + (long)(p.pos0 + t) * half;
+        const float* gr = w ? sg + row * LD : g + (long)row * D;
+        const float dy1 = unrotate(gr, cs, sn, i, half), dy2 = unrotate(gr, cs, sn, i + half, half);
+        float o1 = dy1, o2 = dy2;
+        if (w) {
+            const float inv = rstd[row], mean = smean[row];
+            const float xh1 = sx[row * LD + i] * inv, xh2 = sx[row * LD + i + half] * inv;
+            o1 = inv * (dy1 * w[i] - xh1 * mean);
+            o2 = inv * (dy2 * w[i + half] - xh2 * mean);
+        }
+        dx[(long)row * D + i] += o1;
+        dx[(long)row * D + i + half] += o2;
+    }
+}
+
 // partial[which][chunk][i] = sum over the chunk's rows of dy[row][i] * xhat[row][i].
 __global__ __launch_bounds__(256) void prologue_bwd_dw_partial_kernel(const ProBwdParams p) {
 #pragma clang fp contract(off)
@@ -163,16 +298,27 @@ __global__ __launch_bounds__(256) void prologue_bwd_dw_partial_kernel(const ProB
     p.partial[slot * p.hd + i] = acc;
 }
 
+// dw[i] += sum over chunks of partial[..][chunk][i]: one workgroup per (q or k,
+// i).  Thread t adds chunks t, t+256, ... in order, then a fixed tree over the
+// 256 thread sums, so the result does not depend on scheduling.
 __global__ __launch_bounds__(256) void prologue_bwd_dw_reduce_kernel(const ProBwdParams p) {
-    const int i = threadIdx.x;
-    if (i >= p.hd) return;
-    const bool isq = blockIdx.x == 0;
+#pragma clang fp contract(off)
+    __shared__ float red[256];
+    const int tid = threadIdx.x;
+    const int i = blockIdx.x % p.hd;
+    const bool isq = blockIdx.x < p.hd;
     const int n = isq ? p.n_chunks_q : p.n_chunks_k;
     const long base = isq ? 0 : p.n_chunks_q;
     float acc = 0.0f;
-    for (int c = 0; c < n; c++) acc += p.partial[(base + c) * p.hd + i];
-    float* dw = isq ? p.dqw : p.dkw;
-    dw[i] += acc;
+    for (int c = tid; c < n; c += 256) acc += p.partial[(base + c) * p.hd + i];
+    red[tid] = acc;
+    __syncthreads();
+#pragma unroll
+    for (int w = 128; w >= 1; w >>= 1) {
+        if (tid < w) red[tid] = red[tid] + red[tid + w];
+        __syncthreads();
+    }
+    if (tid == 0) (isq ? p.dqw : p.dkw)[i] += red[0];
 }
 
 __global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
@@ -217,8 +363,19 @@ hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, cons
     p.rows_k = (long)d.batch * d.seq * d.nkv;
     const long rows = p.rows_q + p.rows_k;
     if (rows == 0) return hipSuccess;
-    const unsigned grid = (unsigned)((rows + 255) / 256);
     TimedLaunch tl(timer, kKernProFwd, st);
+    if (d.hd <= kStageMaxD) {
+        p.srows = stage_rows(d.hd + 1, 1);  // the rstd column counted as one more float per row
+        const long blocks = (p.rows_q + p.srows - 1) / p.srows + (p.rows_k + p.srows - 1) / p.srows;
+        if (blocks > 0x7fffffffL) return hipErrorInvalidConfiguration;
+        const size_t lds = pr.qw ? (size_t)p.srows * (d.hd + 2) * sizeof(float) : 0;
+        if (dt == kBF16)
+            hipLaunchKernelGGL(prologue_fwd_staged_kernel<bf16_bits>, dim3((unsigned)blocks), dim3(256), lds, st, p);
+        else
+            hipLaunchKernelGGL(prologue_fwd_staged_kernel<float>, dim3((unsigned)blocks), dim3(256), lds, st, p);
+        return hipGetLastError();
+    }
+    const unsigned grid = (unsigned)((rows + 255) / 256);
     if (dt == kBF16)
         hipLaunchKernelGGL(prologue_fwd_kernel<bf16_bits>, dim3(grid), dim3(256), 0, st, p);
     else
@@ -226,7 +383,7 @@ hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, cons
     return hipGetLastError();
 }
 
-static constexpr int kChunkRows = 256;
+static constexpr int kChunkRows = 32;  // rows per partial sum of the norm-gain gradient
 
 size_t prologue_bwd_scratch_floats(const Dims& d) {
     const long rq = (long)d.batch * d.seq * d.nh, rk = (long)d.batch * d.seq * d.nkv;
@@ -268,13 +425,21 @@ hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* d
     const long rows = p.rows_q + p.rows_k;
     if (rows == 0) return hipSuccess;
     TimedLaunch tl(timer, kKernProBwd, st);
-    hipLaunchKernelGGL(prologue_bwd_rows_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, p);
+    if (d.hd <= kStageMaxD) {
+        p.srows = stage_rows(d.hd + 1, 2);  // the mean column counted as one more float per row
+        const long blocks = (p.rows_q + p.srows - 1) / p.srows + (p.rows_k + p.srows - 1) / p.srows;
+        if (blocks > 0x7fffffffL) return hipErrorInvalidConfiguration;
+        const size_t lds = pr.qw ? (2 * (size_t)p.srows * (d.hd + 1) + p.srows) * sizeof(float) : 0;
+        hipLaunchKernelGGL(prologue_bwd_rows_staged_kernel, dim3((unsigned)blocks), dim3(256), lds, st, p);
+    } else {
+        hipLaunchKernelGGL(prologue_bwd_rows_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !pr.qw) return e;
     hipLaunchKernelGGL(prologue_bwd_dw_partial_kernel, dim3(p.n_chunks_q + p.n_chunks_k), dim3(256), 0, st, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(prologue_bwd_dw_reduce_kernel, dim3(2), dim3(256), 0, st, p);
+    hipLaunchKernelGGL(prologue_bwd_dw_reduce_kernel, dim3(2 * d.hd), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 
