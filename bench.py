@@ -72,6 +72,9 @@ def parse():
                     help="run one plain device copy of MIB MiB before timing (calibrates rocprofv3 byte counters)")
     ap.add_argument("--host-slices", action="store_true",
                     help="time the drop-in host-slice entry points instead (PCIe-inclusive; not the headline value)")
+    ap.add_argument("--fused", action="store_true",
+                    help="time the Layer-level path instead: q/k prologue (RoPE, Qwen3 norm) + attention, forward "
+                         "and backward (cfattn_fused_fwd/bwd); prints its own JSON line")
     ap.add_argument("--traffic-file", default=None,
                     help="rocprofv3 traffic summary to read `traffic` from (default: profiles/ match)")
     return ap.parse_args()
@@ -162,6 +165,57 @@ def host_slices(a, mode):
           flush=True)
 
 
+def fused_layer(a, mode):
+    """Times cfattn_fused_fwd + cfattn_fused_bwd: Layer::forward/backward's
+    attention part (crates/model/src/layer.rs:104-121, 183-206): pre-RoPE
+    q/k in f32 -> [q/k RMSNorm] -> RoPE -> attention, and back to dq_pre,
+    dk_pre, dv (and the norm-gain gradients).  Prints its own JSON line, with
+    the time of each kernel."""
+    import torch
+
+    import cpuforge_amd as cf
+    from cpuforge_amd import device as dev
+    B, S, Hq, Hk, D, theta, scaling, qk_norm = CONFIGS[a.config]
+    ctx = cf.Context(0)
+    torch.manual_seed(1234)
+    dt = torch.bfloat16 if mode == "bf16" else torch.float32
+    q_pre = torch.randn(B, S, Hq, D, device="cuda")
+    k_pre = torch.randn(B, S, Hk, D, device="cuda")
+    v = torch.randn(B, S, Hk, D, device="cuda").to(dt)
+    d_o = torch.randn(B, S, Hq, D, device="cuda").to(dt)
+    sc = cf.Llama3Scaling(*scaling) if scaling else None
+    qn = kn = None
+    if qk_norm:
+        qn = (1.0 + 0.02 * torch.randn(D, device="cuda")).float()
+        kn = (1.0 + 0.02 * torch.randn(D, device="cuda")).float()
+    pr = dev.DeviceRope(cf.RopeCache(D, S, theta, sc), "cuda", 0, qn, kn, 1e-6)
+    dq_pre, dk_pre = torch.zeros_like(q_pre), torch.zeros_like(k_pre)
+    dv = torch.zeros(B, S, Hk, D, device="cuda")
+
+    def step():
+        o, lse, q, k, qr, kr = dev.fused_fwd(q_pre, k_pre, v, pr, ctx=ctx)
+        dev.fused_bwd(d_o, q_pre, k_pre, q, k, v, o, lse, qr, kr, pr, dq_pre, dk_pre, dv, ctx=ctx)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    ctx.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    per = (time.perf_counter() - t0) / a.steps
+    kernels = {n: round(ms / max(1, c), 4) for n, (ms, c) in ctx.profile_read().items() if c}
+    ctx.close()
+    flops = 7.0 * B * Hq * D * S * (S + 1)
+    print(json.dumps({"metric": "Layer attention fwd+bwd (prologue + attention) TFLOP/s, attention FLOPs only",
+                      "value": round(flops / per / 1e12, 3), "unit": "TFLOP/s", "ms_per_step": round(per * 1e3, 3),
+                      "steps": a.steps, "warmup": a.warmup, "dtype": mode, "higher_is_better": True,
+                      "kernels_ms": kernels,
+                      "config": {"workload": WORKLOAD[a.config], "config": a.config, "path": "cfattn_fused_fwd/bwd"}}),
+          flush=True)
+
+
 def main():
     a = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -173,6 +227,9 @@ def main():
     B, S, Hq, Hk, D, theta, scaling, qk_norm = CONFIGS[a.config]
     if a.host_slices:
         host_slices(a, mode)
+        return
+    if a.fused:
+        fused_layer(a, mode)
         return
 
     import torch

@@ -91,6 +91,24 @@ static int stage_rows(int hd, int nbuf) {
     return r < kStageMaxRows ? r : kStageMaxRows;
 }
 
+// Copy n consecutive floats of `src` (rows of D) into LDS rows LD apart, 256
+// threads, eight loads in flight per thread before their stores.
+__device__ __forceinline__ void stage_rows_to_lds(float* dst, const float* src, int n, int D, int LD, int tid) {
+    for (int j0 = 0; j0 < n; j0 += 256 * 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u * 256 + tid;
+            v[u] = j < n ? src[j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u * 256 + tid;
+            if (j < n) dst[(j / D) * LD + j % D] = v[u];
+        }
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void prologue_fwd_staged_kernel(const ProParams p) {
 #pragma clang fp contract(off)
@@ -109,7 +127,7 @@ __global__ __launch_bounds__(256) void prologue_fwd_staged_kernel(const ProParam
     const float* w = isq ? p.qw : p.kw;
     float* srstd = stage + p.srows * LD;
     if (w) {
-        for (int j = tid; j < nr * D; j += 256) stage[(j / D) * LD + j % D] = x[j];
+        stage_rows_to_lds(stage, x, nr * D, D, LD, tid);
         __syncthreads();
         if (tid < nr) {
             const float* xr = stage + tid * LD;
@@ -206,13 +224,15 @@ __global__ __launch_bounds__(256) void prologue_bwd_rows_kernel(const ProBwdPara
     }
 }
 
-// The same rows restructured like prologue_fwd_staged_kernel: Qwen3 stages
-// the gradient and input rows in LDS and runs the sequential dot product with
-// one lane per row; the rest is elementwise over column pairs (i, i+D/2),
-// with the expressions above and a coalesced += into dq_pre/dk_pre.
+// The same rows restructured like prologue_fwd_staged_kernel, elementwise
+// over column pairs (i, i+D/2) with the expressions above and a coalesced +=
+// into dq_pre/dk_pre.  Qwen3 first writes the unrotated gradient dy and stages
+// the input rows and w in LDS, then runs the sequential dot product with one
+// lane per row reading only LDS.
 __global__ __launch_bounds__(256) void prologue_bwd_rows_staged_kernel(const ProBwdParams p) {
 #pragma clang fp contract(off)
-    extern __shared__ float stage[];  // Qwen3: [srows][hd + 1] gradient rows, [srows][hd + 1] input rows, [srows] mean
+    // Qwen3: [srows][hd + 1] dy rows, [srows][hd + 1] input rows, [srows] mean, [hd] w
+    extern __shared__ float stage[];
     const int tid = threadIdx.x;
     const long nbq = (p.rows_q + p.srows - 1) / p.srows;
     long blk = blockIdx.x;
@@ -227,46 +247,63 @@ __global__ __launch_bounds__(256) void prologue_bwd_rows_staged_kernel(const Pro
     const float* g = (isq ? p.dq : p.dk) + r0 * D;
     const float* x = (isq ? p.q_pre : p.k_pre) + r0 * D;
     const float* rstd = w ? (isq ? p.q_rstd : p.k_rstd) + r0 : nullptr;
-    float* sg = stage;
+    float* sdy = stage;
     float* sx = stage + p.srows * LD;
     float* smean = stage + 2 * p.srows * LD;
-    if (w) {
-        for (int j = tid; j < nr * D; j += 256) {
-            sg[(j / D) * LD + j % D] = g[j];
-            sx[(j / D) * LD + j % D] = x[j];
-        }
-        __syncthreads();
-        if (tid < nr) {
-            const long r = r0 + tid;
-            const int t = (int)((r / heads) % p.seq);
-            const float* cs = p.cos + (long)(p.pos0 + t) * half;
-            const float* sn = p.sin + (long)(p.pos0 + t) * half;
-            const float* gr = sg + tid * LD;
-            const float* xr = sx + tid * LD;
-            const float inv = rstd[tid];
-            float dot = 0.0f;
-            for (int i = 0; i < D; i++) dot += unrotate(gr, cs, sn, i, half) * w[i] * xr[i] * inv;
-            smean[tid] = dot / (float)D;
-        }
-        __syncthreads();
-    }
+    float* sw = smean + p.srows;
     float* dx = (isq ? p.dq_pre : p.dk_pre) + r0 * D;
-    for (int j = tid; j < nr * half; j += 256) {
-        const int row = j / half, i = j % half;
+    auto dy_pair = [&](int row, int i, float& dy1, float& dy2) {
         const int t = (int)(((r0 + row) / heads) % p.seq);
         const float* cs = p.cos + (long)(p.pos0 + t) * half;
         const float* sn = p.sin + (long)(p.pos0 + t) * half;
-        const float* gr = w ? sg + row * LD : g + (long)row * D;
-        const float dy1 = unrotate(gr, cs, sn, i, half), dy2 = unrotate(gr, cs, sn, i + half, half);
-        float o1 = dy1, o2 = dy2;
-        if (w) {
-            const float inv = rstd[row], mean = smean[row];
-            const float xh1 = sx[row * LD + i] * inv, xh2 = sx[row * LD + i + half] * inv;
-            o1 = inv * (dy1 * w[i] - xh1 * mean);
-            o2 = inv * (dy2 * w[i + half] - xh2 * mean);
+        const float* gr = g + (long)row * D;
+        dy1 = unrotate(gr, cs, sn, i, half);
+        dy2 = unrotate(gr, cs, sn, i + half, half);
+    };
+    if (!w) {
+        for (int j = tid; j < nr * half; j += 256) {
+            const int row = j / half, i = j % half;
+            float dy1, dy2;
+            dy_pair(row, i, dy1, dy2);
+            dx[(long)row * D + i] += dy1;
+            dx[(long)row * D + i + half] += dy2;
         }
-        dx[(long)row * D + i] += o1;
-        dx[(long)row * D + i + half] += o2;
+        return;
+    }
+    stage_rows_to_lds(sx, x, nr * D, D, LD, tid);
+    for (int i = tid; i < D; i += 256) sw[i] = w[i];
+    for (int j = tid; j < nr * half; j += 256) {
+        const int row = j / half, i = j % half;
+        float dy1, dy2;
+        dy_pair(row, i, dy1, dy2);
+        sdy[row * LD + i] = dy1;
+        sdy[row * LD + i + half] = dy2;
+    }
+    __syncthreads();
+    if (tid < nr) {
+        const float* dyr = sdy + tid * LD;
+        const float* xr = sx + tid * LD;
+        const float inv = rstd[tid];
+        float dot = 0.0f;
+        for (int i = 0; i < D; i++) dot += dyr[i] * sw[i] * xr[i] * inv;
+        smean[tid] = dot / (float)D;
+    }
+    // This block's share of the norm-gain gradient, in row order:
+    // partial[block][i] = sum over its rows of dy * xhat (reduced over blocks
+    // by prologue_bwd_dw_reduce_kernel).
+    for (int i = tid; i < D; i += 256) {
+        float acc = 0.0f;
+        for (int row = 0; row < nr; row++) acc += sdy[row * LD + i] * (sx[row * LD + i] * rstd[row]);
+        p.partial[(isq ? blk : nbq + blk) * D + i] = acc;
+    }
+    __syncthreads();
+    for (int j = tid; j < nr * half; j += 256) {
+        const int row = j / half, i = j % half;
+        const float inv = rstd[row], mean = smean[row];
+        const float dy1 = sdy[row * LD + i], dy2 = sdy[row * LD + i + half];
+        const float xh1 = sx[row * LD + i] * inv, xh2 = sx[row * LD + i + half] * inv;
+        dx[(long)row * D + i] += inv * (dy1 * sw[i] - xh1 * mean);
+        dx[(long)row * D + i + half] += inv * (dy2 * sw[i + half] - xh2 * mean);
     }
 }
 
@@ -383,11 +420,16 @@ hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, cons
     return hipGetLastError();
 }
 
-static constexpr int kChunkRows = 32;  // rows per partial sum of the norm-gain gradient
+static constexpr int kChunkRows = 32;  // rows per partial sum of the norm-gain gradient (row-per-thread path)
+
+// Rows per partial sum of the norm-gain gradient: the staged kernel's block,
+// else kChunkRows.
+static int dw_chunk_rows(int hd) { return hd <= kStageMaxD ? stage_rows(hd + 2, 2) : kChunkRows; }
 
 size_t prologue_bwd_scratch_floats(const Dims& d) {
     const long rq = (long)d.batch * d.seq * d.nh, rk = (long)d.batch * d.seq * d.nkv;
-    const long nq = (rq + kChunkRows - 1) / kChunkRows, nk = (rk + kChunkRows - 1) / kChunkRows;
+    const long cr = dw_chunk_rows(d.hd);
+    const long nq = (rq + cr - 1) / cr, nk = (rk + cr - 1) / cr;
     return (size_t)((nq + nk) * d.hd);
 }
 
@@ -419,26 +461,28 @@ hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* d
     p.hd = d.hd;
     p.rows_q = (long)d.batch * d.seq * d.nh;
     p.rows_k = (long)d.batch * d.seq * d.nkv;
-    p.chunk_rows = kChunkRows;
-    p.n_chunks_q = (int)((p.rows_q + kChunkRows - 1) / kChunkRows);
-    p.n_chunks_k = (int)((p.rows_k + kChunkRows - 1) / kChunkRows);
+    p.chunk_rows = dw_chunk_rows(d.hd);
+    p.n_chunks_q = (int)((p.rows_q + p.chunk_rows - 1) / p.chunk_rows);
+    p.n_chunks_k = (int)((p.rows_k + p.chunk_rows - 1) / p.chunk_rows);
     const long rows = p.rows_q + p.rows_k;
     if (rows == 0) return hipSuccess;
     TimedLaunch tl(timer, kKernProBwd, st);
     if (d.hd <= kStageMaxD) {
-        p.srows = stage_rows(d.hd + 1, 2);  // the mean column counted as one more float per row
+        p.srows = p.chunk_rows;  // stage_rows(hd + 2, 2): the mean column and w counted as more floats per row
         const long blocks = (p.rows_q + p.srows - 1) / p.srows + (p.rows_k + p.srows - 1) / p.srows;
         if (blocks > 0x7fffffffL) return hipErrorInvalidConfiguration;
-        const size_t lds = pr.qw ? (2 * (size_t)p.srows * (d.hd + 1) + p.srows) * sizeof(float) : 0;
+        const size_t lds = pr.qw ? (2 * (size_t)p.srows * (d.hd + 1) + p.srows + d.hd) * sizeof(float) : 0;
         hipLaunchKernelGGL(prologue_bwd_rows_staged_kernel, dim3((unsigned)blocks), dim3(256), lds, st, p);
     } else {
         hipLaunchKernelGGL(prologue_bwd_rows_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, p);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !pr.qw) return e;
-    hipLaunchKernelGGL(prologue_bwd_dw_partial_kernel, dim3(p.n_chunks_q + p.n_chunks_k), dim3(256), 0, st, p);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (d.hd > kStageMaxD) {  // the staged kernel writes the partial sums itself
+        hipLaunchKernelGGL(prologue_bwd_dw_partial_kernel, dim3(p.n_chunks_q + p.n_chunks_k), dim3(256), 0, st, p);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(prologue_bwd_dw_reduce_kernel, dim3(2 * d.hd), dim3(256), 0, st, p);
     return hipGetLastError();
 }
