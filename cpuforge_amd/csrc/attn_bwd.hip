@@ -802,8 +802,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             if (full) {
                 // The softmax's lse values are read before the products, so
                 // their latency is not paid once per group of four.
+                // (With more than two query blocks the registers are not there:
+                // each block's values are read just before its softmax.)
                 float4 l4s[NQB][4];
-                if constexpr (PW) {
+                if constexpr (PW && NQB <= 2) {
 #pragma unroll
                     for (int qb = 0; qb < NQB; qb++)
 #pragma unroll
@@ -819,10 +821,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     for (int qb = 0; qb < NQB; qb++) sc[qb] = mfma32(row_read(qb, kd), xf[kd], sc[qb]);
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++) {
-                    if constexpr (PW)
+                    if constexpr (PW) {
+                        if constexpr (NQB > 2)
+#pragma unroll
+                            for (int g4 = 0; g4 < 4; g4++) l4s[qb][g4] = lse4(qb, g4);
                         p_block(qb, sc[qb], false, l4s[qb]);
-                    else
+                    } else {
                         dpv[qb] = sc[qb];
+                    }
                 }
             } else if (act) {
 #pragma unroll
@@ -893,7 +899,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             if (full) {
                 // dS waves read every P and delta value of the step first.
                 float4 p4s[NQB][4], d4s[NQB][4];
-                if constexpr (!PW) {
+                if constexpr (!PW && NQB <= 2) {
 #pragma unroll
                     for (int qb = 0; qb < NQB; qb++)
 #pragma unroll
@@ -901,7 +907,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
-                for (int qb = 0; qb < NQB; qb++) phase2(qb, p4s[qb], d4s[qb]);
+                for (int qb = 0; qb < NQB; qb++) {
+                    if constexpr (!PW && NQB > 2)
+#pragma unroll
+                        for (int g4 = 0; g4 < 4; g4++) pd4(qb, g4, p4s[qb][g4], d4s[qb][g4]);
+                    phase2(qb, p4s[qb], d4s[qb]);
+                }
             } else if (act) {
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++) {
@@ -1041,7 +1052,7 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
             if (d.hd == 128)
                 hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
             else
-                hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<64, 64>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
+                hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<64, 128>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
             e = hipGetLastError();
         }
         if (e != hipSuccess) return e;
