@@ -59,6 +59,8 @@ SIGNATURES = {
     "cfattn_rope_table": (C.c_int, [_sz, _sz, C.c_double, C.POINTER(Llama3ScalingC), _vp, _vp]),
     "cfattn_llama3_scale": (C.c_double, [C.POINTER(Llama3ScalingC), C.c_double]),
     "cfattn_f32_to_bf16": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    "cfattn_set_ds_limit": (C.c_int, [_vp, _sz]),
+    "cfattn_get_ds_limit": (_sz, [_vp]),
     "cfattn_profile_enable": (C.c_int, [_vp, C.c_int]),
     "cfattn_profile_read": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]),
     "cfattn_kernel_name": (C.c_char_p, [C.c_int]),

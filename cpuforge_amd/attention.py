@@ -79,6 +79,16 @@ class Context:
     def stream(self) -> int:
         return self._lib.cfattn_stream(self.handle) or 0
 
+    @property
+    def ds_limit(self) -> int:
+        """Bytes of device scratch the bf16 backward may keep to store dS, so
+        that dQ needs no softmax recompute; 0 disables that path."""
+        return int(self._lib.cfattn_get_ds_limit(self.handle))
+
+    @ds_limit.setter
+    def ds_limit(self, nbytes: int) -> None:
+        _lib.check(self._lib.cfattn_set_ds_limit(self.handle, int(nbytes)), self.handle)
+
     def profile_enable(self, on: bool = True) -> None:
         """Bracket every kernel this context queues with hipEvents on its
         stream (enabling again resets the totals)."""

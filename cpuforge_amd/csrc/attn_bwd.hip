@@ -42,6 +42,11 @@ struct BwdParams {
     float scale, sl2;
     long q_bs, kv_bs;
     int vec_ok, g_vec_ok, xcd;
+    // Stored dS (fast bf16 path only, null otherwise): per (sequence, query
+    // head), the 32x32 blocks (query block qi, key block ki <= qi) of the
+    // causal triangle, block qi*(qi+1)/2 + ki, 2 KiB each (kDsBlock).
+    uint16_t* ds;
+    long ds_ntri;  // blocks per (sequence, head)
 };
 
 // delta[b][h][t] = sum_d dO[b,t,h,d] * O[b,t,h,d]; 16 lanes per row.
@@ -432,6 +437,33 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const BwdParams p) {
 // Waves per workgroup of the fast dQ kernel.  All of them share each K/V
 // tile; four (two workgroups per CU) measured faster than eight (one).
 constexpr int kDqWaves = 4;
+// Waves per workgroup of the stored-dS dQ kernel: more query blocks share
+// each K tile, which that kernel streams as many bytes of as it does dS.
+constexpr int kDqDsWaves = 8;
+
+// Stored dS block: kDsBlock bf16 values (2 KiB) for query block qi and key
+// block ki.  Element (MFMA row m, key k) of the 32x32 block -- query
+// 32*qi + qperm(m), key 32*ki + k -- sits in 16-byte slot
+//   c*64 + (l ^ (2*c + hh)),   l = k + 32*hh,  hh = (m/4) % 2,  c = m / 16,
+// at position 4*((m/8) % 2) + m % 4 of the slot.  Slot l ^ .. thus holds the
+// eight values lane l of a dK/dV dS wave has for its key, in accumulator
+// order, so the writer stores two 16-byte pieces per lane.  The XOR spreads
+// the 8-byte pieces one transposed read of the dQ kernel gathers (keys 4
+// apart, four row quads) over all 64 LDS banks.
+constexpr int kDsBlock = 1024;
+// Cache-policy operand of global_load_lds: nt (non-temporal, streamed past
+// the caches), for data read exactly once.
+constexpr int kCacheNT = 2;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// s_waitcnt vmcnt(N): at most N vector memory operations of this wave still
+// outstanding (counts up to 63).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14;
+    // expcnt (bits 6:4) and lgkmcnt (bits 11:8) left at their maximum.
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 // dQ: the forward's decomposition (a wave owns 32 queries of one head, NW
 // waves per workgroup); K/V tiles of BN keys are shared by the workgroup and
@@ -614,6 +646,160 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
 }
 
+// dQ from the stored dS: dQ^T += K^T dS^T over the key blocks at or before
+// each wave's 32 queries, with no softmax recompute (one product per key
+// block instead of three).  NW waves per workgroup (query heads of one GQA
+// group x query blocks, as in attn_bwd_dq_bf16_kernel) share each K tile.
+// Both the K tile and each wave's dS blocks (2 KiB each, non-temporal: read
+// once) go straight to LDS one tile ahead, double-buffered in distinct
+// arrays (with a third stage the compiler loses track of which direct-to-LDS
+// loads a read depends on and waits for all of them before every read).
+// The dS blocks are read transposed: in 16-lane
+// group G, lane 4*kk + a supplies the 8-byte piece of key
+// 16*(u/2) + 4*kk + 2*(u%2) + hh and rows 16*(G%2) + 4*a.. for read u, so
+// lane l ends up with MFMA column l32 (query 32*qi + qperm(l32)) and, for
+// each k-index, the key the K^T operand read uses.
+template <int DP, int BN, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams p) {
+    constexpr int CPR = DP / 8;
+    using L = BlkTile<DP, BN>;
+    constexpr int CPW = L::NB / NW;  // 1 KiB K loads per wave per tile
+    constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16;
+    static_assert(L::NB % NW == 0, "tile must split evenly over the waves");
+    constexpr int NDB = DP / 32, NKB = BN / 32;
+    constexpr int SB = kDsBlock;
+    __shared__ __attribute__((aligned(16))) bf16_bits sK0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sK1[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sS0[NW * NKB * SB];
+    __shared__ __attribute__((aligned(16))) bf16_bits sS1[NW * NKB * SB];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg_q, p.xcd);
+    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;
+    int rest = id / p.n_ttiles;
+    const int sub = rest % p.n_sub;
+    rest /= p.n_sub;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+
+    const int head = g * p.group + sub * p.hpw + wave % p.hpw;
+    const int TT = 32 * p.tpw;
+    const int t_wave = tile * TT + (wave / p.hpw) * 32;
+    const int wg_end = min(p.seq, tile * TT + TT);
+    const int n_kt = (wg_end + BN - 1) / BN;
+    const bool wave_active = t_wave < p.seq;
+    // Query block of the wave; a wave past the end reads block 0 (unused).
+    const int qi = wave_active ? t_wave >> 5 : 0;
+    const int tq = t_wave + qperm(l32);
+    const bool row_ok = wave_active && tq < p.seq;
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const bf16_bits* kg = static_cast<const bf16_bits*>(p.k) + (long)b * p.kv_bs + (long)g * DP;
+    // This wave's first stored block (query block qi, key block 0), lane part.
+    const bf16_bits* dsg = p.ds + (((long)b * p.nh + head) * p.ds_ntri + (long)qi * (qi + 1) / 2) * SB + lane * 8;
+
+    // K^T reads as in attn_bwd_dq_bf16_kernel: tile rows 4k + hh (+2, +16, +18).
+    const int G = lane >> 4, jj = lane & 15;
+    const int trow = L::row(4 * (jj >> 2) + hh) + 16 * (G & 1) + 4 * (jj & 3);
+    // dS reads (elements): reads u = 0, 2 use srd0 (+128 for u = 2), reads
+    // u = 1, 3 use srd1; the XOR of the layout flips the key's bit 1 with G%2.
+    const int sc_ = G & 1, kk_ = jj >> 2, a_ = jj & 3;
+    const int sbase = sc_ * 64 + 32 * (a_ & 1) + 4 * kk_ + (hh ^ (a_ & 1));
+    const int srd0 = (sbase + 2 * sc_) * 8 + (a_ >> 1) * 4;
+    const int srd1 = (sbase + 2 * (sc_ ^ 1)) * 8 + (a_ >> 1) * 4;
+
+    // Tile kt: wave w loads K blocks w*CPW.. (lane l of block bk: chunk
+    // l % CPR of tile row bk + NB*(l / CPR), keys past the end reading the
+    // last key), and its own dS blocks of the tile (blocks past the
+    // diagonal reload the diagonal block, unused).
+    const int wv = wave_uniform(wave);
+    constexpr int NBL = L::NB;
+    const int lane_off = NBL * (lane / CPR) * (int)kvrs + (lane % CPR) * 8;
+    auto dma = [&](int kt, bf16_bits* Kd, bf16_bits* Sd) {
+        if ((kt + 1) * BN <= p.seq) {
+            const long base = (long)kt * BN * kvrs;
+#pragma unroll
+            for (int i = 0; i < CPW; i++) {
+                const int blk = wv * CPW + i;
+                __builtin_amdgcn_global_load_lds(kg + base + (long)blk * kvrs + lane_off, Kd + blk * BSTRIDE, 16, 0,
+                                                 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPW; i++) {
+                const int blk = wv * CPW + i;
+                const int r = blk + L::NB * (lane / CPR);
+                const long off = (long)min(kt * BN + r, p.seq - 1) * kvrs + (lane % CPR) * 8;
+                __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const bf16_bits* src = dsg + (long)min(kt * NKB + kb, qi) * SB;
+            bf16_bits* dst = Sd + (wv * NKB + kb) * SB;
+            __builtin_amdgcn_global_load_lds(src, dst, 16, 0, kCacheNT);
+            __builtin_amdgcn_global_load_lds(src + SB / 2, dst + SB / 2, 16, 0, kCacheNT);
+        }
+    };
+
+    f32x16 dqt[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) dqt[i] = zero16();
+
+    auto step = [&](int kt, const bf16_bits* Ks, const bf16_bits* Ss, bf16_bits* Kn, bf16_bits* Sn) {
+        if (kt + 1 < n_kt) dma(kt + 1, Kn, Sn);
+        // Key blocks of the tile at or before the wave's query block.
+        const int nkb = wave_active ? min(NKB, qi - kt * NKB + 1) : 0;
+        if (nkb > 0) {
+            const bf16_bits* sw = Ss + wv * NKB * SB;
+            auto block = [&](int kb) {
+                const bf16_bits* sp = sw + kb * SB;
+                const bf16x8 d0 = join_bf16x4(ds_read_tr16(sp + srd0), ds_read_tr16(sp + srd1));
+                const bf16x8 d1 = join_bf16x4(ds_read_tr16(sp + srd0 + 128), ds_read_tr16(sp + srd1 + 128));
+                const bf16_bits* t0 = Ks + trow + kb * 2 * ROW16;
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    const bf16_bits* tp = t0 + db * 32;
+                    const bf16x8 a0 = join_bf16x4(ds_read_tr16(tp), ds_read_tr16(tp + 2 * BSTRIDE));
+                    const bf16x8 a1 =
+                        join_bf16x4(ds_read_tr16(tp + ROW16), ds_read_tr16(tp + ROW16 + 2 * BSTRIDE));
+                    dqt[db] = mfma32(a0, d0, dqt[db]);
+                    dqt[db] = mfma32(a1, d1, dqt[db]);
+                }
+            };
+            if (nkb == NKB) {
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) block(kb);
+            } else {
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++)
+                    if (kb < nkb) block(kb);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for tile kt + 1 have landed
+        __syncthreads();
+    };
+
+    dma(0, sK0, sS0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int kt = 0; kt < n_kt; kt += 2) {
+        step(kt, sK0, sS0, sK1, sS1);
+        if (kt + 1 < n_kt) step(kt + 1, sK1, sS1, sK0, sS0);
+    }
+
+    if (!row_ok) return;
+    float* dqrow = p.dq + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
+#pragma unroll
+    for (int db = 0; db < NDB; db++) {
+        dqt[db] *= p.scale;  // dS was stored without the softmax scale
+        add_row_block(dqrow, dqt[db], db * 32, hh, DP, true);
+    }
+}
+
 // dK/dV with two specialised waves per 32-key slice: eight waves, 128 keys per
 // workgroup of one KV head; steps run over (query head of the group, query
 // tile of BM rows) in a fixed order, low key tiles (the most queries) first.
@@ -626,7 +812,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 // softmax of one runs while the other issues matrix work, and each needs half
 // the registers of a wave doing both.  Two barriers per step: P is written
 // before the first and read after it.
-template <int DP, int BM>
+// With WDS the dS waves also store each 32x32 block of dS (bf16, the values
+// their dK product uses) for attn_bwd_dq_ds_kernel; the layout is given at
+// kDsBlock.
+template <int DP, int BM, bool WDS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dkdv_ws_kernel(
     const BwdParams p) {
     constexpr int NT = 512;
@@ -677,10 +866,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int G = lane >> 4, jj = lane & 15;
     const int trow = L::row(4 * (jj >> 2) + hh) + 16 * (G & 1) + 4 * (jj & 3);
 
+    // Stored dS: lane l (key l32 of the slice, MFMA rows 4*hh + ...) writes
+    // its first eight values to 16-byte slot l ^ hh of the block and the
+    // other eight to slot 64 + (l ^ (2 + hh)) (see kDsBlock).
+    const int ds_off0 = (lane ^ hh) * 8, ds_off1 = (64 + (lane ^ (2 + hh))) * 8;
+    const int ki = key0 >> 5;
+
     const int n_qt = (p.seq + BM - 1) / BM;
     const int qt_begin = wg_key0 / BM;
     const int nq = n_qt - qt_begin;
     const int n_steps = p.group * nq;
+    // Step s covers query tile qt_begin + s % nq of query head s / nq.
+    // (Walking every workgroup's tiles from the last one down, heads
+    // innermost, so that the workgroups on an XCD read the same Q/dO tiles
+    // together, measured 4% slower.)
+    auto step_q0 = [&](int s) { return (qt_begin + s % nq) * BM; };
+    auto step_h = [&](int s) { return g * p.group + s / nq; };
 
     float pl = 0.0f;
     // The dS waves (threads 256..511) load the tiles, lse and delta: they
@@ -688,8 +889,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int dt = tid - NT / 2;
     // Query of MFMA row i (0 <= i < BM) of a tile.
     const int lrow = (dt % BM & ~31) + qperm(dt & 31);
-    // Step s covers query tile qt_begin + s % nq of query head s / nq; its Q
-    // and dO rows go straight into the blocked LDS tile: dS wave w fills load
+    // A step's Q and dO rows go straight into the blocked LDS tile: dS wave w fills load
     // blocks w*CPW.., lane l of block b loading chunk l % CPR of tile row
     // b + NB*(l / CPR).  Rows past the end load the last row (finite values);
     // their lse is +inf and delta 0 below, so P = dS = 0 there.
@@ -699,8 +899,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int NBL = L::NB;
     const int lane_off = NBL * (lane / CPR) * (int)qrs + (lane % CPR) * 8;
     auto dma = [&](int s, bf16_bits* Qd, bf16_bits* Od) {
-        const int h = g * p.group + s / nq;
-        const int q0 = (qt_begin + s % nq) * BM;
+        const int h = step_h(s);
+        const int q0 = step_q0(s);
         if (dt < 0) return;
         if (q0 + BM <= p.seq) {
             const long base = (long)q0 * qrs + (long)h * DP;
@@ -728,7 +928,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     };
     auto store_ld = [&](int s, int st) {
-        const int t = (qt_begin + s % nq) * BM + lrow;
+        const int t = step_q0(s) + lrow;
         if (dt < 0) return;
         if (dt < BM)
             sL[st][dt] = t < p.seq ? pl * kLog2e : INFINITY;  // rows past the end: P = 0
@@ -759,7 +959,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         auto step = [&](int s, const bf16_bits* Qs, const bf16_bits* Os, bf16_bits* Qn, bf16_bits* On) {
             const int st = s & 1;
             const bool more = s + 1 < n_steps;
-            const int q0 = (qt_begin + s % nq) * BM;
+            const int q0 = step_q0(s);
             const bool act = wave_active && q0 + BM - 1 >= key0;
             // Every query of the step is past every key of the slice: no mask
             // and no per-block tests.
@@ -771,8 +971,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             // so each names its LDS array directly.
             const bf16_bits* A1 = PW ? Qs : Os;
             const bf16_bits* A2 = PW ? Os : Qs;
+            const long ds_head = ((long)b * p.nh + step_h(s)) * p.ds_ntri;
             bf16x8 pbf[NQB][2];  // P waves: P of each block as MFMA operands
             f32x16 dpv[NQB];     // dS waves: dP of each block
+            bf16x8 dsv[NQB][2];  // dS waves with WDS: dS of each block, stored after the step
             auto row_read = [&](int qb, int kd) {
                 return __builtin_bit_cast(bf16x8,
                                           *reinterpret_cast<const uint4*>(A1 + rrow + qb * 2 * ROW16 + kd * 8));
@@ -881,6 +1083,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     }
                     b0 = cvt_bf16x8(&ds[0]);
                     b1 = cvt_bf16x8(&ds[8]);
+                    if constexpr (WDS) {
+                        dsv[qb][0] = b0;
+                        dsv[qb][1] = b1;
+                    }
                 }
                 // dO^T (P waves) or Q^T (dS waves), read transposed from the
                 // tile: MFMA rows 4hh..+3 and 8+4hh..+3 of the block for b0,
@@ -929,6 +1135,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 if (more) store_ld(s + 1, st ^ 1);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for step s + 1 have landed
             __syncthreads();
+            // The step's dS goes out only now: stores still in flight at the
+            // wait above would hold it up (the wait counts them too); issued
+            // here they complete during the next step.  Non-temporal: the
+            // 2 KiB blocks are read once, by the dQ kernel, and should not
+            // displace the Q/dO tiles in the caches.
+            if constexpr (!PW && WDS) {
+#pragma unroll
+                for (int qb = 0; qb < NQB; qb++) {
+                    const int tq0 = q0 + qb * 32;
+                    if (full || (act && tq0 < p.seq && tq0 + 31 >= key0)) {
+                        const long qi = tq0 >> 5;
+                        bf16_bits* blk = p.ds + (ds_head + qi * (qi + 1) / 2 + ki) * kDsBlock;
+                        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, dsv[qb][0]),
+                                                    reinterpret_cast<u32x4*>(blk + ds_off0));
+                        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, dsv[qb][1]),
+                                                    reinterpret_cast<u32x4*>(blk + ds_off1));
+                    }
+                }
+            }
         };
 
         for (int s = 0; s < n_steps; s += 2) {
@@ -986,9 +1211,17 @@ static hipError_t bwd_dp(const BwdParams& p, hipStream_t st, int kv_waves, int q
     return hipGetLastError();
 }
 
+size_t attn_bwd_ds_bytes(Dtype dt, const Dims& d) {
+    // head_dim 128 only: at 64 the recompute costs half the matrix work per
+    // stored byte and measured faster than the dS round trip through HBM.
+    if (dt != kBF16 || d.hd != 128 || d.batch <= 0 || d.seq <= 0) return 0;
+    const size_t nqb = ((size_t)d.seq + 31) / 32;
+    return (size_t)d.batch * d.nh * (nqb * (nqb + 1) / 2) * kDsBlock * sizeof(bf16_bits);
+}
+
 hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
                            const float* o, const float* lse, float* delta, float* dq, float* dk, float* dv,
-                           hipStream_t st, const Tuning& tu) {
+                           hipStream_t st, const Tuning& tu, void* ds, size_t ds_bytes) {
     if (d.batch == 0 || d.seq == 0 || d.nh == 0) return hipSuccess;
     BwdParams p{};
     p.d_o = d_o;
@@ -1047,16 +1280,38 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
             e = hipGetLastError();
         }
         if (e != hipSuccess) return e;
+        const size_t need = attn_bwd_ds_bytes(dt, d);
+        const bool use_ds = ds != nullptr && need > 0 && ds_bytes >= need;
+        if (use_ds) {
+            p.ds = static_cast<bf16_bits*>(ds);
+            const long nqb = (d.seq + 31) / 32;
+            p.ds_ntri = nqb * (nqb + 1) / 2;
+        }
         {
             TimedLaunch tl(tu.timer, kKernBwdDkdv, st);
-            if (d.hd == 128)
-                hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
-            else
-                hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<64, 128>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
+            if (d.hd == 128) {
+                if (use_ds)
+                    hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64, true>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
+                else
+                    hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64, false>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
+            } else {
+                hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<64, 128, false>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
+            }
             e = hipGetLastError();
         }
         if (e != hipSuccess) return e;
         TimedLaunch tl(tu.timer, kKernBwdDq, st);
+        if (use_ds) {
+            // kDqDsWaves waves per workgroup: the group's heads x query blocks.
+            p.tpw = kDqDsWaves / p.hpw;
+            p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
+            const long n = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+            if (n > 0x7fffffffL) return hipErrorInvalidConfiguration;
+            p.n_wg_q = (int)n;
+            hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<128, 64, kDqDsWaves>), dim3(p.n_wg_q), dim3(64 * kDqDsWaves), 0,
+                               st, p);
+            return hipGetLastError();
+        }
         if (d.hd == 128)
             hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 64, kDqWaves>), dim3(p.n_wg_q), dim3(64 * kDqWaves), 0, st,
                                p);

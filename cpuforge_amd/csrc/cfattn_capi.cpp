@@ -102,10 +102,11 @@ struct cfattn_ctx {
     int mode = CFATTN_F32;
     std::string err;
     std::mutex mu;
-    enum Slot { Q, K, V, O, LSE, DO_, DQ, DK, DV, QB, KB, VB, DOB, DELTA, PARTIAL, DQROT, DKROT, NSLOT };
+    enum Slot { Q, K, V, O, LSE, DO_, DQ, DK, DV, QB, KB, VB, DOB, DELTA, PARTIAL, DQROT, DKROT, DS, NSLOT };
     void* buf[NSLOT] = {};
     size_t cap[NSLOT] = {};
     EventTimer* timer = nullptr;  // non-null while profiling is on
+    size_t ds_limit = (size_t)8 << 30;  // stored-dS scratch limit (cfattn_set_ds_limit)
 
     cfattn::Tuning tuning() const {
         cfattn::Tuning t;
@@ -166,6 +167,24 @@ void* slot(cfattn_ctx* c, int s, size_t bytes, int* rc) {
     }
     c->buf[s] = p;
     c->cap[s] = want;
+    return p;
+}
+
+// Scratch for the stored-dS dQ path, or null (dQ recomputes the softmax)
+// when the path does not apply, needs more than the context's limit, or the
+// allocation fails.  Never an error: the recompute path needs no scratch.
+void* ds_scratch(cfattn_ctx* c, Dtype dt, const Dims& d, size_t* bytes) {
+    *bytes = cfattn::attn_bwd_ds_bytes(dt, d);
+    if (*bytes == 0 || *bytes > c->ds_limit) {
+        *bytes = 0;
+        return nullptr;
+    }
+    int rc = CFATTN_OK;
+    void* p = slot(c, cfattn_ctx::DS, *bytes, &rc);
+    if (!p) {
+        c->err.clear();
+        *bytes = 0;
+    }
     return p;
 }
 
@@ -323,8 +342,10 @@ int backward_host(cfattn_ctx* c, const float* d_o, size_t d_o_len, const float* 
     CF_HIP(c, hipMemcpyAsync(g_q, dq, dq_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dq");
     CF_HIP(c, hipMemcpyAsync(g_k, dk, dk_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dk");
     CF_HIP(c, hipMemcpyAsync(g_v, dv, dv_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dv");
+    size_t ds_bytes = 0;
+    void* ds = ds_scratch(c, bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), &ds_bytes);
     CF_HIP(c, cfattn::launch_attn_bwd(bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), ddo, dq_in, dk_in, dv_in,
-                                      d_out, d_lse, delta, g_q, g_k, g_v, c->stream, c->tuning()),
+                                      d_out, d_lse, delta, g_q, g_k, g_v, c->stream, c->tuning(), ds, ds_bytes),
            "attention backward launch");
     CF_HIP(c, hipMemcpyAsync(dq, g_q, dq_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H dq");
     CF_HIP(c, hipMemcpyAsync(dk, g_k, dk_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H dk");
@@ -479,8 +500,10 @@ static int cfattn_bwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dt
     int rc = CFATTN_OK;
     float* delta = static_cast<float*>(slot(c, cfattn_ctx::DELTA, batch * s.n_heads * s.seq * 4, &rc));
     if (!delta) return rc;
+    size_t ds_bytes = 0;
+    void* ds = ds_scratch(c, (Dtype)dtype, dims_of(s, batch), &ds_bytes);
     CF_HIP(c, cfattn::launch_attn_bwd((Dtype)dtype, dims_of(s, batch), d_o, q, k, v, o, lse, delta, dq, dk, dv,
-                                      pick_stream(c, stream), c->tuning()),
+                                      pick_stream(c, stream), c->tuning(), ds, ds_bytes),
            "attention backward launch");
     return CFATTN_OK;
 }
@@ -627,6 +650,22 @@ int cfattn_f32_to_bf16(cfattn_ctx* c, const float* src, uint16_t* dst, size_t n,
     CF_HIP(c, cfattn::launch_f32_to_bf16(src, dst, n, pick_stream(c, stream)), "f32_to_bf16 launch");
     return CFATTN_OK;
 }
+
+int cfattn_set_ds_limit(cfattn_ctx* c, size_t bytes) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    c->ds_limit = bytes;
+    if (c->buf[cfattn_ctx::DS] && c->cap[cfattn_ctx::DS] > bytes) {
+        DeviceGuard dg(c->device);
+        (void)hipFree(c->buf[cfattn_ctx::DS]);
+        c->buf[cfattn_ctx::DS] = nullptr;
+        c->cap[cfattn_ctx::DS] = 0;
+    }
+    return CFATTN_OK;
+}
+
+size_t cfattn_get_ds_limit(const cfattn_ctx* c) { return c ? c->ds_limit : 0; }
 
 int cfattn_profile_enable(cfattn_ctx* c, int on) {
     if (!c) return CFATTN_ERR_ARG;

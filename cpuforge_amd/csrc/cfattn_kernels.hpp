@@ -63,9 +63,17 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
 
 // Backward.  `delta` is caller-provided scratch of batch*n_heads*seq floats.
 // dq, dk, dv are accumulated (+=).
+//
+// `ds` is optional scratch for the stored-dS dQ path: when it is non-null
+// and `ds_bytes` >= attn_bwd_ds_bytes(dt, d), and the fast bf16 kernels run,
+// the dK/dV kernel writes dS (bf16, causal blocks only) and dQ is one
+// product over it instead of a second softmax recompute.  Otherwise dQ
+// recomputes S and dP.  Both paths give the same result up to bf16
+// rounding of dS, which both apply.
+size_t attn_bwd_ds_bytes(Dtype dt, const Dims& d);
 hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
                            const float* o, const float* lse, float* delta, float* dq, float* dk, float* dv,
-                           hipStream_t st, const Tuning& tu);
+                           hipStream_t st, const Tuning& tu, void* ds = nullptr, size_t ds_bytes = 0);
 
 // Attention prologue: optional per-head RMSNorm of q_pre/k_pre (when qw/kw
 // are non-null) followed by rotate-half RoPE at positions pos0+t, written in

@@ -176,6 +176,19 @@ int cfattn_rope_table(size_t head_dim, size_t max_pos, double theta, const cfatt
 double cfattn_llama3_scale(const cfattn_llama3_scaling* scaling, double inv_freq);
 /* Device f32 -> bf16 (round to nearest even) conversion on `stream`. */
 int cfattn_f32_to_bf16(cfattn_ctx* ctx, const float* src, uint16_t* dst, size_t n, void* stream);
+/* ---- backward scratch ---------------------------------------------------- */
+/* No reference counterpart (the reference's backward recomputes everything
+ * per query block, attention.rs:142-262).  Limit, in bytes, of the device
+ * scratch the bf16 backward (head_dim 64 or 128) may keep in the context's
+ * pool to store dS: bf16 values of the causal 32x32 blocks,
+ * batch * n_heads * nb*(nb+1)/2 * 2 KiB with nb = ceil(seq/32) (2.2 GB at
+ * seq 8192, 32 heads).  With it, dQ is one product over the stored dS instead
+ * of a second softmax recompute; results agree to bf16 rounding of dS, which
+ * both paths apply.  Larger shapes, or limit 0, use the recompute.  Lowering
+ * the limit below the kept scratch frees it.  Default: 8 GiB. */
+int cfattn_set_ds_limit(cfattn_ctx* ctx, size_t bytes);
+size_t cfattn_get_ds_limit(const cfattn_ctx* ctx);
+
 /* ---- measurement ----------------------------------------------------------- */
 /* No reference counterpart: the reference times whole steps with a wall clock
  * (cli/src/cmd_bench.rs:13-22).  While enabled, every kernel this context

@@ -219,25 +219,48 @@ FAST_SHAPES = [(1, 1, 4, 1, 128), (2, 33, 4, 2, 64), (1, 100, 8, 2, 128), (1, 25
                (2, 130, 3, 3, 128), (1, 200, 4, 1, 64), (1, 511, 2, 2, 128)]
 
 
-@pytest.mark.parametrize("shape", FAST_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_bf16_fast_path_shapes(cf, shape):
+def _fast_inputs(shape, seed=500):
     import torch
-    from cpuforge_amd import device as D
-    mod, ctx = cf
     B, S, Hq, Hk, Dh = shape
-    print(f"fast-path shape {shape}", flush=True)
     host = []
     for b in range(B):
-        sd = 500 + 16 * b
+        sd = seed + 16 * b
         host.append(tuple(O.round_bf16(O.rand(S * h * Dh, sd + i, 1.0)) for i, h in enumerate((Hq, Hk, Hk, Hq))))
 
     def dev(i, heads):
         return torch.from_numpy(np.stack([h[i] for h in host])).view(B, S, heads, Dh).to("cuda").to(torch.bfloat16)
 
-    q, k, v, g = dev(0, Hq), dev(1, Hk), dev(2, Hk), dev(3, Hq)
-    o, lse = D.fwd(q, k, v, ctx=ctx)
-    dq, dk, dv = D.bwd(g, q, k, v, o, lse, ctx=ctx)
-    torch.cuda.synchronize()
+    return host, (dev(0, Hq), dev(1, Hk), dev(2, Hk), dev(3, Hq))
+
+
+class _DsLimit:
+    """Sets the context's stored-dS scratch limit for a block (0: dQ
+    recomputes the softmax) and restores it afterwards."""
+
+    def __init__(self, ctx, nbytes):
+        self.ctx, self.nbytes = ctx, nbytes
+
+    def __enter__(self):
+        self.old = self.ctx.ds_limit
+        self.ctx.ds_limit = self.nbytes
+
+    def __exit__(self, *exc):
+        self.ctx.ds_limit = self.old
+
+
+@pytest.mark.parametrize("ds", ["stored", "recompute"])
+@pytest.mark.parametrize("shape", FAST_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_bf16_fast_path_shapes(cf, shape, ds):
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    B, S, Hq, Hk, Dh = shape
+    print(f"fast-path shape {shape}, dQ from {ds} dS", flush=True)
+    host, (q, k, v, g) = _fast_inputs(shape)
+    with _DsLimit(ctx, ctx.ds_limit if ds == "stored" else 0):
+        o, lse = D.fwd(q, k, v, ctx=ctx)
+        dq, dk, dv = D.bwd(g, q, k, v, o, lse, ctx=ctx)
+        torch.cuda.synchronize()
     o, lse, dq, dk, dv = (x.cpu().numpy() for x in (o, lse, dq, dk, dv))
     for b in range(B):
         hq, hk, hv, hg = host[b]
@@ -250,3 +273,28 @@ def test_bf16_fast_path_shapes(cf, shape):
                            ("dv", dv[b], rv)):
             e = rel_err(a.reshape(-1), r)
             assert e <= BF16_TOL, f"{shape} seq {b} {name}: {e}"
+
+
+@pytest.mark.parametrize("shape", [(1, 300, 8, 2, 128), (2, 97, 4, 4, 64), (1, 1000, 4, 1, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_stored_ds_matches_recompute(cf, shape):
+    """dQ from the dS the dK/dV kernel stores against dQ with the softmax
+    recomputed: the dK/dV kernel's arithmetic is the same in both, so dK and
+    dV are bitwise equal; dQ sums the same bf16-rounded dS values in the
+    same key order and may differ only where the two kernels' products of S
+    and dP round differently."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    print(f"stored vs recomputed dS, shape {shape}", flush=True)
+    _, (q, k, v, g) = _fast_inputs(shape, seed=900)
+    o, lse = D.fwd(q, k, v, ctx=ctx)
+    out = {}
+    for ds in ("recompute", "stored"):
+        with _DsLimit(ctx, ctx.ds_limit if ds == "stored" else 0):
+            out[ds] = [x.cpu().numpy() for x in D.bwd(g, q, k, v, o, lse, ctx=ctx)]
+    (rq, rk, rv), (sq, sk, sv) = out["recompute"], out["stored"]
+    assert np.array_equal(rk, sk) and np.array_equal(rv, sv)
+    e = rel_err(sq.reshape(-1), rq.reshape(-1))
+    print(f"  dq rel diff {e:.3e}, bitwise equal {np.array_equal(sq, rq)}", flush=True)
+    assert e <= 1e-5
