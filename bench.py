@@ -66,6 +66,8 @@ def parse():
     ap.add_argument("--mode", default=None, choices=["bf16", "f32"], help="default: bf16 (f32 for C1)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--cpu-heads", type=int, default=16, help="query heads of sequence 0 in the CPU sample")
+    ap.add_argument("--cpu-single-heads", type=int, default=4,
+                    help="query heads of sequence 0 in the single-thread CPU sample (0 skips it)")
     ap.add_argument("--no-train", action="store_true", help="skip the SmolLM-135M train tok/s leg")
     ap.add_argument("--train-steps", type=int, default=3)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -80,38 +82,77 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(cfg_name, mode, heads):
+def _host_cpu():
+    """Host CPU model name and logical CPU count, as lscpu and nproc show them."""
+    name = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": name, "nproc": os.cpu_count()}
+
+
+def cpu_baseline(cfg_name, mode, heads, single_heads):
     """The oracle (a C restatement of attention_forward_blocked /
     attention_backward_blocked with an OpenMP GEMM) timed on query heads
-    [0, heads) of one sequence of the workload.  Runs on the host only."""
+    [0, heads) of one sequence of the workload with all its threads, and on
+    query heads [0, single_heads) with one thread.  Runs on the host only."""
     import numpy as np
 
     from oracle import oracle as O
     B, S, Hq, Hk, D = CONFIGS[cfg_name][:5]
-    heads = max(Hq // Hk, min(heads, Hq))
-    heads -= heads % (Hq // Hk)  # whole GQA groups
+    grp = Hq // Hk
+
+    def whole_groups(n):
+        n = max(grp, min(n, Hq))
+        return n - n % grp
+
+    heads, single_heads = whole_groups(heads), whole_groups(single_heads)
     q = O.rand(S * Hq * D, 1, 1.0)
     k = O.rand(S * Hk * D, 2, 1.0)
     v = O.rand(S * Hk * D, 3, 1.0)
     g = O.rand(S * Hq * D, 4, 1.0)
     if mode == "bf16":
         q, k, v, g = (O.round_bf16(x) for x in (q, k, v, g))
-    o = np.zeros_like(q)
-    lse = np.zeros(Hq * S, np.float32)
-    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
-    t0 = time.perf_counter()
-    O.attention_forward_blocked(q, k, v, o, lse, S, Hq, Hk, D, 128, heads=(0, heads))
-    O.attention_backward_blocked(g, q, k, v, o, lse, dq, dk, dv, S, Hq, Hk, D, 128, heads=(0, heads))
-    dt = time.perf_counter() - t0
-    flops = 7.0 * heads * D * S * (S + 1)
-    return {
+
+    def run(nh):
+        o = np.zeros_like(q)
+        lse = np.zeros(Hq * S, np.float32)
+        dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+        t0 = time.perf_counter()
+        O.attention_forward_blocked(q, k, v, o, lse, S, Hq, Hk, D, 128, heads=(0, nh))
+        O.attention_backward_blocked(g, q, k, v, o, lse, dq, dk, dv, S, Hq, Hk, D, 128, heads=(0, nh))
+        dt = time.perf_counter() - t0
+        return 7.0 * nh * D * S * (S + 1), dt
+
+    threads = O.gemm_threads()
+    flops, dt = run(heads)
+    out = {
         "value": flops / dt / 1e12,
         "unit": "TFLOP/s",
-        "cores": O.gemm_threads(),
+        "cores": threads,
         "kind": "port",
         "sample": (f"oracle fwd+bwd (q_block 128, f32 arithmetic) over query heads 0..{heads} of one sequence "
                    f"of {cfg_name} (S={S}, D={D}); {dt:.2f} s for {flops / 1e9:.1f} GFLOP"),
+        "host": _host_cpu(),
     }
+    if single_heads > 0:
+        O.set_gemm_threads(1)
+        try:
+            flops1, dt1 = run(single_heads)
+        finally:
+            O.set_gemm_threads(threads)
+        out["single_core"] = {
+            "value": flops1 / dt1 / 1e12,
+            "unit": "TFLOP/s",
+            "cores": 1,
+            "sample": f"query heads 0..{single_heads} of the same sequence; {dt1:.2f} s for {flops1 / 1e9:.1f} GFLOP",
+        }
+    return out
 
 
 def read_traffic(path, kernel, workload_key):
@@ -339,7 +380,7 @@ def main():
         out["smollm_train"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in tr.items()}
     if not a.no_cpu:
         print("bench: cpu baseline ...", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(a.config, mode, a.cpu_heads)
+        out["cpu_baseline"] = cpu_baseline(a.config, mode, a.cpu_heads, a.cpu_single_heads)
     else:
         out["cpu_baseline"] = None
     ctx.close()

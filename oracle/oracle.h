@@ -15,6 +15,7 @@ void orc_fill_normal(uint64_t seed, float* out, size_t n, float std);
 void orc_gemm_strided(const float* a, long a_rs, long a_cs, const float* b, long b_rs, long b_cs, float* c,
                       long c_rs, long c_cs, size_t m, size_t k, size_t n, int acc);
 int orc_gemm_threads(void);
+void orc_set_gemm_threads(int n);
 
 int orc_attention_forward_blocked(const float* q, const float* k, const float* v, float* o, float* lse,
                                   size_t seq, size_t nh, size_t nkv, size_t hd, size_t q_block);

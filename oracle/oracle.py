@@ -51,6 +51,8 @@ def lib():
         L.orc_gemm_strided.argtypes = [C.c_void_p, C.c_long, C.c_long, C.c_void_p, C.c_long, C.c_long,
                                        C.c_void_p, C.c_long, C.c_long, _sz, _sz, _sz, C.c_int]
         L.orc_gemm_threads.restype = C.c_int
+        L.orc_set_gemm_threads.argtypes = [C.c_int]
+        L.orc_set_gemm_threads.restype = None
         L.orc_attention_forward_heads.restype = C.c_int
         L.orc_attention_forward_heads.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p] + [_sz] * 7
         L.orc_attention_backward_heads.restype = C.c_int
@@ -115,6 +117,11 @@ def gemm_strided(a, a_rs, a_cs, b, b_rs, b_cs, c, c_rs, c_cs, m, k, n, acc):
 
 def gemm_threads() -> int:
     return lib().orc_gemm_threads()
+
+
+def set_gemm_threads(n: int) -> None:
+    """Threads the oracle GEMM uses from now on (n >= 1)."""
+    lib().orc_set_gemm_threads(int(n))
 
 
 # ---------------------------------------------------------- attention

@@ -30,6 +30,16 @@ int orc_gemm_threads(void) {
 #endif
 }
 
+/* Threads the GEMM uses from now on (n >= 1); for timing the single-core
+ * baseline beside the all-cores one. */
+void orc_set_gemm_threads(int n) {
+#ifdef _OPENMP
+    if (n >= 1) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+
 static void tile(const float* a, long a_rs, long a_cs, const float* b, long b_rs, long b_cs, float* c, long c_rs,
                  long c_cs, size_t i0, size_t mb, size_t j0, size_t nb, size_t k, int acc, float* ap, float* bp,
                  float* tmp) {
