@@ -77,6 +77,9 @@ def parse():
     ap.add_argument("--fused", action="store_true",
                     help="time the Layer-level path instead: q/k prologue (RoPE, Qwen3 norm) + attention, forward "
                          "and backward (cfattn_fused_fwd/bwd); prints its own JSON line")
+    ap.add_argument("--ops", action="store_true",
+                    help="time the layer ops (include/cfops.h) at the SmolLM-135M train shape and the train step "
+                         "with and without them; prints its own JSON line")
     ap.add_argument("--traffic-file", default=None,
                     help="rocprofv3 traffic summary to read `traffic` from (default: profiles/ match)")
     return ap.parse_args()
@@ -257,6 +260,91 @@ def fused_layer(a, mode):
           flush=True)
 
 
+def layer_ops(a):
+    """Times the layer ops of include/cfops.h at the SmolLM-135M training
+    shape of the train tok/s metric (batch 8 x seq 512 = 4096 tokens, hidden
+    576, FFN 1536, vocab 49152; crates/cli/src/cmd_bench.rs:43-99) and the
+    train step itself with every op in libcfattn.so (backend "cfops") and
+    with torch ops (backend "torch").  Each op's `achieved` is its
+    algorithmic bytes (HBM-bound ops) or FLOPs (GEMM-bound ops) per call over
+    its mean time, measured with HIP events on the stream the ops run on.
+    Prints its own JSON line."""
+    import torch
+
+    from cpuforge_amd import ops as P
+    from cpuforge_amd.train_bench import SMOLLM_135M, train_tok_s
+    c = SMOLLM_135M
+    t, d, f, V, r = 8 * 512, c["d"], c["ffn"], c["vocab"], 16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    rn = lambda *s_, std=1.0: torch.randn(*s_, generator=g, device="cuda") * std  # noqa: E731
+    x, w, y, rstd = rn(t, d), 1 + rn(d, std=0.1), torch.empty(t, d, device="cuda"), torch.empty(t, device="cuda")
+    dx, dw = torch.zeros(t, d, device="cuda"), torch.zeros(d, device="cuda")
+    gg, uu, hh = rn(t, f, std=2.0), rn(t, f), torch.empty(t, f, device="cuda")
+    dg, du = torch.zeros(t, f, device="cuda"), torch.zeros(t, f, device="cuda")
+    logits = rn(t, V, std=3.0)
+    dl = torch.empty_like(logits)
+    tg = torch.randint(0, V, (t,), generator=g, device="cuda")
+    head = rn(V, d, std=0.02)
+    dhn = torch.empty(t, d, device="cuda")
+    wq, la, lb = rn(d, d, std=0.02), rn(r, d, std=0.04), rn(d, r, std=0.1)
+    yq, xs = torch.empty(t, d, device="cuda"), torch.empty(t, r, device="cuda")
+    ga, gb = torch.zeros(r, d, device="cuda"), torch.zeros(d, r, device="cuda")
+    n_opt = 1 << 24
+    pp, pg, pm, pv = rn(n_opt), rn(n_opt), torch.zeros(n_opt, device="cuda"), torch.zeros(n_opt, device="cuda")
+    F = 4
+    cases = {
+        # name: (call, bytes or flops per call, bound)
+        "rmsnorm_forward": (lambda: P.rmsnorm_forward(x, w, y, rstd, t, d, 1e-5), F * (2 * t * d + d + t), "hbm"),
+        "rmsnorm_backward": (lambda: P.rmsnorm_backward(y, x, w, rstd, dx, dw, t, d), F * (4 * t * d + 2 * d + t),
+                             "hbm"),
+        "silu_mul_forward": (lambda: P.silu_mul_forward(gg, uu, hh), F * 3 * t * f, "hbm"),
+        "silu_mul_backward": (lambda: P.silu_mul_backward(hh, gg, uu, dg, du), F * 7 * t * f, "hbm"),
+        "cross_entropy_fwd_bwd": (lambda: P.cross_entropy_fwd_bwd(logits, tg, dl, t, V), F * 2 * t * V, "hbm"),
+        "adamw_update": (lambda: P.adamw_update(pp, pg, pm, pv, 1, 1e-3, 0.9, 0.95, 1e-8, 0.1), F * 7 * n_opt,
+                         "hbm"),
+        "linear_forward_lora": (lambda: P.linear_forward(x, wq, t, d, d, yq, la, lb, 2.0, xs),
+                                2.0 * t * d * (d + 2 * r), "mfma"),
+        "linear_backward_lora": (lambda: P.linear_backward(x, xs, yq, wq, t, d, d, dx, None, ga, gb, la, lb, 2.0),
+                                 2.0 * t * (d * d + 3 * d * r + r * d), "mfma"),
+        "lm_head_ce": (lambda: P.lm_head_ce(x, head, tg, t, d, V, dhn), 2.0 * 2 * t * d * V, "mfma"),
+    }
+    out = {}
+    for name, (fn, amount, bound) in cases.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 20
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / n
+        if bound == "hbm":
+            ach = amount / (ms * 1e-3) / 1e9
+            out[name] = {"ms": round(ms, 4), "achieved": round(ach, 1), "unit": "GB/s", "peak": PEAK_HBM_GBS,
+                         "frac": round(ach / PEAK_HBM_GBS, 4), "bytes": int(amount)}
+        else:
+            ach = amount / (ms * 1e-3) / 1e12
+            out[name] = {"ms": round(ms, 4), "achieved": round(ach, 2), "unit": "TFLOP/s",
+                         "peak": PEAK_TFLOPS["f32"], "frac": round(ach / PEAK_TFLOPS["f32"], 4), "flops": amount}
+    del x, y, dx, gg, uu, hh, dg, du, logits, dl, head, pp, pg, pm, pv
+    torch.cuda.empty_cache()
+    train = {}
+    for backend in ("cfops", "torch"):
+        tr = train_tok_s(batch=8, seq=512, steps=a.train_steps, backend=backend)
+        train[backend] = {"tok_s": round(tr["value"], 1), "ms_per_step": round(tr["ms_per_step"], 3),
+                          "first_loss": round(tr["first_loss"], 5)}
+    print(json.dumps({"metric": "SmolLM-135M train tok/s with the layer ops in libcfattn.so; per-op roofline",
+                      "value": train["cfops"]["tok_s"], "unit": "tok/s", "higher_is_better": True,
+                      "data": "synthetic (torch.randn / randint)", "dtype": "f32",
+                      "config": {"workload": "SmolLM-135M LoRA r=16 train step, batch 8 x seq 512, 30 layers",
+                                 "tokens": t, "hidden": d, "ffn": f, "vocab": V},
+                      "train": train, "ops": out}), flush=True)
+
+
 def main():
     a = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -271,6 +359,9 @@ def main():
         return
     if a.fused:
         fused_layer(a, mode)
+        return
+    if a.ops:
+        layer_ops(a)
         return
 
     import torch

@@ -1,5 +1,5 @@
 """Loads libcfattn.so (built in-tree by cpuforge_amd/build.py) and declares
-the C ABI of include/cfattn.h for ctypes.
+the C ABI of include/cfattn.h and include/cfops.h for ctypes.
 
 There is no fallback: if the library is missing the import of any compute
 function raises, so nothing can silently run on the CPU instead of the GPU.
@@ -16,7 +16,8 @@ LIB_PATH = os.path.join(HERE, "libcfattn.so")
 OK, ERR_SHAPE, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_NOMEM = range(6)
 F32, BF16 = 0, 1
 
-# Every function include/cfattn.h declares, with (restype, argtypes).
+# Every function include/cfattn.h and include/cfops.h declare, with
+# (restype, argtypes).
 _sz = C.c_size_t
 _vp = C.c_void_p
 _fp = C.POINTER(C.c_float)
@@ -67,7 +68,23 @@ SIGNATURES = {
     "cfattn_kernel_count": (C.c_int, []),
     "cfattn_flops_fwd_bwd": (C.c_double, [Shape, _sz]),
     "cfattn_version": (C.c_char_p, []),
+    # include/cfops.h
+    "cfops_matmul": (C.c_int, [_vp, C.c_int, _vp, _vp, _vp, _sz, _sz, _sz, C.c_int, _vp]),
+    "cfops_rmsnorm_forward": (C.c_int, [_vp] * 5 + [_sz, _sz, C.c_float, _vp]),
+    "cfops_rmsnorm_backward": (C.c_int, [_vp] * 7 + [_sz, _sz, _vp]),
+    "cfops_silu_mul_forward": (C.c_int, [_vp] * 4 + [_sz, _vp]),
+    "cfops_silu_mul_backward": (C.c_int, [_vp] * 6 + [_sz, _vp]),
+    "cfops_cross_entropy_fwd_bwd": (C.c_int, [_vp] * 4 + [_sz, _sz, _fp, _vp]),
+    "cfops_lm_head_ce": (C.c_int, [_vp] * 4 + [_sz, _sz, _sz, _vp, _vp, _fp, _vp]),
+    "cfops_set_head_chunk_limit": (C.c_int, [_vp, _sz]),
+    "cfops_linear_forward": (C.c_int, [_vp] * 5 + [C.c_float] + [_sz] * 4 + [_vp] * 3),
+    "cfops_linear_backward": (C.c_int, [_vp] * 7 + [C.c_float] + [_sz] * 4 + [_vp] * 5),
+    "cfops_adamw_update": (C.c_int, [_vp] * 5 + [_sz, C.c_uint64] + [C.c_float] * 5 + [_vp]),
 }
+
+# matmul kinds of cfops_matmul (include/cfops.h)
+NN, NT, TN = 0, 1, 2
+IGNORE_INDEX = -100
 
 _lib = None
 _lock = threading.Lock()

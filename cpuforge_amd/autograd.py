@@ -1,0 +1,127 @@
+"""torch autograd functions over the layer ops of include/cfops.h, so a host
+model can run cpuforge's Layer and LM head on the GPU with every hot op in
+libcfattn.so.  Each backward keeps the reference's gradient contract (the
+`Linear::backward` / `rmsnorm_backward` / `silu_mul_backward` formulas,
+accumulating into fresh zero buffers); frozen tensors (requires_grad False)
+get no gradient work, as an empty LinGrad vector does in the reference
+(crates/model/src/linear.rs:22-27)."""
+from __future__ import annotations
+
+import torch
+
+from . import ops as P
+
+
+def _flat(x: torch.Tensor, cols: int) -> torch.Tensor:
+    return x.contiguous().view(-1, cols)
+
+
+class RMSNormFn(torch.autograd.Function):
+    """y = rmsnorm(x, w) over the last dim (crates/core/src/ops/rmsnorm.rs)."""
+
+    @staticmethod
+    def forward(ctx, x, w, eps: float):
+        dim = x.shape[-1]
+        x2 = _flat(x, dim)
+        rows = x2.shape[0]
+        y = torch.empty_like(x2)
+        rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
+        P.rmsnorm_forward(x2, w, y, rstd, rows, dim, eps)
+        ctx.save_for_backward(x2, w, rstd)
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, w, rstd = ctx.saved_tensors
+        rows, dim = x2.shape
+        dx = torch.zeros_like(x2)
+        dw = torch.zeros_like(w) if ctx.needs_input_grad[1] else None
+        P.rmsnorm_backward(_flat(dy, dim), x2, w, rstd, dx, dw, rows, dim)
+        return dx.view(dy.shape), dw, None
+
+
+class SiluMulFn(torch.autograd.Function):
+    """h = silu(g) * u (crates/core/src/ops/swiglu.rs)."""
+
+    @staticmethod
+    def forward(ctx, g, u):
+        g, u = g.contiguous(), u.contiguous()
+        h = torch.empty_like(g)
+        P.silu_mul_forward(g, u, h)
+        ctx.save_for_backward(g, u)
+        return h
+
+    @staticmethod
+    def backward(ctx, dh):
+        g, u = ctx.saved_tensors
+        dg, du = torch.zeros_like(g), torch.zeros_like(u)
+        P.silu_mul_backward(dh.contiguous(), g, u, dg, du)
+        return dg, du
+
+
+class LinearFn(torch.autograd.Function):
+    """y = x W^T (+ scale (x A^T) B^T) (crates/model/src/linear.rs:56-91)."""
+
+    @staticmethod
+    def forward(ctx, x, w, a, b, scale: float):
+        inn, out = w.shape[1], w.shape[0]
+        x2 = _flat(x, inn)
+        t = x2.shape[0]
+        y = torch.empty(t, out, device=x.device, dtype=torch.float32)
+        xs = torch.empty(t, a.shape[0], device=x.device, dtype=torch.float32) if a is not None else None
+        P.linear_forward(x2, w, t, inn, out, y, a, b, scale, xs)
+        ctx.save_for_backward(x2, xs, w, a, b)
+        ctx.scale = scale
+        return y.view(*x.shape[:-1], out)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, xs, w, a, b = ctx.saved_tensors
+        t, inn = x2.shape
+        out = w.shape[0]
+        need = ctx.needs_input_grad
+        dx = torch.zeros_like(x2)
+        gw = torch.zeros_like(w) if need[1] else None
+        ga = torch.zeros_like(a) if a is not None and need[2] else None
+        gb = torch.zeros_like(b) if b is not None and need[3] else None
+        P.linear_backward(x2, xs, _flat(dy, out), w, t, inn, out, dx, gw, ga, gb, a, b, ctx.scale)
+        return dx.view(*dy.shape[:-1], inn), gw, ga, gb, None
+
+
+class LMHeadCEFn(torch.autograd.Function):
+    """Mean cross-entropy of logits = hn head^T (model.rs:436-457); the
+    forward already forms dhn (and dhead), as cross_entropy_fwd_bwd does."""
+
+    @staticmethod
+    def forward(ctx, hn, head, targets):
+        d = hn.shape[-1]
+        h2 = _flat(hn, d)
+        t, vocab = h2.shape[0], head.shape[0]
+        dhn = torch.empty_like(h2)
+        dhead = torch.zeros_like(head) if ctx.needs_input_grad[1] else None
+        loss = P.lm_head_ce(h2, head, targets.contiguous().view(-1), t, d, vocab, dhn, dhead)
+        ctx.save_for_backward(dhn, dhead if dhead is not None else torch.empty(0))
+        ctx.has_dhead = dhead is not None
+        ctx.shape = hn.shape
+        return torch.tensor(loss, device=hn.device)
+
+    @staticmethod
+    def backward(ctx, g):
+        dhn, dhead = ctx.saved_tensors
+        return (dhn * g).view(ctx.shape), (dhead * g if ctx.has_dhead else None), None
+
+
+def rmsnorm(x, w, eps):
+    return RMSNormFn.apply(x, w, eps)
+
+
+def silu_mul(g, u):
+    return SiluMulFn.apply(g, u)
+
+
+def linear(x, w, a=None, b=None, scale=1.0):
+    return LinearFn.apply(x, w, a, b, scale)
+
+
+def lm_head_ce(hn, head, targets):
+    return LMHeadCEFn.apply(hn, head, targets)

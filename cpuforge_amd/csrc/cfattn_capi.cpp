@@ -15,160 +15,14 @@
 #include <vector>
 
 #include "cfattn.h"
+#include "cfattn_ctx.hpp"
 #include "cfattn_kernels.hpp"
-
-// Per-kernel timing for cfattn_profile_*: every launch a timed call queues is
-// bracketed by two hipEvents recorded on the launch's stream; the elapsed
-// times are summed when the caller reads them.
-struct EventTimer final : cfattn::KernelTimer {
-    struct Rec {
-        int kernel;
-        hipEvent_t a, b;
-    };
-    std::vector<hipEvent_t> pool;
-    std::vector<Rec> pending;
-    hipEvent_t open_ev = nullptr;
-    int open_kernel = -1;
-    double total_ms[cfattn::kNumKernels] = {};
-    long long launches[cfattn::kNumKernels] = {};
-    hipError_t err = hipSuccess;
-
-    hipEvent_t take() {
-        if (!pool.empty()) {
-            hipEvent_t e = pool.back();
-            pool.pop_back();
-            return e;
-        }
-        hipEvent_t e = nullptr;
-        hipError_t r = hipEventCreate(&e);
-        if (r != hipSuccess && err == hipSuccess) err = r;
-        return r == hipSuccess ? e : nullptr;
-    }
-    void begin(int kernel, hipStream_t st) override {
-        open_ev = take();
-        open_kernel = kernel;
-        if (open_ev) {
-            hipError_t r = hipEventRecord(open_ev, st);
-            if (r != hipSuccess && err == hipSuccess) err = r;
-        }
-    }
-    void end(int kernel, hipStream_t st) override {
-        hipEvent_t b = take();
-        if (!open_ev || !b || kernel != open_kernel) {
-            if (b) pool.push_back(b);
-            return;
-        }
-        hipError_t r = hipEventRecord(b, st);
-        if (r != hipSuccess && err == hipSuccess) err = r;
-        pending.push_back(Rec{kernel, open_ev, b});
-        open_ev = nullptr;
-    }
-    // Waits for every pending pair and folds it into the totals.
-    hipError_t collect() {
-        for (const Rec& r : pending) {
-            hipError_t e = hipEventSynchronize(r.b);
-            float ms = 0.0f;
-            if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.a, r.b);
-            if (e != hipSuccess && err == hipSuccess) err = e;
-            total_ms[r.kernel] += ms;
-            launches[r.kernel] += 1;
-            pool.push_back(r.a);
-            pool.push_back(r.b);
-        }
-        pending.clear();
-        hipError_t e = err;
-        err = hipSuccess;
-        return e;
-    }
-    void reset() {
-        for (int i = 0; i < cfattn::kNumKernels; i++) {
-            total_ms[i] = 0.0;
-            launches[i] = 0;
-        }
-    }
-    ~EventTimer() override {
-        for (const Rec& r : pending) {
-            (void)hipEventSynchronize(r.b);
-            pool.push_back(r.a);
-            pool.push_back(r.b);
-        }
-        for (hipEvent_t e : pool) (void)hipEventDestroy(e);
-    }
-};
-
-struct cfattn_ctx {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    int mode = CFATTN_F32;
-    std::string err;
-    std::mutex mu;
-    enum Slot { Q, K, V, O, LSE, DO_, DQ, DK, DV, QB, KB, VB, DOB, DELTA, PARTIAL, DQROT, DKROT, DS, NSLOT };
-    void* buf[NSLOT] = {};
-    size_t cap[NSLOT] = {};
-    EventTimer* timer = nullptr;  // non-null while profiling is on
-    size_t ds_limit = (size_t)8 << 30;  // stored-dS scratch limit (cfattn_set_ds_limit)
-
-    cfattn::Tuning tuning() const {
-        cfattn::Tuning t;
-        t.timer = timer;
-        return t;
-    }
-};
 
 namespace {
 
+using namespace cfcapi;
 using cfattn::Dims;
 using cfattn::Dtype;
-
-int fail(cfattn_ctx* c, int code, const char* fmt, ...) {
-    char msg[512];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(msg, sizeof msg, fmt, ap);
-    va_end(ap);
-    if (c) c->err = msg;
-    return code;
-}
-
-int hip_fail(cfattn_ctx* c, hipError_t e, const char* what) {
-    return fail(c, CFATTN_ERR_HIP, "%s: %s (%s)", what, hipGetErrorName(e), hipGetErrorString(e));
-}
-
-// Makes the context's device current for the duration of a call and restores
-// the caller's device afterwards.
-struct DeviceGuard {
-    int prev = -1;
-    bool ok = true;
-    explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
-    }
-    ~DeviceGuard() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
-
-// Grow-only device buffer of a pool slot.
-void* slot(cfattn_ctx* c, int s, size_t bytes, int* rc) {
-    if (bytes == 0) bytes = 256;
-    if (c->cap[s] >= bytes) return c->buf[s];
-    if (c->buf[s]) {
-        (void)hipFree(c->buf[s]);
-        c->buf[s] = nullptr;
-        c->cap[s] = 0;
-    }
-    size_t want = (bytes + 4095) & ~(size_t)4095;
-    void* p = nullptr;
-    hipError_t e = hipMalloc(&p, want);
-    if (e != hipSuccess) {
-        *rc = fail(c, CFATTN_ERR_NOMEM, "hipMalloc of %zu bytes failed: %s", want, hipGetErrorString(e));
-        return nullptr;
-    }
-    c->buf[s] = p;
-    c->cap[s] = want;
-    return p;
-}
 
 // Scratch for the stored-dS dQ path, or null (dQ recomputes the softmax)
 // when the path does not apply, needs more than the context's limit, or the
@@ -224,17 +78,7 @@ Dims dims_of(const cfattn_shape& s, size_t batch) {
 // on that stream (PyTorch's default stream, for one) stays ordered with ours.
 hipStream_t pick_stream(cfattn_ctx*, void* st) { return static_cast<hipStream_t>(st); }
 
-#define CF_TRY(expr)                 \
-    do {                             \
-        int _rc = (expr);            \
-        if (_rc != CFATTN_OK) return _rc; \
-    } while (0)
 
-#define CF_HIP(c, expr, what)                                    \
-    do {                                                         \
-        hipError_t _e = (expr);                                  \
-        if (_e != hipSuccess) return hip_fail((c), _e, (what));  \
-    } while (0)
 
 // Uploads an f32 host slice into a pool slot; with bf16 compute also rounds
 // it into the matching bf16 slot.  Returns the device pointer the kernels read.
@@ -410,6 +254,7 @@ int cfattn_destroy(cfattn_ctx* c) {
         c->timer = nullptr;
         for (int i = 0; i < cfattn_ctx::NSLOT; i++)
             if (c->buf[i]) (void)hipFree(c->buf[i]);
+        if (c->blas && c->blas_release) c->blas_release(c->blas);
     }
     delete c;
     return CFATTN_OK;

@@ -1,0 +1,287 @@
+// C ABI of the layer ops (declared in include/cfops.h).
+//
+// Host-side plumbing only: argument checks, scratch from the context's pool,
+// rocBLAS for the plain f32 GEMMs of matmul_* and Linear, and dispatch to the
+// gfx950 kernels of layer_ops.hip.  There is no CPU compute path.
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <climits>
+#include <cstring>
+
+#include "cfattn_ctx.hpp"
+#include "cfops.h"
+#include "cfops_kernels.hpp"
+
+namespace {
+
+using namespace cfcapi;
+
+hipStream_t to_stream(void* st) { return static_cast<hipStream_t>(st); }
+
+void release_blas(void* h) { (void)rocblas_destroy_handle(static_cast<rocblas_handle>(h)); }
+
+// The context's rocBLAS handle, created on first use: no atomics, so every
+// GEMM result is reproducible run to run.
+rocblas_handle blas(cfattn_ctx* c, int* rc) {
+    if (!c->blas) {
+        rocblas_handle h = nullptr;
+        if (rocblas_create_handle(&h) != rocblas_status_success) {
+            *rc = fail(c, CFATTN_ERR_HIP, "rocblas_create_handle failed");
+            return nullptr;
+        }
+        (void)rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed);
+        c->blas = h;
+        c->blas_release = release_blas;
+    }
+    return static_cast<rocblas_handle>(c->blas);
+}
+
+bool fits_int(size_t x) { return x <= (size_t)INT_MAX; }
+
+// Row-major C[m,n] = alpha * op(A) op(B) (+ C when acc), as matmul.rs's
+// matmul_nn / matmul_nt / matmul_tn (core/src/matmul.rs:127-147).  rocBLAS is
+// column-major, so it computes C^T = op(B)^T op(A)^T on the same memory.
+int gemm(cfattn_ctx* c, int kind, const float* a, const float* b, float* out, size_t m, size_t k, size_t n,
+         float alpha, bool acc, hipStream_t st) {
+    if (m == 0 || n == 0) return CFATTN_OK;
+    if (!fits_int(m) || !fits_int(n) || !fits_int(k))
+        return fail(c, CFATTN_ERR_UNSUPPORTED, "GEMM dimension above 2^31 (m=%zu, k=%zu, n=%zu)", m, k, n);
+    if (k == 0) {  // matmul.rs:58-67: zero C unless accumulating
+        if (!acc) CF_HIP(c, cfattn::launch_fill_zero(out, m * n, st), "zero-fill launch");
+        return CFATTN_OK;
+    }
+    int rc = CFATTN_OK;
+    rocblas_handle h = blas(c, &rc);
+    if (!h) return rc;
+    if (rocblas_set_stream(h, st) != rocblas_status_success) return fail(c, CFATTN_ERR_HIP, "rocblas_set_stream failed");
+    const float beta = acc ? 1.0f : 0.0f;
+    const rocblas_int M = (rocblas_int)n, N = (rocblas_int)m, K = (rocblas_int)k;
+    rocblas_status s;
+    switch (kind) {
+        case CFOPS_NN:
+            s = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, M, N, K, &alpha, b, (rocblas_int)n,
+                              a, (rocblas_int)k, &beta, out, (rocblas_int)n);
+            break;
+        case CFOPS_NT:
+            s = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, M, N, K, &alpha, b,
+                              (rocblas_int)k, a, (rocblas_int)k, &beta, out, (rocblas_int)n);
+            break;
+        case CFOPS_TN:
+            s = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_transpose, M, N, K, &alpha, b,
+                              (rocblas_int)n, a, (rocblas_int)m, &beta, out, (rocblas_int)n);
+            break;
+        default:
+            return fail(c, CFATTN_ERR_ARG, "unknown matmul kind %d", kind);
+    }
+    if (s != rocblas_status_success)
+        return fail(c, CFATTN_ERR_HIP, "rocblas_sgemm failed: %s", rocblas_status_to_string(s));
+    return CFATTN_OK;
+}
+
+// Rust's f32::powi at run time (compiler-rt __powisf2): square-and-multiply
+// from the low bit of the exponent, reciprocal for a negative one.
+float powi_f32(float a, int b) {
+    const bool recip = b < 0;
+    unsigned int e = recip ? (unsigned int)(-(long)b) : (unsigned int)b;
+    float r = 1.0f;
+    for (;;) {
+        if (e & 1u) r *= a;
+        e >>= 1;
+        if (e == 0) break;
+        a *= a;
+    }
+    return recip ? 1.0f / r : r;
+}
+
+// Reads the loss block after the stream has drained; reports a target out
+// of range as the reference's panic message.
+int ce_result(cfattn_ctx* c, const void* misc, const int64_t* targets, size_t vocab, float* loss, hipStream_t st) {
+    cfattn::CeMisc m{};
+    CF_HIP(c, hipMemcpyAsync(&m, misc, sizeof m, hipMemcpyDeviceToHost, st), "hipMemcpyAsync D2H loss");
+    CF_HIP(c, hipStreamSynchronize(st), "cross-entropy");
+    if (m.bad_row != INT_MAX) {
+        int64_t t = 0;
+        CF_HIP(c, hipMemcpy(&t, targets + m.bad_row, sizeof t, hipMemcpyDeviceToHost), "hipMemcpy D2H target");
+        return fail(c, CFATTN_ERR_ARG, "target %lld out of range for vocab %zu", (long long)t, vocab);
+    }
+    *loss = m.loss;
+    return CFATTN_OK;
+}
+
+#define CF_LOCK(c)                                                                        \
+    if (!(c)) return CFATTN_ERR_ARG;                                                      \
+    std::lock_guard<std::mutex> lk((c)->mu);                                              \
+    (c)->err.clear();                                                                     \
+    DeviceGuard dev_guard_((c)->device);                                                  \
+    if (!dev_guard_.ok) return fail((c), CFATTN_ERR_HIP, "hipSetDevice(%d) failed", (c)->device);
+
+}  // namespace
+
+extern "C" {
+
+int cfops_matmul(cfattn_ctx* c, int kind, const float* a, const float* b, float* out, size_t m, size_t k, size_t n,
+                 int acc, void* stream) {
+    CF_LOCK(c);
+    if ((m && n && !out) || (m && n && k && (!a || !b))) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    return gemm(c, kind, a, b, out, m, k, n, 1.0f, acc != 0, to_stream(stream));
+}
+
+int cfops_rmsnorm_forward(cfattn_ctx* c, const float* x, const float* w, float* y, float* rstd, size_t rows,
+                          size_t dim, float eps, void* stream) {
+    CF_LOCK(c);
+    if (rows == 0 || dim == 0) return CFATTN_OK;
+    if (!x || !w || !y || !rstd) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (!fits_int(dim)) return fail(c, CFATTN_ERR_UNSUPPORTED, "dim=%zu above 2^31", dim);
+    CF_HIP(c, cfattn::launch_rmsnorm_fwd(x, w, y, rstd, rows, dim, eps, to_stream(stream)), "rmsnorm forward launch");
+    return CFATTN_OK;
+}
+
+int cfops_rmsnorm_backward(cfattn_ctx* c, const float* dy, const float* x, const float* w, const float* rstd,
+                           float* dx, float* dw, size_t rows, size_t dim, void* stream) {
+    CF_LOCK(c);
+    if (rows == 0 || dim == 0) return CFATTN_OK;
+    if (!dy || !x || !w || !rstd || !dx) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (!fits_int(dim)) return fail(c, CFATTN_ERR_UNSUPPORTED, "dim=%zu above 2^31", dim);
+    float* partial = nullptr;
+    if (dw) {
+        int rc = CFATTN_OK;
+        partial = static_cast<float*>(
+            slot(c, cfattn_ctx::OPS_PARTIAL, cfattn::rmsnorm_bwd_partial_floats(rows, dim) * sizeof(float), &rc));
+        if (!partial) return rc;
+    }
+    CF_HIP(c, cfattn::launch_rmsnorm_bwd(dy, x, w, rstd, dx, dw, partial, rows, dim, to_stream(stream)),
+           "rmsnorm backward launch");
+    return CFATTN_OK;
+}
+
+int cfops_silu_mul_forward(cfattn_ctx* c, const float* g, const float* u, float* h, size_t n, void* stream) {
+    CF_LOCK(c);
+    if (n == 0) return CFATTN_OK;
+    if (!g || !u || !h) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    CF_HIP(c, cfattn::launch_silu_mul_fwd(g, u, h, n, to_stream(stream)), "silu_mul forward launch");
+    return CFATTN_OK;
+}
+
+int cfops_silu_mul_backward(cfattn_ctx* c, const float* dh, const float* g, const float* u, float* dg, float* du,
+                            size_t n, void* stream) {
+    CF_LOCK(c);
+    if (n == 0) return CFATTN_OK;
+    if (!dh || !g || !u || !dg || !du) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    CF_HIP(c, cfattn::launch_silu_mul_bwd(dh, g, u, dg, du, n, to_stream(stream)), "silu_mul backward launch");
+    return CFATTN_OK;
+}
+
+int cfops_cross_entropy_fwd_bwd(cfattn_ctx* c, const float* logits, const int64_t* targets, float* dlogits,
+                                size_t rows, size_t vocab, float* loss, void* stream) {
+    CF_LOCK(c);
+    if (!loss) return fail(c, CFATTN_ERR_ARG, "null loss");
+    *loss = 0.0f;
+    if (rows == 0) return CFATTN_OK;
+    if (!logits || !targets || !dlogits) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (rows > (size_t)INT_MAX) return fail(c, CFATTN_ERR_UNSUPPORTED, "rows=%zu above 2^31", rows);
+    const hipStream_t st = to_stream(stream);
+    int rc = CFATTN_OK;
+    void* misc = slot(c, cfattn_ctx::OPS_MISC, cfattn::kCeMiscBytes, &rc);
+    if (!misc) return rc;
+    float* row_loss = static_cast<float*>(slot(c, cfattn_ctx::OPS_ROWLOSS, rows * sizeof(float), &rc));
+    if (!row_loss) return rc;
+    CF_HIP(c, cfattn::launch_ce_begin(targets, rows, misc, st), "cross-entropy launch");
+    CF_HIP(c, cfattn::launch_ce_rows(logits, targets, dlogits, row_loss, 0, rows, vocab, misc, st),
+           "cross-entropy launch");
+    CF_HIP(c, cfattn::launch_ce_finish(targets, row_loss, rows, misc, st), "cross-entropy launch");
+    return ce_result(c, misc, targets, vocab, loss, st);
+}
+
+int cfops_set_head_chunk_limit(cfattn_ctx* c, size_t bytes) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->head_chunk_bytes = bytes;
+    return CFATTN_OK;
+}
+
+int cfops_lm_head_ce(cfattn_ctx* c, const float* hn, const float* head, const int64_t* targets, size_t t, size_t d,
+                     size_t vocab, float* dhn, float* dhead, float* loss, void* stream) {
+    CF_LOCK(c);
+    if (!loss) return fail(c, CFATTN_ERR_ARG, "null loss");
+    *loss = 0.0f;
+    if (t == 0) return CFATTN_OK;
+    if (!hn || !head || !targets || !dhn) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (vocab == 0) return fail(c, CFATTN_ERR_ARG, "vocab must be positive");
+    if (t > (size_t)INT_MAX) return fail(c, CFATTN_ERR_UNSUPPORTED, "t=%zu above 2^31", t);
+    const hipStream_t st = to_stream(stream);
+    size_t chunk = c->head_chunk_bytes / (vocab * sizeof(float));
+    if (chunk < 1) chunk = 1;
+    if (chunk > t) chunk = t;
+    int rc = CFATTN_OK;
+    void* misc = slot(c, cfattn_ctx::OPS_MISC, cfattn::kCeMiscBytes, &rc);
+    if (!misc) return rc;
+    float* row_loss = static_cast<float*>(slot(c, cfattn_ctx::OPS_ROWLOSS, t * sizeof(float), &rc));
+    if (!row_loss) return rc;
+    float* logits = static_cast<float*>(slot(c, cfattn_ctx::OPS_LOGITS, chunk * vocab * sizeof(float), &rc));
+    if (!logits) return rc;
+    CF_HIP(c, cfattn::launch_ce_begin(targets, t, misc, st), "cross-entropy launch");
+    for (size_t r0 = 0; r0 < t; r0 += chunk) {
+        const size_t nr = t - r0 < chunk ? t - r0 : chunk;
+        // logits = hn . head^T (model.rs:438), then dlogits in place.
+        CF_TRY(gemm(c, CFOPS_NT, hn + r0 * d, head, logits, nr, d, vocab, 1.0f, false, st));
+        CF_HIP(c, cfattn::launch_ce_rows(logits, targets, logits, row_loss, r0, nr, vocab, misc, st),
+               "cross-entropy launch");
+        // dhn = dlogits . head (model.rs:454, overwritten); dhead += dlogits^T . hn (:457).
+        CF_TRY(gemm(c, CFOPS_NN, logits, head, dhn + r0 * d, nr, vocab, d, 1.0f, false, st));
+        if (dhead) CF_TRY(gemm(c, CFOPS_TN, logits, hn + r0 * d, dhead, vocab, nr, d, 1.0f, true, st));
+    }
+    CF_HIP(c, cfattn::launch_ce_finish(targets, row_loss, t, misc, st), "cross-entropy launch");
+    return ce_result(c, misc, targets, vocab, loss, st);
+}
+
+int cfops_linear_forward(cfattn_ctx* c, const float* x, const float* w, const float* lora_a, const float* lora_b,
+                         float lora_scale, size_t t, size_t in, size_t out, size_t rank, float* y, float* xs,
+                         void* stream) {
+    CF_LOCK(c);
+    if (t == 0 || out == 0) return CFATTN_OK;
+    if (!x || !w || !y) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (lora_a && (!lora_b || !xs || rank == 0)) return fail(c, CFATTN_ERR_ARG, "adapter needs A, B, xs and rank > 0");
+    const hipStream_t st = to_stream(stream);
+    // linear.rs:58-69
+    CF_TRY(gemm(c, CFOPS_NT, x, w, y, t, in, out, 1.0f, false, st));
+    if (!lora_a) return CFATTN_OK;
+    CF_TRY(gemm(c, CFOPS_NT, x, lora_a, xs, t, in, rank, lora_scale, false, st));
+    return gemm(c, CFOPS_NT, xs, lora_b, y, t, rank, out, 1.0f, true, st);
+}
+
+int cfops_linear_backward(cfattn_ctx* c, const float* x, const float* xs, const float* dy, const float* w,
+                          const float* lora_a, const float* lora_b, float lora_scale, size_t t, size_t in, size_t out,
+                          size_t rank, float* dx, float* gw, float* ga, float* gb, void* stream) {
+    CF_LOCK(c);
+    if (t == 0) return CFATTN_OK;
+    if (!x || !dy || !w || !dx) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (lora_a && (!lora_b || !xs || rank == 0)) return fail(c, CFATTN_ERR_ARG, "adapter needs A, B, xs and rank > 0");
+    const hipStream_t st = to_stream(stream);
+    // linear.rs:75-90
+    CF_TRY(gemm(c, CFOPS_NN, dy, w, dx, t, out, in, 1.0f, true, st));
+    if (gw) CF_TRY(gemm(c, CFOPS_TN, dy, x, gw, out, t, in, 1.0f, true, st));
+    if (!lora_a) return CFATTN_OK;
+    if (gb) CF_TRY(gemm(c, CFOPS_TN, dy, xs, gb, out, t, rank, 1.0f, true, st));
+    int rc = CFATTN_OK;
+    float* dxa = static_cast<float*>(slot(c, cfattn_ctx::OPS_DXA, t * rank * sizeof(float), &rc));
+    if (!dxa) return rc;
+    CF_TRY(gemm(c, CFOPS_NN, dy, lora_b, dxa, t, out, rank, lora_scale, false, st));
+    if (ga) CF_TRY(gemm(c, CFOPS_TN, dxa, x, ga, rank, t, in, 1.0f, true, st));
+    return gemm(c, CFOPS_NN, dxa, lora_a, dx, t, rank, in, 1.0f, true, st);
+}
+
+int cfops_adamw_update(cfattn_ctx* c, float* p, const float* g, float* m, float* v, size_t n, uint64_t t, float lr,
+                       float beta1, float beta2, float eps, float weight_decay, void* stream) {
+    CF_LOCK(c);
+    if (n == 0) return CFATTN_OK;
+    if (!p || !g || !m || !v) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    // optim.rs:21-22: the bias corrections, `t as i32` as in the reference.
+    const float bc1 = 1.0f - powi_f32(beta1, (int)(int32_t)t);
+    const float bc2 = 1.0f - powi_f32(beta2, (int)(int32_t)t);
+    CF_HIP(c, cfattn::launch_adamw(p, g, m, v, n, lr, beta1, beta2, eps, weight_decay, bc1, bc2, to_stream(stream)),
+           "adamw launch");
+    return CFATTN_OK;
+}
+
+}  // extern "C"

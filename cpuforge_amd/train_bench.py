@@ -21,9 +21,13 @@ the tier's metric. It follows the reference's `cpuforge bench-train`
   `batch` sequences in one device pass. tok/s = batch·seq / step time.
 
 The attention of every layer is `cpuforge_amd.layer.layer_attention`, the
-fused RoPE + attention kernels. The projections and the LM head are plain
-torch matmuls (rocBLAS/hipBLASLt), because only the attention op is the path
-this library replaces.
+fused RoPE + attention kernels.  With `backend="cfops"` (the default) every
+other op of the step also runs through libcfattn.so (include/cfops.h, via
+`cpuforge_amd.autograd`): RMSNorm, the LoRA linears (rocBLAS GEMMs), the
+SwiGLU gate and the LM head with its cross-entropy, whose [t, vocab] logits
+are formed a chunk of rows at a time.  Only the embedding gather and the
+residual adds stay torch ops.  `backend="torch"` runs those ops as plain torch
+ops instead, for comparison.
 """
 from __future__ import annotations
 
@@ -32,6 +36,7 @@ import time
 import torch
 import torch.nn.functional as F
 
+from . import autograd as A
 from .layer import LayerRope, layer_attention
 from .rope import RopeCache
 
@@ -48,7 +53,9 @@ class LoRALinear:
         self.b = torch.zeros(out, rank, device=device, dtype=dtype, requires_grad=True)
         self.scale = alpha / rank
 
-    def __call__(self, x):
+    def __call__(self, x, backend="torch"):
+        if backend == "cfops":
+            return A.linear(x, self.w, self.a, self.b, self.scale)
         return x @ self.w.t() + (self.scale * (x @ self.a.t())) @ self.b.t()
 
     def params(self):
@@ -61,9 +68,13 @@ def rmsnorm(x, w, eps):
 
 class SmolLM:
     def __init__(self, layers: int = 30, seq: int = 512, rank: int = 16, dtype=torch.float32, device="cuda",
-                 seed: int = 1, attn_dtype=None):
+                 seed: int = 1, attn_dtype=None, backend: str = "cfops"):
+        if backend not in ("cfops", "torch"):
+            raise ValueError(f"unknown backend {backend!r}")
+        if backend == "cfops" and dtype != torch.float32:
+            raise ValueError("the cfops backend runs the reference's f32 arithmetic")
         c = SMOLLM_135M
-        self.c, self.dtype, self.layers_n = c, dtype, layers
+        self.c, self.dtype, self.layers_n, self.backend = c, dtype, layers, backend
         self.attn_dtype = attn_dtype or dtype
         gen = torch.Generator(device=device)
         gen.manual_seed(seed)
@@ -86,6 +97,8 @@ class SmolLM:
         return out
 
     def loss(self, tokens, targets):
+        if self.backend == "cfops":
+            return self._loss_cfops(tokens, targets)
         c = self.c
         B, S = tokens.shape
         x = self.embed[tokens]
@@ -102,12 +115,31 @@ class SmolLM:
         logits = hn @ self.embed.t()
         return F.cross_entropy(logits.view(-1, c["vocab"]).float(), targets.view(-1))
 
+    def _loss_cfops(self, tokens, targets):
+        """Layer::forward (crates/model/src/layer.rs:90-143) per layer, then the
+        final norm and the tied LM head with its loss (model.rs:436-442), every
+        op but the gather and the residual adds in libcfattn.so."""
+        c, cf = self.c, "cfops"
+        B, S = tokens.shape
+        x = self.embed[tokens]
+        for layer in self.layers:
+            n1 = A.rmsnorm(x, layer["attn_norm"], c["eps"])
+            q = layer["wq"](n1, cf).view(B, S, c["heads"], c["head_dim"])
+            k = layer["wk"](n1, cf).view(B, S, c["kv_heads"], c["head_dim"])
+            v = layer["wv"](n1, cf).view(B, S, c["kv_heads"], c["head_dim"])
+            o = self.attention(q, k, v.to(self.attn_dtype), self.rope)
+            x = x + layer["wo"](o.view(B, S, -1), cf)
+            n2 = A.rmsnorm(x, layer["mlp_norm"], c["eps"])
+            x = x + layer["down"](A.silu_mul(layer["gate"](n2, cf), layer["up"](n2, cf)), cf)
+        hn = A.rmsnorm(x, self.final_norm, c["eps"])
+        return A.lm_head_ce(hn, self.embed, targets)
+
 
 def train_tok_s(batch: int = 8, seq: int = 512, layers: int = 30, rank: int = 16, steps: int = 3,
-                dtype=torch.float32, attn_dtype=None, device="cuda") -> dict:
+                dtype=torch.float32, attn_dtype=None, device="cuda", backend: str = "cfops") -> dict:
     """Build the model, warm up one step, time `steps` forward+backward
     passes; returns tok/s and the step time."""
-    model = SmolLM(layers, seq, rank, dtype, device, attn_dtype=attn_dtype)
+    model = SmolLM(layers, seq, rank, dtype, device, attn_dtype=attn_dtype, backend=backend)
     gen = torch.Generator(device=device)
     gen.manual_seed(7)
     tokens = torch.randint(0, model.c["vocab"], (batch, seq), generator=gen, device=device)
@@ -130,4 +162,5 @@ def train_tok_s(batch: int = 8, seq: int = 512, layers: int = 30, rank: int = 16
     per = (time.perf_counter() - t0) / steps
     return {"value": batch * seq / per, "unit": "tok/s", "ms_per_step": per * 1e3, "batch": batch, "seq": seq,
             "layers": layers, "lora_rank": rank, "dtype": str(dtype).replace("torch.", ""),
-            "attn_dtype": str(attn_dtype or dtype).replace("torch.", ""), "steps": steps, "first_loss": loss0}
+            "attn_dtype": str(attn_dtype or dtype).replace("torch.", ""), "steps": steps, "first_loss": loss0,
+            "backend": backend}

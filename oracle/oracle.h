@@ -44,6 +44,18 @@ int orc_rope_apply(const float* cos_t, const float* sin_t, size_t max_pos, size_
 void orc_rmsnorm_forward(const float* x, const float* w, float* y, float* rstd, size_t rows, size_t dim, float eps);
 void orc_rmsnorm_backward(const float* dy, const float* x, const float* w, const float* rstd, float* dx, float* dw,
                           size_t rows, size_t dim);
+void orc_silu_mul_forward(const float* g, const float* u, float* h, size_t n);
+void orc_silu_mul_backward(const float* dh, const float* g, const float* u, float* dg, float* du, size_t n);
+float orc_cross_entropy_fwd_bwd(const float* logits, const int64_t* targets, float* dlogits, size_t rows,
+                                size_t vocab, long* bad_row);
+float orc_powi_f32(float a, int b);
+void orc_adamw_update(float* p, const float* g, float* m, float* v, size_t n, uint64_t t, float lr, float beta1,
+                      float beta2, float eps, float weight_decay);
+void orc_linear_forward(const float* x, const float* w, const float* a, const float* b, float scale, size_t t,
+                        size_t in, size_t out, size_t r, float* y, float* xs);
+void orc_linear_backward(const float* x, const float* xs, const float* dy, const float* w, const float* a,
+                         const float* b, float scale, size_t t, size_t in, size_t out, size_t r, float* dx, float* gw,
+                         float* ga, float* gb, float* dxa);
 uint16_t orc_f32_to_bf16(float f);
 void orc_round_bf16(const float* src, float* dst, size_t n);
 double orc_grad_close_metric(const float* a, const double* n, size_t len, size_t* worst_i);

@@ -1,10 +1,10 @@
-"""ctypes binding of the C attention oracle (oracle/liboracle.so).
+"""ctypes binding of the C attention and layer-op oracle (oracle/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg, as the checker.  The product package
 (cpuforge_amd) never imports this module.
 
-Every function mirrors one in cforge_oracle.c, which cites the reference
+Every function mirrors one in cforge_oracle.c or oracle_layer.c, which cite the reference
 file:line it restates.  Arrays are numpy, C-contiguous; the caller owns them,
 as in the reference where callers lend slices.
 """
@@ -22,6 +22,7 @@ _lib = None
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
 _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
 _sz = C.c_size_t
 
@@ -77,6 +78,20 @@ def lib():
         L.orc_round_bf16.argtypes = [_f32p, _f32p, _sz]
         L.orc_grad_close_metric.restype = C.c_double
         L.orc_grad_close_metric.argtypes = [_f32p, _f64p, _sz, C.POINTER(C.c_size_t)]
+        L.orc_silu_mul_forward.restype = None
+        L.orc_silu_mul_forward.argtypes = [_f32p] * 3 + [_sz]
+        L.orc_silu_mul_backward.restype = None
+        L.orc_silu_mul_backward.argtypes = [_f32p] * 5 + [_sz]
+        L.orc_cross_entropy_fwd_bwd.restype = C.c_float
+        L.orc_cross_entropy_fwd_bwd.argtypes = [_f32p, _i64p, _f32p, _sz, _sz, C.POINTER(C.c_long)]
+        L.orc_powi_f32.restype = C.c_float
+        L.orc_powi_f32.argtypes = [C.c_float, C.c_int]
+        L.orc_adamw_update.restype = None
+        L.orc_adamw_update.argtypes = [_f32p] * 4 + [_sz, C.c_uint64] + [C.c_float] * 5
+        L.orc_linear_forward.restype = None
+        L.orc_linear_forward.argtypes = [C.c_void_p] * 4 + [C.c_float] + [_sz] * 4 + [C.c_void_p] * 2
+        L.orc_linear_backward.restype = None
+        L.orc_linear_backward.argtypes = [C.c_void_p] * 6 + [C.c_float] + [_sz] * 4 + [C.c_void_p] * 5
         _lib = L
     return _lib
 
@@ -199,6 +214,59 @@ def rmsnorm_forward(x, w, y, rstd, rows, dim, eps):
 
 def rmsnorm_backward(dy, x, w, rstd, dx, dw, rows, dim):
     lib().orc_rmsnorm_backward(dy, x, w, rstd, dx, dw, rows, dim)
+
+
+# ----------------------------------------------- layer ops (oracle_layer.c)
+IGNORE_INDEX = -100  # crates/core/src/ops/loss.rs:4
+
+
+def silu_mul_forward(g, u, h):
+    """crates/core/src/ops/swiglu.rs:10-16: h = silu(g) * u (overwrites h)."""
+    lib().orc_silu_mul_forward(g, u, h, g.size)
+
+
+def silu_mul_backward(dh, g, u, dg, du):
+    """crates/core/src/ops/swiglu.rs:18-30: accumulates into dg, du."""
+    lib().orc_silu_mul_backward(dh, g, u, dg, du, g.size)
+
+
+def cross_entropy_fwd_bwd(logits, targets, dlogits, rows, vocab):
+    """crates/core/src/ops/loss.rs:9-55: mean cross-entropy, dlogits
+    overwritten.  Raises ValueError where the reference panics (a target out
+    of range)."""
+    bad = C.c_long(-1)
+    loss = lib().orc_cross_entropy_fwd_bwd(logits, np.ascontiguousarray(targets, dtype=np.int64), dlogits, rows,
+                                           vocab, C.byref(bad))
+    if bad.value >= 0:
+        raise ValueError(f"target {int(targets[bad.value])} out of range for vocab {vocab}")
+    return float(loss)
+
+
+def powi_f32(a: float, b: int) -> float:
+    return lib().orc_powi_f32(a, b)
+
+
+def adamw_update(p, g, m, v, t, lr, beta1, beta2, eps, weight_decay):
+    """crates/train/src/optim.rs:9-30, in place on p, m, v."""
+    lib().orc_adamw_update(p, g, m, v, p.size, t, lr, beta1, beta2, eps, weight_decay)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def linear_forward(x, w, a, b, scale, t, inn, out, r, y, xs):
+    """Linear::forward (crates/model/src/linear.rs:56-71); a/b/xs None
+    without an adapter."""
+    lib().orc_linear_forward(_ptr(x), _ptr(w), _ptr(a), _ptr(b), scale, t, inn, out, r, _ptr(y), _ptr(xs))
+
+
+def linear_backward(x, xs, dy, w, a, b, scale, t, inn, out, r, dx, gw=None, ga=None, gb=None):
+    """Linear::backward (crates/model/src/linear.rs:73-91): accumulates into
+    dx and every gradient given."""
+    dxa = np.zeros(t * max(r, 1), dtype=np.float32)
+    lib().orc_linear_backward(_ptr(x), _ptr(xs), _ptr(dy), _ptr(w), _ptr(a), _ptr(b), scale, t, inn, out, r, _ptr(dx),
+                              _ptr(gw), _ptr(ga), _ptr(gb), _ptr(dxa))
 
 
 # ---------------------------------------------------------------- bf16

@@ -1,6 +1,6 @@
 """CPU tests of the C ABI (no GPU needed): libcfattn.so loads, exports every
-function include/cfattn.h declares, the ctypes table covers them, and the
-host-only helpers agree with the oracle."""
+function include/cfattn.h and include/cfops.h declare, the ctypes table
+covers them, and the host-only helpers agree with the oracle."""
 import ctypes as C
 import os
 import re
@@ -12,13 +12,15 @@ from cpuforge_amd import _lib
 from oracle import oracle as O
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "cfattn.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("cfattn.h", "cfops.h")]
+
+
+def header_text():
+    return re.sub(r"/\*.*?\*/", "", "\n".join(open(h).read() for h in HEADERS), flags=re.S)
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(cfattn_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(cf(?:attn|ops)_\w+)\s*\(", header_text())))
 
 
 def test_header_declares_the_reference_interface():
@@ -36,10 +38,9 @@ def test_library_exports_every_declared_symbol():
 
 
 def declared_arities():
-    """Parameter count of every function include/cfattn.h declares."""
-    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    """Parameter count of every function the headers declare."""
     out = {}
-    for name, params in re.findall(r"\b(cfattn_\w+)\s*\(([^)]*)\)\s*;", text):
+    for name, params in re.findall(r"\b(cf(?:attn|ops)_\w+)\s*\(([^)]*)\)\s*;", header_text()):
         params = params.strip()
         out[name] = 0 if params in ("", "void") else params.count(",") + 1
     return out
@@ -52,6 +53,22 @@ def test_ctypes_table_matches_header():
     # a missing trailing argument would make ctypes pass a 64-bit pointer as int
     wrong = {n: (len(args), arity[n]) for n, (_, args) in _lib.SIGNATURES.items() if len(args) != arity[n]}
     assert not wrong, f"ctypes argument counts differ from the header: {wrong}"
+
+
+def test_layer_op_header_declares_the_reference_ops():
+    names = declared_functions()
+    for n in ("cfops_matmul", "cfops_rmsnorm_forward", "cfops_rmsnorm_backward", "cfops_silu_mul_forward",
+              "cfops_silu_mul_backward", "cfops_cross_entropy_fwd_bwd", "cfops_lm_head_ce", "cfops_linear_forward",
+              "cfops_linear_backward", "cfops_adamw_update"):
+        assert n in names
+
+
+def test_layer_ops_reject_a_null_context():
+    L = _lib.lib()
+    assert L.cfops_rmsnorm_forward(None, None, None, None, None, 1, 1, 1e-5, None) == _lib.ERR_ARG
+    assert L.cfops_matmul(None, 0, None, None, None, 1, 1, 1, 0, None) == _lib.ERR_ARG
+    loss = C.c_float(0)
+    assert L.cfops_cross_entropy_fwd_bwd(None, None, None, None, 1, 1, C.byref(loss), None) == _lib.ERR_ARG
 
 
 def test_rope_table_matches_oracle_bitwise():

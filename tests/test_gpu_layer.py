@@ -143,13 +143,16 @@ def _reference_loss(model, tokens, targets):
     return F.cross_entropy(logits.view(-1, c["vocab"]), targets.cpu().view(-1)), leaves
 
 
-def test_smollm_lora_train_step_matches_float64_reference():
+@pytest.mark.parametrize("backend", ["cfops", "torch"])
+def test_smollm_lora_train_step_matches_float64_reference(backend):
     """Two layers of the SmolLM-135M shape, batch 2, seq 48: loss and every
-    LoRA gradient against the float64 CPU model with the reference attention."""
+    LoRA gradient against the float64 CPU model with the reference attention,
+    with the layer ops in libcfattn.so (cfops) or as torch ops."""
     import torch
 
     from cpuforge_amd.train_bench import SmolLM
-    model = SmolLM(layers=2, seq=48, rank=16)
+    print(f"smollm backend={backend}", flush=True)
+    model = SmolLM(layers=2, seq=48, rank=16, backend=backend)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(11)
     tokens = torch.randint(0, model.c["vocab"], (2, 48), generator=gen, device="cuda")
