@@ -16,6 +16,18 @@ def _flat(x: torch.Tensor, cols: int) -> torch.Tensor:
     return x.contiguous().view(-1, cols)
 
 
+def _zeros(*likes):
+    """Zero-filled buffers shaped like `likes` (None entries stay None), cut
+    from one allocation so they cost one fill launch."""
+    sizes = [t.numel() if t is not None else 0 for t in likes]
+    flat = torch.zeros(sum(sizes), device=next(t for t in likes if t is not None).device, dtype=torch.float32)
+    out, off = [], 0
+    for t, n in zip(likes, sizes):
+        out.append(None if t is None else flat[off:off + n].view(t.shape))
+        off += n
+    return out
+
+
 class RMSNormFn(torch.autograd.Function):
     """y = rmsnorm(x, w) over the last dim (crates/core/src/ops/rmsnorm.rs)."""
 
@@ -34,8 +46,7 @@ class RMSNormFn(torch.autograd.Function):
     def backward(ctx, dy):
         x2, w, rstd = ctx.saved_tensors
         rows, dim = x2.shape
-        dx = torch.zeros_like(x2)
-        dw = torch.zeros_like(w) if ctx.needs_input_grad[1] else None
+        dx, dw = _zeros(x2, w if ctx.needs_input_grad[1] else None)
         P.rmsnorm_backward(_flat(dy, dim), x2, w, rstd, dx, dw, rows, dim)
         return dx.view(dy.shape), dw, None
 
@@ -54,7 +65,7 @@ class SiluMulFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dh):
         g, u = ctx.saved_tensors
-        dg, du = torch.zeros_like(g), torch.zeros_like(u)
+        dg, du = _zeros(g, u)
         P.silu_mul_backward(dh.contiguous(), g, u, dg, du)
         return dg, du
 
@@ -80,10 +91,8 @@ class LinearFn(torch.autograd.Function):
         t, inn = x2.shape
         out = w.shape[0]
         need = ctx.needs_input_grad
-        dx = torch.zeros_like(x2)
-        gw = torch.zeros_like(w) if need[1] else None
-        ga = torch.zeros_like(a) if a is not None and need[2] else None
-        gb = torch.zeros_like(b) if b is not None and need[3] else None
+        dx, gw, ga, gb = _zeros(x2, w if need[1] else None, a if a is not None and need[2] else None,
+                                b if b is not None and need[3] else None)
         P.linear_backward(x2, xs, _flat(dy, out), w, t, inn, out, dx, gw, ga, gb, a, b, ctx.scale)
         return dx.view(*dy.shape[:-1], inn), gw, ga, gb, None
 

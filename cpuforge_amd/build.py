@@ -64,8 +64,8 @@ def build(verbose: bool = False) -> str:
     if failed:
         raise RuntimeError("hipcc failed:\n" + "\n".join(failed))
     tmp = LIB + ".tmp"
-    # rocBLAS runs the plain f32 GEMMs of the layer ops (matmul_*, Linear).
-    cmd = [cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp, "-L/opt/rocm/lib", "-lrocblas"]
+    # hipBLASLt runs the plain f32 GEMMs of the layer ops (matmul_*, Linear).
+    cmd = [cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp, "-L/opt/rocm/lib", "-lhipblaslt"]
     out = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if out.returncode != 0:
         raise RuntimeError("link failed:\n" + _filter(out.stdout))

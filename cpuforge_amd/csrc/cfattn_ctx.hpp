@@ -101,15 +101,16 @@ struct cfattn_ctx {
     enum Slot {
         Q, K, V, O, LSE, DO_, DQ, DK, DV, QB, KB, VB, DOB, DELTA, PARTIAL, DQROT, DKROT, DS,
         // layer ops (cfops_capi.cpp)
-        OPS_PARTIAL, OPS_ROWLOSS, OPS_MISC, OPS_LOGITS, OPS_DXA,
+        OPS_PARTIAL, OPS_ROWLOSS, OPS_MISC, OPS_LOGITS, OPS_DXA, OPS_WS,
         NSLOT
     };
     void* buf[NSLOT] = {};
     size_t cap[NSLOT] = {};
     EventTimer* timer = nullptr;  // non-null while profiling is on
     size_t ds_limit = (size_t)8 << 30;  // stored-dS scratch limit (cfattn_set_ds_limit)
-    // rocBLAS handle of the layer ops, created on first use; released by
-    // cfattn_destroy through blas_release.
+    // GEMM library state of the layer ops (hipBLASLt handle and per-shape
+    // plans), created on first use; released by cfattn_destroy through
+    // blas_release.
     void* blas = nullptr;
     void (*blas_release)(void*) = nullptr;
     size_t head_chunk_bytes = (size_t)512 << 20;  // logits buffer limit of cfops_lm_head_ce

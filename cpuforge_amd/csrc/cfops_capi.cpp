@@ -1,13 +1,15 @@
 // C ABI of the layer ops (declared in include/cfops.h).
 //
 // Host-side plumbing only: argument checks, scratch from the context's pool,
-// rocBLAS for the plain f32 GEMMs of matmul_* and Linear, and dispatch to the
-// gfx950 kernels of layer_ops.hip.  There is no CPU compute path.
+// hipBLASLt for the plain f32 GEMMs of matmul_* and Linear, and dispatch to
+// the gfx950 kernels of layer_ops.hip.  There is no CPU compute path.
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <climits>
 #include <cstring>
+#include <map>
+#include <tuple>
 
 #include "cfattn_ctx.hpp"
 #include "cfops.h"
@@ -19,29 +21,53 @@ using namespace cfcapi;
 
 hipStream_t to_stream(void* st) { return static_cast<hipStream_t>(st); }
 
-void release_blas(void* h) { (void)rocblas_destroy_handle(static_cast<rocblas_handle>(h)); }
+// hipBLASLt state of a context: the handle and, per GEMM shape, the
+// descriptors and the algorithm its heuristic picked (queried once).
+struct GemmPlan {
+    hipblasLtMatmulDesc_t op = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+    size_t ws = 0;
+};
+struct BlasState {
+    hipblasLtHandle_t h = nullptr;
+    std::map<std::tuple<int, size_t, size_t, size_t>, GemmPlan> plans;
+    ~BlasState() {
+        for (auto& kv : plans) {
+            GemmPlan& p = kv.second;
+            if (p.a) (void)hipblasLtMatrixLayoutDestroy(p.a);
+            if (p.b) (void)hipblasLtMatrixLayoutDestroy(p.b);
+            if (p.c) (void)hipblasLtMatrixLayoutDestroy(p.c);
+            if (p.op) (void)hipblasLtMatmulDescDestroy(p.op);
+        }
+        if (h) (void)hipblasLtDestroy(h);
+    }
+};
+constexpr size_t kGemmWorkspace = (size_t)32 << 20;
 
-// The context's rocBLAS handle, created on first use: no atomics, so every
-// GEMM result is reproducible run to run.
-rocblas_handle blas(cfattn_ctx* c, int* rc) {
+void release_blas(void* p) { delete static_cast<BlasState*>(p); }
+
+BlasState* blas(cfattn_ctx* c, int* rc) {
     if (!c->blas) {
-        rocblas_handle h = nullptr;
-        if (rocblas_create_handle(&h) != rocblas_status_success) {
-            *rc = fail(c, CFATTN_ERR_HIP, "rocblas_create_handle failed");
+        BlasState* bs = new BlasState();
+        if (hipblasLtCreate(&bs->h) != HIPBLAS_STATUS_SUCCESS) {
+            delete bs;
+            *rc = fail(c, CFATTN_ERR_HIP, "hipblasLtCreate failed");
             return nullptr;
         }
-        (void)rocblas_set_atomics_mode(h, rocblas_atomics_not_allowed);
-        c->blas = h;
+        c->blas = bs;
         c->blas_release = release_blas;
     }
-    return static_cast<rocblas_handle>(c->blas);
+    return static_cast<BlasState*>(c->blas);
 }
 
 bool fits_int(size_t x) { return x <= (size_t)INT_MAX; }
 
 // Row-major C[m,n] = alpha * op(A) op(B) (+ C when acc), as matmul.rs's
-// matmul_nn / matmul_nt / matmul_tn (core/src/matmul.rs:127-147).  rocBLAS is
-// column-major, so it computes C^T = op(B)^T op(A)^T on the same memory.
+// matmul_nn / matmul_nt / matmul_tn (core/src/matmul.rs:127-147).  hipBLASLt
+// is column-major, so it computes C^T = op(B)^T op(A)^T on the same memory:
+// an n x m column-major product whose first operand is B.  f32 inputs,
+// f32 compute (HIPBLAS_COMPUTE_32F, no reduced-precision shortcut).
 int gemm(cfattn_ctx* c, int kind, const float* a, const float* b, float* out, size_t m, size_t k, size_t n,
          float alpha, bool acc, hipStream_t st) {
     if (m == 0 || n == 0) return CFATTN_OK;
@@ -51,31 +77,61 @@ int gemm(cfattn_ctx* c, int kind, const float* a, const float* b, float* out, si
         if (!acc) CF_HIP(c, cfattn::launch_fill_zero(out, m * n, st), "zero-fill launch");
         return CFATTN_OK;
     }
+    if (kind != CFOPS_NN && kind != CFOPS_NT && kind != CFOPS_TN)
+        return fail(c, CFATTN_ERR_ARG, "unknown matmul kind %d", kind);
     int rc = CFATTN_OK;
-    rocblas_handle h = blas(c, &rc);
-    if (!h) return rc;
-    if (rocblas_set_stream(h, st) != rocblas_status_success) return fail(c, CFATTN_ERR_HIP, "rocblas_set_stream failed");
-    const float beta = acc ? 1.0f : 0.0f;
-    const rocblas_int M = (rocblas_int)n, N = (rocblas_int)m, K = (rocblas_int)k;
-    rocblas_status s;
-    switch (kind) {
-        case CFOPS_NN:
-            s = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, M, N, K, &alpha, b, (rocblas_int)n,
-                              a, (rocblas_int)k, &beta, out, (rocblas_int)n);
-            break;
-        case CFOPS_NT:
-            s = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, M, N, K, &alpha, b,
-                              (rocblas_int)k, a, (rocblas_int)k, &beta, out, (rocblas_int)n);
-            break;
-        case CFOPS_TN:
-            s = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_transpose, M, N, K, &alpha, b,
-                              (rocblas_int)n, a, (rocblas_int)m, &beta, out, (rocblas_int)n);
-            break;
-        default:
-            return fail(c, CFATTN_ERR_ARG, "unknown matmul kind %d", kind);
+    BlasState* bs = blas(c, &rc);
+    if (!bs) return rc;
+    void* ws = slot(c, cfattn_ctx::OPS_WS, kGemmWorkspace, &rc);
+    if (!ws) return rc;
+    auto key = std::make_tuple(kind, m, k, n);
+    auto it = bs->plans.find(key);
+    if (it == bs->plans.end()) {
+        GemmPlan p;
+        // First operand (B) and second (A) of the column-major product, as
+        // stored: NN  B n x k (ld n), A k x m (ld k);  NT  B k x n (ld k)
+        // transposed, A k x m;  TN  B n x k, A m x k (ld m) transposed.
+        const hipblasOperation_t ta = kind == CFOPS_NT ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+        const hipblasOperation_t tb = kind == CFOPS_TN ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+        const uint64_t ar = ta == HIPBLAS_OP_N ? n : k, ac = ta == HIPBLAS_OP_N ? k : n;
+        const uint64_t br = tb == HIPBLAS_OP_N ? k : m, bc = tb == HIPBLAS_OP_N ? m : k;
+        bool ok = hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) ==
+                       HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) ==
+                       HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatrixLayoutCreate(&p.a, HIP_R_32F, ar, ac, (int64_t)ar) == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatrixLayoutCreate(&p.b, HIP_R_32F, br, bc, (int64_t)br) == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipblasLtMatrixLayoutCreate(&p.c, HIP_R_32F, n, m, (int64_t)n) == HIPBLAS_STATUS_SUCCESS;
+        hipblasLtMatmulPreference_t pref = nullptr;
+        ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+        const uint64_t wsb = kGemmWorkspace;
+        ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
+                                                         sizeof wsb) == HIPBLAS_STATUS_SUCCESS;
+        hipblasLtMatmulHeuristicResult_t res[1];
+        int nres = 0;
+        ok = ok && hipblasLtMatmulAlgoGetHeuristic(bs->h, p.op, p.a, p.b, p.c, p.c, pref, 1, res, &nres) ==
+                       HIPBLAS_STATUS_SUCCESS && nres > 0;
+        if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
+        if (ok) {
+            p.algo = res[0].algo;
+            p.ws = res[0].workspaceSize;
+        }
+        it = bs->plans.emplace(key, p).first;
+        if (!ok) {
+            bs->plans.erase(it);
+            if (p.a) (void)hipblasLtMatrixLayoutDestroy(p.a);
+            if (p.b) (void)hipblasLtMatrixLayoutDestroy(p.b);
+            if (p.c) (void)hipblasLtMatrixLayoutDestroy(p.c);
+            if (p.op) (void)hipblasLtMatmulDescDestroy(p.op);
+            return fail(c, CFATTN_ERR_HIP, "hipBLASLt has no f32 GEMM for kind %d m=%zu k=%zu n=%zu", kind, m, k, n);
+        }
     }
-    if (s != rocblas_status_success)
-        return fail(c, CFATTN_ERR_HIP, "rocblas_sgemm failed: %s", rocblas_status_to_string(s));
+    const GemmPlan& p = it->second;
+    const float beta = acc ? 1.0f : 0.0f;
+    const hipblasStatus_t s = hipblasLtMatmul(bs->h, p.op, &alpha, b, p.a, a, p.b, &beta, out, p.c, out, p.c, &p.algo,
+                                              ws, p.ws, st);
+    if (s != HIPBLAS_STATUS_SUCCESS) return fail(c, CFATTN_ERR_HIP, "hipblasLtMatmul failed (status %d)", (int)s);
     return CFATTN_OK;
 }
 

@@ -23,7 +23,7 @@ the tier's metric. It follows the reference's `cpuforge bench-train`
 The attention of every layer is `cpuforge_amd.layer.layer_attention`, the
 fused RoPE + attention kernels.  With `backend="cfops"` (the default) every
 other op of the step also runs through libcfattn.so (include/cfops.h, via
-`cpuforge_amd.autograd`): RMSNorm, the LoRA linears (rocBLAS GEMMs), the
+`cpuforge_amd.autograd`): RMSNorm, the LoRA linears (hipBLASLt GEMMs), the
 SwiGLU gate and the LM head with its cross-entropy, whose [t, vocab] logits
 are formed a chunk of rows at a time.  Only the embedding gather and the
 residual adds stay torch ops.  `backend="torch"` runs those ops as plain torch

@@ -7,7 +7,7 @@
  * slices, so a layer's activations stay in HBM between the projections, the
  * norms and the attention (include/cfattn.h).  `stream` NULL is the device's
  * null stream.  A context (cfattn_create) provides the device, the scratch
- * pool and the rocBLAS handle of the GEMMs; calls on one context are
+ * pool and the hipBLASLt handle of the GEMMs; calls on one context are
  * serialised.  Status codes and cfattn_last_error() are those of cfattn.h.
  *
  * Reference sources (Sm0r3s-source/cpuforge, crates/...):

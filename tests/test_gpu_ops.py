@@ -6,7 +6,7 @@ Bars: bitwise where the kernel keeps the reference's order of f32 operations
 (RMSNorm forward, AdamW); otherwise the reference's own test tolerance,
 `|a - r| / (1 + |r|)` (core/src/gradcheck.rs:31-48): 1e-5 for RMSNorm's
 backward, SwiGLU and cross-entropy, whose row sums run in a parallel order,
-and matmul.rs's 1e-4 (core/src/matmul.rs:200-282) for the rocBLAS GEMMs."""
+and matmul.rs's 1e-4 (core/src/matmul.rs:200-282) for the hipBLASLt GEMMs."""
 import numpy as np
 import pytest
 import torch
@@ -190,6 +190,19 @@ def test_matmul_matches_f64(m, k, n):  # matmul.rs:200-282 SHAPES and tolerance
         c = dev(c0)
         fn(dev(A), dev(B), c, m, k, n, True)
         assert np.max(np.abs(host(c) - (want + c0)) / (1 + np.abs(want + c0))) <= 1e-4
+
+
+def test_matmul_is_repeatable():
+    """The same GEMM twice gives the same bits (no split-K atomics), at the
+    SmolLM-135M LoRA-gradient shape (m=16, k=4096, n=576) and the LM head."""
+    P = ops()
+    for m, k, n, fn in ((16, 4096, 576, P.matmul_tn), (4096, 576, 49152 // 8, P.matmul_nt)):
+        a = dev(rnd((k, m) if fn is P.matmul_tn else (m, k), 50))
+        b = dev(rnd((k, n) if fn is P.matmul_tn else (n, k), 51))
+        c1, c2 = torch.zeros(m, n, device=DEV), torch.zeros(m, n, device=DEV)
+        fn(a, b, c1, m, k, n, True)
+        fn(a, b, c2, m, k, n, True)
+        assert torch.equal(c1, c2)
 
 
 def test_matmul_k0_zeroes_or_keeps():  # matmul.rs:58-67
