@@ -19,35 +19,10 @@
 //          K/V tiles in LDS are shared across the heads of the group;
 //          S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T.
 #include "cfattn_common.hpp"
+#include "attn_params.hpp"
 #include "cfattn_kernels.hpp"
 
 namespace cfattn {
-
-struct BwdParams {
-    const void* d_o;
-    const void* q;
-    const void* k;
-    const void* v;
-    const float* o;
-    const float* lse;
-    float* delta;
-    float* dq;
-    float* dk;
-    float* dv;
-    int batch, seq, nh, nkv, hd, group;
-    // dK/dV grid
-    int kv_tile, n_kvtiles, n_wg_kv;
-    // dQ grid
-    int hpw, tpw, n_sub, n_ttiles, n_wg_q;
-    float scale, sl2;
-    long q_bs, kv_bs;
-    int vec_ok, g_vec_ok, xcd;
-    // Stored dS (fast bf16 path only, null otherwise): per (sequence, query
-    // head), the 32x32 blocks (query block qi, key block ki <= qi) of the
-    // causal triangle, block qi*(qi+1)/2 + ki, 2 KiB each (kDsBlock).
-    uint16_t* ds;
-    long ds_ntri;  // blocks per (sequence, head)
-};
 
 // delta[b][h][t] = sum_d dO[b,t,h,d] * O[b,t,h,d]; 16 lanes per row.
 template <typename T>
@@ -1212,6 +1187,7 @@ static hipError_t bwd_dp(const BwdParams& p, hipStream_t st, int kv_waves, int q
 }
 
 size_t attn_bwd_ds_bytes(Dtype dt, const Dims& d) {
+    if (dt == kF32) return attn_f32_scratch_bytes(d);
     // head_dim 128 only: at 64 the recompute costs half the matrix work per
     // stored byte and measured faster than the dS round trip through HBM.
     if (dt != kBF16 || d.hd != 128 || d.batch <= 0 || d.seq <= 0) return 0;
@@ -1319,6 +1295,17 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
             hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, 128, kDqWaves>), dim3(p.n_wg_q), dim3(64 * kDqWaves), 0, st,
                                p);
         return hipGetLastError();
+    }
+    if (dt == kF32 && attn_f32_fast_applies(d, p.vec_ok, p.g_vec_ok) && tu.bwd_kv_waves == 0 && ds != nullptr &&
+        ds_bytes >= attn_f32_scratch_bytes(d)) {
+        const long rows = (long)p.batch * p.seq * p.nh;
+        {
+            TimedLaunch tl(tu.timer, kKernBwdDelta, st);
+            hipLaunchKernelGGL((attn_bwd_delta_kernel<float>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, p);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_attn_bwd_f32(d, p, ds, st, tu.timer);
     }
     const int q_waves = p.hpw * p.tpw;
     const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;

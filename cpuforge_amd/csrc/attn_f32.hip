@@ -1,0 +1,614 @@
+// fp32 parity mode on gfx950: causal GQA attention forward, dQ and dK/dV with
+// f32 inputs and v_mfma_f32_32x32x2_f32 (exact f32 products, f32
+// accumulation), for head_dim 64 and 128 with 16-byte aligned rows.
+//
+// An f32 MFMA takes one value per lane and operand (lane l: A[l%32][l/32],
+// B[l/32][l%32]), so every operand is read row-major:
+//   - a "row" operand (K rows for S^T = K Q^T, Q/dO rows for S and dP in
+//     dK/dV) is four consecutive head dims of one row per lane, one
+//     ds_read_b128 feeding four MFMAs;
+//   - a "column" operand (V^T for O^T += V^T P^T, K^T for dQ, dO^T and Q^T for
+//     dK/dV) is one head dim per lane of one row per half-wave, a ds_read_b32.
+// Tiles go straight from global memory into LDS (global_load_lds, 16 bytes a
+// lane), one tile ahead of the compute; 16-byte chunk c of tile row r sits at
+// chunk slot c ^ swz(r) of its row, so both read shapes are bank-conflict-free
+// (see f32_swz).  The per-query softmax follows the bf16 kernels: the running
+// max moves lazily, P is formed in the exp2 domain, and the MFMA k-index of
+// every P/dS product is chosen so the accumulator registers of one product are
+// the operands of the next.
+//
+// dK/dV parallelism: a workgroup owns 128 keys of one KV head for ONE query
+// head of its group (and, on small grids, every QS-th query tile), so the
+// serial chain of a workgroup is one head's query tiles, not the whole
+// group's.  Each workgroup writes its dK/dV contribution to a scratch slot;
+// attn_f32_reduce_kernel adds the slots of a KV head in a fixed order (query
+// head, then query split), so results are reproducible bit for bit.
+#include "attn_params.hpp"
+#include "cfattn_common.hpp"
+#include "cfattn_kernels.hpp"
+
+namespace cfattn {
+
+namespace {
+
+// Chunk slot swizzle of a tile row: a bijection on r % 16 (bits 2 and 3
+// swapped), so (1) the 16 rows of a ds_read_b128 (same logical chunk) land on
+// 16 distinct 16-byte bank groups, and (2) the two half-waves of a column read
+// (rows r and r + 4 of the accumulator layout) use disjoint bank halves.
+__device__ __forceinline__ int f32_swz(int r) { return (r & 3) | ((r >> 1) & 4) | ((r << 1) & 8); }
+// Element (r, d) of a DP-wide f32 tile.
+template <int DP>
+__device__ __forceinline__ int f32_at(int r, int d) {
+    return r * DP + ((((d >> 2) ^ f32_swz(r & 15))) << 2) + (d & 3);
+}
+// Accumulator row held by lane half hh at register index r of a 32x32 block.
+__device__ __forceinline__ int acc_row(int r, int hh) { return ((r >> 2) << 3) + (hh << 2) + (r & 3); }
+
+__device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Issue this wave's share of the direct-to-LDS loads of a 32-row tile: rows
+// row0 .. row0 + 31 (clamped to last_row, so padding rows repeat finite
+// data) of a DP-wide f32 tensor with row stride `rs` floats.  A 1 KiB block
+// is 64 chunk slots; slot p holds chunk (p % CPR) ^ swz(row) of row p / CPR.
+template <int DP, int NW>
+__device__ __forceinline__ void f32_tile_dma(const float* __restrict__ g, long rs, int row0, int last_row,
+                                             float* __restrict__ tile, int wv, int lane) {
+    constexpr int CPR = DP / 4;
+    constexpr int NBLK = 32 * DP / 256;
+    constexpr int BPW = NBLK / NW;
+    static_assert(NBLK % NW == 0, "tile blocks must split evenly over the waves");
+#pragma unroll
+    for (int i = 0; i < BPW; i++) {
+        const int blk = wv * BPW + i;
+        const int slot = blk * 64 + lane;
+        const int r = slot / CPR;
+        const int c = (slot % CPR) ^ f32_swz(r & 15);
+        const long row = min(row0 + r, last_row);
+        __builtin_amdgcn_global_load_lds(g + row * rs + c * 4, tile + blk * 256, 16, 0, 0);
+    }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ forward
+// A wave owns 32 queries of one head; a workgroup of four waves covers hpw
+// heads of one GQA group x tpw query blocks and shares 32-key K/V tiles.
+template <int DP>
+__global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
+    constexpr int NW = 4, BN = 32, HALF = DP / 2, NDB = DP / 32;
+    constexpr float kLazy = 8.0f;
+    __shared__ __attribute__((aligned(16))) float sK0[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sK1[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sV0[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sV1[BN * DP];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int wv = wave_uniform(wave);
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
+    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;  // longest tiles first
+    int rest = id / p.n_ttiles;
+    const int sub = rest % p.n_sub;
+    rest /= p.n_sub;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+    const int head = g * p.group + sub * p.hpw + wave % p.hpw;
+    const int TT = 32 * p.tpw;
+    const int t_wave = tile * TT + (wave / p.hpw) * 32;
+    const int tq = t_wave + l32;
+    const int wg_end = min(p.seq, tile * TT + TT);
+    const int n_kt = (wg_end + BN - 1) / BN;
+    const bool wave_active = t_wave < p.seq;
+    const int wave_last = min(t_wave + 31, p.seq - 1);
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const float* kg = static_cast<const float*>(p.k) + (long)b * p.kv_bs + (long)g * DP;
+    const float* vg = static_cast<const float*>(p.v) + (long)b * p.kv_bs + (long)g * DP;
+
+    // Q^T operand: query tq, head dims hh*HALF + kd.
+    float qf[HALF];
+    {
+        const float* qrow = static_cast<const float*>(p.q) + (long)b * p.q_bs + (long)min(tq, p.seq - 1) * qrs +
+                            (long)head * DP + hh * HALF;
+#pragma unroll
+        for (int i = 0; i < HALF / 4; i++) {
+            const float4 v = *reinterpret_cast<const float4*>(qrow + 4 * i);
+            qf[4 * i] = v.x;
+            qf[4 * i + 1] = v.y;
+            qf[4 * i + 2] = v.z;
+            qf[4 * i + 3] = v.w;
+        }
+    }
+
+    f32x16 oacc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) oacc[i] = zero16();
+    float m2 = -INFINITY, lsum = 0.0f;
+
+    auto dma = [&](int kt, float* Kd, float* Vd) {
+        f32_tile_dma<DP, NW>(kg, kvrs, kt * BN, p.seq - 1, Kd, wv, lane);
+        f32_tile_dma<DP, NW>(vg, kvrs, kt * BN, p.seq - 1, Vd, wv, lane);
+    };
+
+    auto step = [&](int kt, const float* Ks, const float* Vs, float* Kn, float* Vn) {
+        const bool more = kt + 1 < n_kt;
+        const int k0 = kt * BN;
+        if (wave_active && k0 <= wave_last) {
+            // S^T: rows = keys k0 + [0, 32), columns = this wave's queries.
+            f32x16 sc = zero16();
+#pragma unroll
+            for (int c = 0; c < HALF / 4; c++) {
+                const float4 a = *reinterpret_cast<const float4*>(Ks + f32_at<DP>(l32, hh * HALF + 4 * c));
+                sc = mfma_f32(a.x, qf[4 * c], sc);
+                sc = mfma_f32(a.y, qf[4 * c + 1], sc);
+                sc = mfma_f32(a.z, qf[4 * c + 2], sc);
+                sc = mfma_f32(a.w, qf[4 * c + 3], sc);
+            }
+            if (more) dma(kt + 1, Kn, Vn);
+            float mx = -INFINITY;
+            const bool masked = k0 + 31 > t_wave;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                if (masked && k0 + acc_row(r, hh) > tq) sc[r] = -INFINITY;
+                mx = fmaxf(mx, sc[r]);
+            }
+            // Key k0 + 0 is unmasked for every query of the first tile, so m2
+            // is finite from the first tile on.
+            mx = max_halves(mx) * p.sl2;
+            const float mnew = mx > m2 + kLazy ? mx : m2;
+            if (__any(mnew != m2)) {
+                const float alpha = __builtin_amdgcn_exp2f(m2 - mnew);
+                lsum *= alpha;
+#pragma unroll
+                for (int i = 0; i < NDB; i++) oacc[i] *= alpha;
+                m2 = mnew;
+            }
+            float pr[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -m2));
+                lsum += pr[r];
+            }
+            // O^T += V^T P^T: product j pairs key acc_row(j, hh) of both operands.
+#pragma unroll
+            for (int db = 0; db < NDB; db++)
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    oacc[db] = mfma_f32(Vs[f32_at<DP>(acc_row(j, hh), db * 32 + l32)], pr[j], oacc[db]);
+        } else if (more) {
+            dma(kt + 1, Kn, Vn);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    };
+
+    dma(0, sK0, sV0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int kt = 0; kt < n_kt; kt += 2) {
+        step(kt, sK0, sV0, sK1, sV1);
+        if (kt + 1 < n_kt) step(kt + 1, sK1, sV1, sK0, sV0);
+    }
+
+    if (!wave_active) return;
+    const float ltot = sum_halves(lsum);
+    if (tq >= p.seq) return;
+    const float inv = 1.0f / ltot;
+    float* orow = p.o + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
+#pragma unroll
+    for (int db = 0; db < NDB; db++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++)
+            *reinterpret_cast<float4*>(orow + db * 32 + rq * 8 + hh * 4) =
+                make_float4(oacc[db][rq * 4] * inv, oacc[db][rq * 4 + 1] * inv, oacc[db][rq * 4 + 2] * inv,
+                            oacc[db][rq * 4 + 3] * inv);
+    if (hh == 0) p.lse[((long)b * p.nh + head) * p.seq + tq] = (m2 + __log2f(ltot)) * kLn2;
+}
+
+// -------------------------------------------------------------------- dQ
+// The forward's decomposition; per 32-key tile: S^T = K Q^T, dP^T = V dO^T,
+// dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T.  The softmax scale is applied
+// once to dQ.
+template <int DP>
+__global__ __launch_bounds__(256) void attn_bwd_dq_f32_kernel(const BwdParams p) {
+    constexpr int NW = 4, BN = 32, HALF = DP / 2, NDB = DP / 32;
+    __shared__ __attribute__((aligned(16))) float sK0[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sK1[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sV0[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sV1[BN * DP];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int wv = wave_uniform(wave);
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg_q, p.xcd);
+    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;
+    int rest = id / p.n_ttiles;
+    const int sub = rest % p.n_sub;
+    rest /= p.n_sub;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+    const int head = g * p.group + sub * p.hpw + wave % p.hpw;
+    const int TT = 32 * p.tpw;
+    const int t_wave = tile * TT + (wave / p.hpw) * 32;
+    const int tq = t_wave + l32;
+    const int wg_end = min(p.seq, tile * TT + TT);
+    const int n_kt = (wg_end + BN - 1) / BN;
+    const bool wave_active = t_wave < p.seq;
+    const int wave_last = min(t_wave + 31, p.seq - 1);
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const float* kg = static_cast<const float*>(p.k) + (long)b * p.kv_bs + (long)g * DP;
+    const float* vg = static_cast<const float*>(p.v) + (long)b * p.kv_bs + (long)g * DP;
+    const long qoff = (long)b * p.q_bs + (long)min(tq, p.seq - 1) * qrs + (long)head * DP + hh * HALF;
+
+    float qf[HALF], of[HALF];
+#pragma unroll
+    for (int i = 0; i < HALF / 4; i++) {
+        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + qoff + 4 * i);
+        const float4 c = *reinterpret_cast<const float4*>(static_cast<const float*>(p.d_o) + qoff + 4 * i);
+        qf[4 * i] = a.x, qf[4 * i + 1] = a.y, qf[4 * i + 2] = a.z, qf[4 * i + 3] = a.w;
+        of[4 * i] = c.x, of[4 * i + 1] = c.y, of[4 * i + 2] = c.z, of[4 * i + 3] = c.w;
+    }
+    const long lrow = ((long)b * p.nh + head) * p.seq + min(tq, p.seq - 1);
+    const float lq = p.lse[lrow] * kLog2e;
+    const float dlq = p.delta[lrow];
+
+    f32x16 acc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) acc[i] = zero16();
+
+    auto dma = [&](int kt, float* Kd, float* Vd) {
+        f32_tile_dma<DP, NW>(kg, kvrs, kt * BN, p.seq - 1, Kd, wv, lane);
+        f32_tile_dma<DP, NW>(vg, kvrs, kt * BN, p.seq - 1, Vd, wv, lane);
+    };
+    auto step = [&](int kt, const float* Ks, const float* Vs, float* Kn, float* Vn) {
+        const bool more = kt + 1 < n_kt;
+        const int k0 = kt * BN;
+        if (wave_active && k0 <= wave_last) {
+            f32x16 sc = zero16(), dp = zero16();
+#pragma unroll
+            for (int c = 0; c < HALF / 4; c++) {
+                const float4 a = *reinterpret_cast<const float4*>(Ks + f32_at<DP>(l32, hh * HALF + 4 * c));
+                const float4 v = *reinterpret_cast<const float4*>(Vs + f32_at<DP>(l32, hh * HALF + 4 * c));
+                sc = mfma_f32(a.x, qf[4 * c], sc);
+                dp = mfma_f32(v.x, of[4 * c], dp);
+                sc = mfma_f32(a.y, qf[4 * c + 1], sc);
+                dp = mfma_f32(v.y, of[4 * c + 1], dp);
+                sc = mfma_f32(a.z, qf[4 * c + 2], sc);
+                dp = mfma_f32(v.z, of[4 * c + 2], dp);
+                sc = mfma_f32(a.w, qf[4 * c + 3], sc);
+                dp = mfma_f32(v.w, of[4 * c + 3], dp);
+            }
+            if (more) dma(kt + 1, Kn, Vn);
+            const bool masked = k0 + 31 > t_wave;
+            float ds[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lq));
+                if (masked && k0 + acc_row(r, hh) > tq) pv = 0.0f;
+                ds[r] = pv * (dp[r] - dlq);
+            }
+#pragma unroll
+            for (int db = 0; db < NDB; db++)
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    acc[db] = mfma_f32(Ks[f32_at<DP>(acc_row(j, hh), db * 32 + l32)], ds[j], acc[db]);
+        } else if (more) {
+            dma(kt + 1, Kn, Vn);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    };
+
+    dma(0, sK0, sV0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int kt = 0; kt < n_kt; kt += 2) {
+        step(kt, sK0, sV0, sK1, sV1);
+        if (kt + 1 < n_kt) step(kt + 1, sK1, sV1, sK0, sV0);
+    }
+    if (!wave_active || tq >= p.seq) return;
+    float* row = p.dq + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
+#pragma unroll
+    for (int db = 0; db < NDB; db++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            float4* dst = reinterpret_cast<float4*>(row + db * 32 + rq * 8 + hh * 4);
+            float4 v = *dst;
+            v.x += acc[db][rq * 4] * p.scale;
+            v.y += acc[db][rq * 4 + 1] * p.scale;
+            v.z += acc[db][rq * 4 + 2] * p.scale;
+            v.w += acc[db][rq * 4 + 3] * p.scale;
+            *dst = v;
+        }
+}
+
+// ------------------------------------------------------------------ dK/dV
+// Workgroup = (128-key tile, query head h, sequence, query split qs): four
+// waves of 32 keys share 32-query Q/dO tiles of head h; the workgroup visits
+// the query tiles qt_begin + qs, + QS, ... that can see its keys.  Per step:
+// S = Q K^T, dP = dO V^T, P = exp2(S*scale*log2e - lse*log2e), dS = P (dP -
+// delta), dV^T += dO^T P, dK^T += Q^T dS.  The result goes to scratch slot
+// (h % group) * QS + qs of the KV head, dK already scaled.
+struct F32DkdvArgs {
+    float* part;     // dK slots [slots][batch][seq][nkv][DP], then the dV slots
+    long part_half;  // floats per slot
+    int qs_n;        // query splits QS
+    int slots;       // group * QS
+};
+
+template <int DP>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams p, const F32DkdvArgs a) {
+    constexpr int NW = 4, BM = 32, HALF = DP / 2, NDB = DP / 32;
+    __shared__ __attribute__((aligned(16))) float sQ0[BM * DP];
+    __shared__ __attribute__((aligned(16))) float sQ1[BM * DP];
+    __shared__ __attribute__((aligned(16))) float sO0[BM * DP];
+    __shared__ __attribute__((aligned(16))) float sO1[BM * DP];
+    __shared__ __attribute__((aligned(16))) float sL[2][BM];
+    __shared__ __attribute__((aligned(16))) float sD[2][BM];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int wv = wave_uniform(wave);
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
+    const int kvt = id % p.n_kvtiles;  // low key tiles see the most queries: first
+    int rest = id / p.n_kvtiles;
+    const int qs = rest % a.qs_n;
+    rest /= a.qs_n;
+    const int h = rest % p.nh;
+    const int b = rest / p.nh;
+    const int g = h / p.group;
+    const int wg_key0 = kvt * 128;
+    const int key0 = wg_key0 + wave * 32;
+    const int kw = key0 + l32;
+    const bool wave_active = key0 < p.seq;
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const float* qg = static_cast<const float*>(p.q) + (long)b * p.q_bs + (long)h * DP;
+    const float* og = static_cast<const float*>(p.d_o) + (long)b * p.q_bs + (long)h * DP;
+    const float* lse_h = p.lse + ((long)b * p.nh + h) * p.seq;
+    const float* dlt_h = p.delta + ((long)b * p.nh + h) * p.seq;
+
+    // K^T / V^T operands: key kw, head dims hh*HALF + kd.
+    float kf[HALF], vf[HALF];
+    {
+        const long off = (long)b * p.kv_bs + (long)min(kw, p.seq - 1) * kvrs + (long)g * DP + hh * HALF;
+#pragma unroll
+        for (int i = 0; i < HALF / 4; i++) {
+            const float4 x = *reinterpret_cast<const float4*>(static_cast<const float*>(p.k) + off + 4 * i);
+            const float4 y = *reinterpret_cast<const float4*>(static_cast<const float*>(p.v) + off + 4 * i);
+            kf[4 * i] = x.x, kf[4 * i + 1] = x.y, kf[4 * i + 2] = x.z, kf[4 * i + 3] = x.w;
+            vf[4 * i] = y.x, vf[4 * i + 1] = y.y, vf[4 * i + 2] = y.z, vf[4 * i + 3] = y.w;
+        }
+    }
+    f32x16 dkt[NDB], dvt[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) dkt[i] = zero16(), dvt[i] = zero16();
+
+    const int n_qt = (p.seq + BM - 1) / BM;
+    const int qt_first = wg_key0 / BM + qs;
+    const int n_steps = qt_first < n_qt ? (n_qt - qt_first + a.qs_n - 1) / a.qs_n : 0;
+    auto step_q0 = [&](int s) { return (qt_first + s * a.qs_n) * BM; };
+
+    float pl = 0.0f;
+    auto dma = [&](int s, float* Qd, float* Od) {
+        const int q0 = step_q0(s);
+        f32_tile_dma<DP, NW>(qg, qrs, q0, p.seq - 1, Qd, wv, lane);
+        f32_tile_dma<DP, NW>(og, qrs, q0, p.seq - 1, Od, wv, lane);
+        if (tid < 2 * BM) {
+            const int t = min(q0 + (tid & (BM - 1)), p.seq - 1);
+            pl = tid < BM ? lse_h[t] : dlt_h[t];
+        }
+    };
+    auto store_ld = [&](int s, int st) {
+        if (tid >= 2 * BM) return;
+        const int i = tid & (BM - 1);
+        const bool ok = step_q0(s) + i < p.seq;
+        if (tid < BM)
+            sL[st][i] = ok ? pl * kLog2e : INFINITY;  // rows past the end: P = 0
+        else
+            sD[st][i] = ok ? pl : 0.0f;
+    };
+
+    auto step = [&](int s, const float* Qs, const float* Os, float* Qn, float* On) {
+        const int st = s & 1;
+        const bool more = s + 1 < n_steps;
+        const int q0 = step_q0(s);
+        if (wave_active && q0 + BM - 1 >= key0 && q0 < p.seq) {
+            // S and dP: rows = queries q0 + [0, 32), columns = this wave's keys.
+            f32x16 sc = zero16(), dp = zero16();
+#pragma unroll
+            for (int c = 0; c < HALF / 4; c++) {
+                const float4 x = *reinterpret_cast<const float4*>(Qs + f32_at<DP>(l32, hh * HALF + 4 * c));
+                const float4 y = *reinterpret_cast<const float4*>(Os + f32_at<DP>(l32, hh * HALF + 4 * c));
+                sc = mfma_f32(x.x, kf[4 * c], sc);
+                dp = mfma_f32(y.x, vf[4 * c], dp);
+                sc = mfma_f32(x.y, kf[4 * c + 1], sc);
+                dp = mfma_f32(y.y, vf[4 * c + 1], dp);
+                sc = mfma_f32(x.z, kf[4 * c + 2], sc);
+                dp = mfma_f32(y.z, vf[4 * c + 2], dp);
+                sc = mfma_f32(x.w, kf[4 * c + 3], sc);
+                dp = mfma_f32(y.w, vf[4 * c + 3], dp);
+            }
+            if (more) dma(s + 1, Qn, On);
+            const bool masked = q0 < key0 + 31;
+            float pr[16], ds[16];
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const float4 l4 = *reinterpret_cast<const float4*>(&sL[st][g4 * 8 + hh * 4]);
+                const float4 d4 = *reinterpret_cast<const float4*>(&sD[st][g4 * 8 + hh * 4]);
+                const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = g4 * 4 + i;
+                    float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lv[i]));
+                    if (masked && kw > q0 + acc_row(r, hh)) pv = 0.0f;
+                    pr[r] = pv;
+                    ds[r] = pv * (dp[r] - dv[i]);
+                }
+            }
+            // dV^T += dO^T P and dK^T += Q^T dS; product j pairs query
+            // acc_row(j, hh) of both operands.
+#pragma unroll
+            for (int db = 0; db < NDB; db++)
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int at = f32_at<DP>(acc_row(j, hh), db * 32 + l32);
+                    dvt[db] = mfma_f32(Os[at], pr[j], dvt[db]);
+                    dkt[db] = mfma_f32(Qs[at], ds[j], dkt[db]);
+                }
+        } else if (more) {
+            dma(s + 1, Qn, On);
+        }
+        if (more) store_ld(s + 1, st ^ 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    };
+
+    if (n_steps > 0) {
+        dma(0, sQ0, sO0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        store_ld(0, 0);
+        __syncthreads();
+    }
+    for (int s = 0; s < n_steps; s += 2) {
+        step(s, sQ0, sO0, sQ1, sO1);
+        if (s + 1 < n_steps) step(s + 1, sQ1, sO1, sQ0, sO0);
+    }
+
+    if (!wave_active || kw >= p.seq) return;
+    const int slot = (h % p.group) * a.qs_n + qs;
+    const long roff = (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
+    float* pk = a.part + (long)slot * a.part_half + roff;
+    float* pv = pk + (long)a.slots * a.part_half;
+#pragma unroll
+    for (int db = 0; db < NDB; db++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            const int d = db * 32 + rq * 8 + hh * 4;
+            *reinterpret_cast<float4*>(pk + d) =
+                make_float4(dkt[db][rq * 4] * p.scale, dkt[db][rq * 4 + 1] * p.scale, dkt[db][rq * 4 + 2] * p.scale,
+                            dkt[db][rq * 4 + 3] * p.scale);
+            *reinterpret_cast<float4*>(pv + d) =
+                make_float4(dvt[db][rq * 4], dvt[db][rq * 4 + 1], dvt[db][rq * 4 + 2], dvt[db][rq * 4 + 3]);
+        }
+}
+
+// dk += sum over slots (query head of the group, then query split) of the
+// dK slots, dv likewise; four floats per thread.  Every workgroup writes its
+// slot for all of its keys (zeros where it saw no query), so every slot row
+// below seq is defined.
+__global__ __launch_bounds__(256) void attn_f32_reduce_kernel(const float* __restrict__ part, long half, int slots,
+                                                              float* __restrict__ dk, float* __restrict__ dv) {
+    const long i4 = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i4 * 4 >= half) return;
+    const float4* pk = reinterpret_cast<const float4*>(part) + i4;
+    const float4* pv = reinterpret_cast<const float4*>(part + (long)slots * half) + i4;
+    const long stride = half / 4;
+    float4 sk = pk[0], sv = pv[0];
+    for (int s = 1; s < slots; s++) {
+        const float4 a = pk[s * stride], c = pv[s * stride];
+        sk.x += a.x, sk.y += a.y, sk.z += a.z, sk.w += a.w;
+        sv.x += c.x, sv.y += c.y, sv.z += c.z, sv.w += c.w;
+    }
+    float4* dk4 = reinterpret_cast<float4*>(dk) + i4;
+    float4* dv4 = reinterpret_cast<float4*>(dv) + i4;
+    float4 x = *dk4, y = *dv4;
+    x.x += sk.x, x.y += sk.y, x.z += sk.z, x.w += sk.w;
+    y.x += sv.x, y.y += sv.y, y.z += sv.z, y.w += sv.w;
+    *dk4 = x;
+    *dv4 = y;
+}
+
+// ------------------------------------------------------------- launchers
+static bool f32_fast_ok(int hd) { return hd == 64 || hd == 128; }
+
+static int f32_hpw(int group) { return group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1; }
+
+// Query splits of the dK/dV grid: enough workgroups for two waves per SIMD.
+static int f32_qsplits(const Dims& d) {
+    const long base = (long)((d.seq + 127) / 128) * d.nh * d.batch;
+    int qs = 1;
+    while (qs < 4 && base * qs * 4 < 2048) qs *= 2;
+    return qs;
+}
+
+size_t attn_f32_scratch_bytes(const Dims& d) {
+    if (!f32_fast_ok(d.hd) || d.batch <= 0 || d.seq <= 0) return 0;
+    const size_t half = (size_t)d.batch * d.seq * d.nkv * d.hd;
+    const size_t slots = (size_t)(d.nh / d.nkv) * f32_qsplits(d);
+    return 2 * slots * half * sizeof(float);
+}
+
+bool attn_f32_fast_applies(const Dims& d, int vec_ok, int o_vec_ok) {
+    return f32_fast_ok(d.hd) && vec_ok && o_vec_ok;
+}
+
+hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, hipStream_t st, KernelTimer* tm) {
+    p.hpw = f32_hpw(p.group);
+    p.tpw = 4 / p.hpw;
+    p.n_sub = p.group / p.hpw;
+    p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
+    const long n_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+    if (n_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    p.n_wg = (int)n_wg;
+    TimedLaunch tl(tm, kKernFwd, st);
+    if (d.hd == 128)
+        hipLaunchKernelGGL(attn_fwd_f32_kernel<128>, dim3(p.n_wg), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL(attn_fwd_f32_kernel<64>, dim3(p.n_wg), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
+// dK/dV then dQ (delta is already computed); `scratch` holds
+// attn_f32_scratch_bytes(d) bytes.
+hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStream_t st, KernelTimer* tm) {
+    F32DkdvArgs a;
+    a.qs_n = f32_qsplits(d);
+    a.part = static_cast<float*>(scratch);
+    a.part_half = (long)d.batch * d.seq * d.nkv * d.hd;
+    const int slots = p.group * a.qs_n;
+    a.slots = slots;
+    p.n_kvtiles = (d.seq + 127) / 128;
+    const long nkv_wg = (long)p.n_kvtiles * a.qs_n * d.nh * d.batch;
+    if (nkv_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    p.n_wg_kv = (int)nkv_wg;
+    hipError_t e;
+    {
+        TimedLaunch tl(tm, kKernBwdDkdv, st);
+        if (d.hd == 128)
+            hipLaunchKernelGGL(attn_bwd_dkdv_f32_kernel<128>, dim3(p.n_wg_kv), dim3(256), 0, st, p, a);
+        else
+            hipLaunchKernelGGL(attn_bwd_dkdv_f32_kernel<64>, dim3(p.n_wg_kv), dim3(256), 0, st, p, a);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const long n4 = a.part_half / 4;
+        hipLaunchKernelGGL(attn_f32_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, a.part,
+                           a.part_half, slots, p.dk, p.dv);
+        e = hipGetLastError();
+    }
+    if (e != hipSuccess) return e;
+    p.hpw = f32_hpw(p.group);
+    p.tpw = 4 / p.hpw;
+    p.n_sub = p.group / p.hpw;
+    p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
+    const long nq_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+    if (nq_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    p.n_wg_q = (int)nq_wg;
+    TimedLaunch tl(tm, kKernBwdDq, st);
+    if (d.hd == 128)
+        hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<128>, dim3(p.n_wg_q), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<64>, dim3(p.n_wg_q), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
+}  // namespace cfattn

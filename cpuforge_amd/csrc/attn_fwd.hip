@@ -20,22 +20,10 @@
 // Workgroups are ordered longest-first (most key tiles) and remapped so each
 // XCD works through contiguous (sequence, KV head) ranges.
 #include "cfattn_common.hpp"
+#include "attn_params.hpp"
 #include "cfattn_kernels.hpp"
 
 namespace cfattn {
-
-struct FwdParams {
-    const void* q;
-    const void* k;
-    const void* v;
-    float* o;
-    float* lse;
-    int seq, nh, nkv, hd;
-    int group, hpw, tpw, n_sub, n_ttiles, n_wg;
-    float sl2;  // softmax scale * log2(e)
-    long q_bs, kv_bs;
-    int vec_ok, o_vec_ok, xcd;
-};
 
 template <typename T, int DP, int BN>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const FwdParams p) {
@@ -536,6 +524,9 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
                                p);
         return hipGetLastError();
     }
+    if (dt == kF32 && attn_f32_fast_applies(d, p.vec_ok, p.o_vec_ok) && tu.fwd_heads_per_wg == 0 &&
+        tu.fwd_tblocks_per_wg == 0)
+        return launch_attn_fwd_f32(d, p, st, tu.timer);
     const int nwaves = p.hpw * p.tpw;
     const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;
     if (dt == kBF16) {

@@ -1,0 +1,59 @@
+// Kernel parameter blocks of the attention kernels, shared by the files that
+// launch them (attn_fwd.hip, attn_bwd.hip, attn_f32.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "cfattn_kernels.hpp"
+
+namespace cfattn {
+
+struct FwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    float* o;
+    float* lse;
+    int seq, nh, nkv, hd;
+    int group, hpw, tpw, n_sub, n_ttiles, n_wg;
+    float sl2;  // softmax scale * log2(e)
+    long q_bs, kv_bs;
+    int vec_ok, o_vec_ok, xcd;
+};
+
+struct BwdParams {
+    const void* d_o;
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* o;
+    const float* lse;
+    float* delta;
+    float* dq;
+    float* dk;
+    float* dv;
+    int batch, seq, nh, nkv, hd, group;
+    // dK/dV grid
+    int kv_tile, n_kvtiles, n_wg_kv;
+    // dQ grid
+    int hpw, tpw, n_sub, n_ttiles, n_wg_q;
+    float scale, sl2;
+    long q_bs, kv_bs;
+    int vec_ok, g_vec_ok, xcd;
+    // Stored dS (fast bf16 path only, null otherwise): per (sequence, query
+    // head), the 32x32 blocks (query block qi, key block ki <= qi) of the
+    // causal triangle, block qi*(qi+1)/2 + ki, 2 KiB each (kDsBlock).
+    uint16_t* ds;
+    long ds_ntri;  // blocks per (sequence, head)
+};
+
+// fp32 fast path (attn_f32.hip): head_dim 64 or 128, 16-byte aligned rows.
+bool attn_f32_fast_applies(const Dims& d, int vec_ok, int o_vec_ok);
+// Scratch of the fp32 dK/dV path: the per-head (and per query split)
+// contributions before their fixed-order sum.
+size_t attn_f32_scratch_bytes(const Dims& d);
+hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, hipStream_t st, KernelTimer* tm);
+hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStream_t st, KernelTimer* tm);
+
+}  // namespace cfattn

@@ -71,6 +71,9 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
 // recomputes S and dP.  Both paths give the same result up to bf16
 // rounding of dS, which both apply.
 size_t attn_bwd_ds_bytes(Dtype dt, const Dims& d);
+// With f32 inputs the same scratch (when large enough) holds the per-head
+// dK/dV contributions of the fp32 fast path (attn_f32.hip), which
+// attn_bwd_ds_bytes reports for kF32.
 hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
                            const float* o, const float* lse, float* delta, float* dq, float* dk, float* dv,
                            hipStream_t st, const Tuning& tu, void* ds = nullptr, size_t ds_bytes = 0);
