@@ -226,14 +226,30 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_rowwise_kernel(const float* _
     }
 }
 
-// dw[i] += partial[0][i], partial[1][i], ... in block order.
+// dw[i] += the partial rows, in a fixed two-level order: a workgroup covers
+// 32 columns with eight threads per column; thread j adds the partial rows
+// j*per .. j*per + per - 1 in order, and the eight sums are then added to dw
+// in j order.  Deterministic, and the loads of one thread are independent
+// of its adds, so they stay in flight together.
 __global__ __launch_bounds__(256) void rmsnorm_dw_reduce_kernel(const float* __restrict__ partial,
                                                                 float* __restrict__ dw, long nblk, long dim) {
-    const long c = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= dim) return;
-    float s = dw[c];
-    for (long b = 0; b < nblk; b++) s = radd(s, partial[b * dim + c]);
-    dw[c] = s;
+    __shared__ float ssum[8][32];
+    const int cl = threadIdx.x & 31, j = threadIdx.x >> 5;
+    const long c = (long)blockIdx.x * 32 + cl;
+    const long per = (nblk + 7) / 8;
+    const long b0 = j * per, b1 = min(nblk, b0 + per);
+    float s = 0.0f;
+    if (c < dim) {
+#pragma unroll 8
+        for (long b = b0; b < b1; b++) s = radd(s, partial[b * dim + c]);
+    }
+    ssum[j][cl] = s;
+    __syncthreads();
+    if (j == 0 && c < dim) {
+        float t = dw[c];
+        for (int i = 0; i < 8; i++) t = radd(t, ssum[i][cl]);
+        dw[c] = t;
+    }
 }
 
 size_t rmsnorm_bwd_partial_floats(size_t rows, size_t dim) {
@@ -289,7 +305,7 @@ hipError_t launch_rmsnorm_bwd(const float* dy, const float* x, const float* w, c
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !dw) return e;
-    hipLaunchKernelGGL(rmsnorm_dw_reduce_kernel, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0, st, part, dw,
+    hipLaunchKernelGGL(rmsnorm_dw_reduce_kernel, dim3((unsigned)((dim + 31) / 32)), dim3(256), 0, st, part, dw,
                        (long)nblk, (long)dim);
     return hipGetLastError();
 }
