@@ -213,8 +213,11 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
 // The forward's decomposition; per 32-key tile: S^T = K Q^T, dP^T = V dO^T,
 // dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T.  The softmax scale is applied
 // once to dQ.
+// Two waves per SIMD at head_dim 64 (the registers fit; measured 7% faster
+// at B8 S2048 9/3 heads), one at 128.
 template <int DP>
-__global__ __launch_bounds__(256) void attn_bwd_dq_f32_kernel(const BwdParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 2 : 1, DP == 64 ? 2 : 1))) void
+attn_bwd_dq_f32_kernel(const BwdParams p) {
     constexpr int NW = 4, BN = 32, HALF = DP / 2, NDB = DP / 32;
     __shared__ __attribute__((aligned(16))) float sK0[BN * DP];
     __shared__ __attribute__((aligned(16))) float sK1[BN * DP];
