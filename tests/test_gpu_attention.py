@@ -219,16 +219,18 @@ FAST_SHAPES = [(1, 1, 4, 1, 128), (2, 33, 4, 2, 64), (1, 100, 8, 2, 128), (1, 25
                (2, 130, 3, 3, 128), (1, 200, 4, 1, 64), (1, 511, 2, 2, 128)]
 
 
-def _fast_inputs(shape, seed=500):
+def _fast_inputs(shape, seed=500, mode="bf16"):
     import torch
     B, S, Hq, Hk, Dh = shape
+    rnd = O.round_bf16 if mode == "bf16" else (lambda x: x)
+    tdt = torch.bfloat16 if mode == "bf16" else torch.float32
     host = []
     for b in range(B):
         sd = seed + 16 * b
-        host.append(tuple(O.round_bf16(O.rand(S * h * Dh, sd + i, 1.0)) for i, h in enumerate((Hq, Hk, Hk, Hq))))
+        host.append(tuple(rnd(O.rand(S * h * Dh, sd + i, 1.0)) for i, h in enumerate((Hq, Hk, Hk, Hq))))
 
     def dev(i, heads):
-        return torch.from_numpy(np.stack([h[i] for h in host])).view(B, S, heads, Dh).to("cuda").to(torch.bfloat16)
+        return torch.from_numpy(np.stack([h[i] for h in host])).view(B, S, heads, Dh).to("cuda").to(tdt)
 
     return host, (dev(0, Hq), dev(1, Hk), dev(2, Hk), dev(3, Hq))
 
@@ -273,6 +275,50 @@ def test_bf16_fast_path_shapes(cf, shape, ds):
                            ("dv", dv[b], rv)):
             e = rel_err(a.reshape(-1), r)
             assert e <= BF16_TOL, f"{shape} seq {b} {name}: {e}"
+
+
+@pytest.mark.parametrize("scratch", ["slots", "generic"])
+@pytest.mark.parametrize("shape", FAST_SHAPES + [(3, 64, 9, 3, 64), (1, 96, 16, 2, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_f32_fast_path_shapes(cf, shape, scratch):
+    """The fp32 fast path (head_dim 64/128) over ragged lengths, GQA, MHA and
+    MQA, batches, every query-split count; with the dK/dV scratch slots, and
+    with the scratch capped to zero (the generic fp32 backward)."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    B, S, Hq, Hk, Dh = shape
+    print(f"f32 fast-path shape {shape}, backward with {scratch}", flush=True)
+    host, (q, k, v, g) = _fast_inputs(shape, seed=700, mode="f32")
+    with _DsLimit(ctx, ctx.ds_limit if scratch == "slots" else 0):
+        o, lse = D.fwd(q, k, v, ctx=ctx)
+        dq, dk, dv = D.bwd(g, q, k, v, o, lse, ctx=ctx)
+        torch.cuda.synchronize()
+    o, lse, dq, dk, dv = (x.cpu().numpy() for x in (o, lse, dq, dk, dv))
+    for b in range(B):
+        hq, hk, hv, hg = host[b]
+        ro = np.zeros(S * Hq * Dh, np.float32)
+        rl = np.zeros(Hq * S, np.float32)
+        O.attention_forward_blocked(hq, hk, hv, ro, rl, S, Hq, Hk, Dh, 128)
+        rq, rk, rv = np.zeros_like(ro), np.zeros(S * Hk * Dh, np.float32), np.zeros(S * Hk * Dh, np.float32)
+        O.attention_backward_blocked(hg, hq, hk, hv, ro, rl, rq, rk, rv, S, Hq, Hk, Dh, 128)
+        for name, a, r in (("o", o[b], ro), ("lse", lse[b], rl), ("dq", dq[b], rq), ("dk", dk[b], rk),
+                           ("dv", dv[b], rv)):
+            e = max_abs(a.reshape(-1), r)
+            assert e <= F32_TOL, f"{shape} seq {b} {name}: {e}"
+
+
+def test_f32_fast_path_is_bitwise_repeatable(cf):
+    """Fixed-order slot sums: the same fp32 backward twice gives the same bits."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    _, (q, k, v, g) = _fast_inputs((2, 300, 9, 3, 64), seed=800, mode="f32")
+    o, lse = D.fwd(q, k, v, ctx=ctx)
+    runs = [[x.cpu().numpy() for x in D.bwd(g, q, k, v, o, lse, ctx=ctx)] for _ in range(2)]
+    torch.cuda.synchronize()
+    for a, b in zip(*runs):
+        assert np.array_equal(a, b)
 
 
 @pytest.mark.parametrize("shape", [(1, 300, 8, 2, 128), (2, 97, 4, 4, 64), (1, 1000, 4, 1, 128)],
