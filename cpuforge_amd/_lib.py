@@ -1,5 +1,5 @@
 """Loads libcfattn.so (built in-tree by cpuforge_amd/build.py) and declares
-the C ABI of include/cfattn.h and include/cfops.h for ctypes.
+the C ABI of include/cfattn.h, include/cfops.h and include/cfio.h for ctypes.
 
 There is no fallback: if the library is missing the import of any compute
 function raises, so nothing can silently run on the CPU instead of the GPU.
@@ -13,10 +13,10 @@ import threading
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcfattn.so")
 
-OK, ERR_SHAPE, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_NOMEM = range(6)
+OK, ERR_SHAPE, ERR_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_NOMEM, ERR_IO = range(7)
 F32, BF16 = 0, 1
 
-# Every function include/cfattn.h and include/cfops.h declare, with
+# Every function include/cfattn.h, include/cfops.h and include/cfio.h declare, with
 # (restype, argtypes).
 _sz = C.c_size_t
 _vp = C.c_void_p
@@ -80,7 +80,28 @@ SIGNATURES = {
     "cfops_linear_forward": (C.c_int, [_vp] * 5 + [C.c_float] + [_sz] * 4 + [_vp] * 3),
     "cfops_linear_backward": (C.c_int, [_vp] * 7 + [C.c_float] + [_sz] * 4 + [_vp] * 5),
     "cfops_adamw_update": (C.c_int, [_vp] * 5 + [_sz, C.c_uint64] + [C.c_float] * 5 + [_vp]),
+    # include/cfio.h
+    "cfio_bf16_to_f32": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    "cfio_f16_to_f32": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    "cfio_st_open": (C.c_int, [C.c_char_p, C.POINTER(_vp), C.c_char_p, _sz]),
+    "cfio_st_close": (C.c_int, [_vp]),
+    "cfio_st_count": (_sz, [_vp]),
+    "cfio_st_tensor": (C.c_int, [_vp, _sz, C.POINTER(C.c_char_p), C.POINTER(C.c_int), C.POINTER(_sz),
+                                 C.POINTER(C.POINTER(_sz)), C.POINTER(_sz)]),
+    "cfio_st_find": (C.c_longlong, [_vp, C.c_char_p]),
+    "cfio_st_meta_count": (_sz, [_vp]),
+    "cfio_st_meta": (C.c_int, [_vp, _sz, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p)]),
+    "cfio_dtype_name": (C.c_char_p, [C.c_int]),
+    "cfio_st_read_f32": (C.c_int, [_vp, _vp, _sz, C.POINTER(_sz), C.POINTER(_vp), _vp]),
+    "cfio_st_write": (C.c_int, [_vp, C.c_char_p, _sz, C.POINTER(C.c_char_p), C.POINTER(_sz),
+                                C.POINTER(C.POINTER(_sz)), C.POINTER(_vp), _sz, C.POINTER(C.c_char_p),
+                                C.POINTER(C.c_char_p), _vp]),
+    "cfio_set_chunk_bytes": (C.c_int, [_vp, _sz]),
 }
+
+# dtype codes of include/cfio.h (the safetensors crate's Dtype order)
+CFIO_DTYPES = ["BOOL", "F4", "F6_E2M3", "F6_E3M2", "U8", "I8", "F8_E5M2", "F8_E4M3", "F8_E8M0", "I16", "U16", "F16",
+               "BF16", "I32", "U32", "F32", "C64", "F64", "I64", "U64"]
 
 # matmul kinds of cfops_matmul (include/cfops.h)
 NN, NT, TN = 0, 1, 2

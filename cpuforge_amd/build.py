@@ -19,8 +19,8 @@ INCLUDE = os.path.join(ROOT, "include")
 OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcfattn.so")
 
-HIP_SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "attn_f32.hip", "prologue.hip", "layer_ops.hip", "cfattn_capi.cpp",
-               "cfops_capi.cpp"]
+HIP_SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "attn_f32.hip", "prologue.hip", "layer_ops.hip", "io_kernels.hip",
+               "cfattn_capi.cpp", "cfops_capi.cpp", "cfio_capi.cpp"]
 ARCH = "gfx950"
 COMMON = ["-std=c++17", "-fPIC", "-O3", f"--offload-arch={ARCH}", f"-I{INCLUDE}", f"-I{CSRC}",
           "-Wall", "-Wno-unused-result",
@@ -65,7 +65,8 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError("hipcc failed:\n" + "\n".join(failed))
     tmp = LIB + ".tmp"
     # hipBLASLt runs the plain f32 GEMMs of the layer ops (matmul_*, Linear).
-    cmd = [cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp, "-L/opt/rocm/lib", "-lhipblaslt"]
+    cmd = [cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp, "-L/opt/rocm/lib", "-lhipblaslt",
+           "-pthread"]
     out = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if out.returncode != 0:
         raise RuntimeError("link failed:\n" + _filter(out.stdout))

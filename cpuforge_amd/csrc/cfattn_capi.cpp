@@ -252,6 +252,7 @@ int cfattn_destroy(cfattn_ctx* c) {
         }
         delete c->timer;
         c->timer = nullptr;
+        if (c->io && c->io_release) c->io_release(c->io);  // waits for its staging copies
         for (int i = 0; i < cfattn_ctx::NSLOT; i++)
             if (c->buf[i]) (void)hipFree(c->buf[i]);
         if (c->blas && c->blas_release) c->blas_release(c->blas);

@@ -1,6 +1,7 @@
 // Internal to libcfattn.so: the context behind the opaque cfattn_ctx handle
 // of include/cfattn.h and the host helpers its C ABI files share
-// (cfattn_capi.cpp for the attention, cfops_capi.cpp for the layer ops).
+// (cfattn_capi.cpp for the attention, cfops_capi.cpp for the layer ops,
+// cfio_capi.cpp for the on-disk formats).
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -102,6 +103,8 @@ struct cfattn_ctx {
         Q, K, V, O, LSE, DO_, DQ, DK, DV, QB, KB, VB, DOB, DELTA, PARTIAL, DQROT, DKROT, DS,
         // layer ops (cfops_capi.cpp)
         OPS_PARTIAL, OPS_ROWLOSS, OPS_MISC, OPS_LOGITS, OPS_DXA, OPS_WS,
+        // on-disk formats (cfio_capi.cpp): the two device staging chunks
+        IO_STAGE,
         NSLOT
     };
     void* buf[NSLOT] = {};
@@ -114,6 +117,11 @@ struct cfattn_ctx {
     void* blas = nullptr;
     void (*blas_release)(void*) = nullptr;
     size_t head_chunk_bytes = (size_t)512 << 20;  // logits buffer limit of cfops_lm_head_ce
+    // Pinned staging of the on-disk formats (two host chunks and their
+    // events), created on first use; released by cfattn_destroy.
+    void* io = nullptr;
+    void (*io_release)(void*) = nullptr;
+    size_t io_chunk = (size_t)32 << 20;
 
     cfattn::Tuning tuning() const {
         cfattn::Tuning t;

@@ -32,6 +32,7 @@ ops instead, for comparison.
 from __future__ import annotations
 
 import time
+from dataclasses import dataclass
 
 import torch
 import torch.nn.functional as F
@@ -39,48 +40,88 @@ import torch.nn.functional as F
 from . import autograd as A
 from .layer import LayerRope, layer_attention
 from .rope import RopeCache
+from .st import FormatError
 
 SMOLLM_135M = dict(vocab=49152, d=576, ffn=1536, heads=9, kv_heads=3, head_dim=64, eps=1e-5, theta=1e4)
 
 
 class LoRALinear:
-    """y = x Wᵀ + (alpha/r) (x Aᵀ) Bᵀ with W frozen (linear.rs:1-3, 56-69)."""
+    """y = x Wᵀ (+ (alpha/r) (x Aᵀ) Bᵀ with an adapter) (linear.rs:1-3, 56-69)."""
 
-    def __init__(self, out: int, inn: int, std: float, rank: int, alpha: float, gen, dtype, device):
+    def __init__(self, out: int, inn: int, std: float, gen, dtype, device):
         self.w = (torch.randn(out, inn, generator=gen, device=device) * std).to(dtype)
+        self.a = self.b = None
+        self.scale = 1.0
+
+    def add_lora(self, rank: int, alpha: float, gen) -> None:
+        """Linear::add_lora (linear.rs:44-52): A uniform in ±1/sqrt(in), B zero,
+        scale alpha / rank."""
+        out, inn = self.w.shape
         bound = 1.0 / inn ** 0.5
-        self.a = ((torch.rand(rank, inn, generator=gen, device=device) * 2 - 1) * bound).to(dtype).requires_grad_()
-        self.b = torch.zeros(out, rank, device=device, dtype=dtype, requires_grad=True)
+        dev, dt = self.w.device, self.w.dtype
+        self.a = ((torch.rand(rank, inn, generator=gen, device=dev) * 2 - 1) * bound).to(dt).requires_grad_()
+        self.b = torch.zeros(out, rank, device=dev, dtype=dt, requires_grad=True)
         self.scale = alpha / rank
 
     def __call__(self, x, backend="torch"):
         if backend == "cfops":
             return A.linear(x, self.w, self.a, self.b, self.scale)
-        return x @ self.w.t() + (self.scale * (x @ self.a.t())) @ self.b.t()
+        y = x @ self.w.t()
+        if self.a is None:
+            return y
+        return y + (self.scale * (x @ self.a.t())) @ self.b.t()
+
+    def named(self, prefix: str):
+        """visit_linear (crates/model/src/model.rs:164-173)."""
+        yield f"{prefix}.weight", self.w
+        if self.a is not None:
+            yield f"{prefix}.lora_A", self.a
+            yield f"{prefix}.lora_B", self.b
 
     def params(self):
-        return [self.a, self.b]
+        return [self.a, self.b] if self.a is not None else []
 
 
 def rmsnorm(x, w, eps):
     return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * w
 
 
+@dataclass
+class LoraConfig:
+    """crates/model/src/model.rs:45-49."""
+    rank: int
+    alpha: float
+    targets: list
+
+
+LORA_TARGETS = ("q", "k", "v", "o", "gate", "up", "down")
+_LINEARS = (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo"), ("gate", "gate"), ("up", "up"), ("down", "down"))
+
+
 class SmolLM:
+    """`rank` > 0 attaches adapters (alpha 2·rank) to every projection, as
+    `cpuforge bench-train` does; `train` is the TrainSpec: "lora" trains the
+    adapters only (LORA_ONLY), "full" every parameter (FULL).  `config`
+    overrides entries of SMOLLM_135M (a smaller model for tests)."""
+
     def __init__(self, layers: int = 30, seq: int = 512, rank: int = 16, dtype=torch.float32, device="cuda",
-                 seed: int = 1, attn_dtype=None, backend: str = "cfops"):
+                 seed: int = 1, attn_dtype=None, backend: str = "cfops", config: dict | None = None,
+                 train: str = "lora"):
         if backend not in ("cfops", "torch"):
             raise ValueError(f"unknown backend {backend!r}")
         if backend == "cfops" and dtype != torch.float32:
             raise ValueError("the cfops backend runs the reference's f32 arithmetic")
-        c = SMOLLM_135M
-        self.c, self.dtype, self.layers_n, self.backend = c, dtype, layers, backend
+        if train not in ("lora", "full"):
+            raise ValueError(f"unknown train spec {train!r}")
+        c = dict(SMOLLM_135M, **(config or {}))
+        self.c, self.dtype, self.layers_n, self.backend, self.train = c, dtype, layers, backend, train
         self.attn_dtype = attn_dtype or dtype
+        self.device = device
         gen = torch.Generator(device=device)
         gen.manual_seed(seed)
         d, f, hd = c["d"], c["ffn"], c["head_dim"]
         qd, kvd = c["heads"] * hd, c["kv_heads"] * hd
-        lin = lambda o, i: LoRALinear(o, i, 0.02, rank, 2.0 * rank, gen, dtype, device)  # noqa: E731
+        lin = lambda o, i: LoRALinear(o, i, 0.02, gen, dtype, device)  # noqa: E731
         self.layers = [dict(attn_norm=torch.ones(d, device=device, dtype=dtype), wq=lin(qd, d), wk=lin(kvd, d),
                             wv=lin(kvd, d), wo=lin(d, qd), mlp_norm=torch.ones(d, device=device, dtype=dtype),
                             gate=lin(f, d), up=lin(f, d), down=lin(d, f)) for _ in range(layers)]
@@ -88,13 +129,48 @@ class SmolLM:
         self.final_norm = torch.ones(d, device=device, dtype=dtype)
         self.rope = LayerRope(RopeCache(hd, seq, c["theta"]), device)
         self.attention = layer_attention  # (q_pre, k_pre, v, LayerRope) -> o
+        self.lora_cfg = None
+        if train == "full":
+            for _, p in self.named_params():
+                p.requires_grad_()
+        if rank:
+            self.add_lora(rank, 2.0 * rank, list(LORA_TARGETS), seed)
+
+    def add_lora(self, rank: int, alpha: float, targets, seed: int) -> None:
+        """Model::add_lora (crates/model/src/model.rs:309-335): adapters on the
+        named projections of every layer, initialised from `seed`."""
+        for t in targets:
+            if t not in LORA_TARGETS:
+                raise FormatError(f"unknown LoRA target '{t}'")
+        if self.lora_cfg is not None:
+            raise FormatError("model already has LoRA adapters")
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(seed)
+        for layer in self.layers:
+            for short, attr in _LINEARS:
+                if short in targets:
+                    layer[attr].add_lora(rank, alpha, gen)
+        self.lora_cfg = LoraConfig(rank, alpha, [str(t) for t in targets])
+
+    def named_params(self):
+        """visit_params order and names (crates/model/src/model.rs:179-208)."""
+        yield "model.embed_tokens.weight", self.embed
+        for i, layer in enumerate(self.layers):
+            p = f"model.layers.{i}"
+            yield f"{p}.input_layernorm.weight", layer["attn_norm"]
+            yield from layer["wq"].named(f"{p}.self_attn.q_proj")
+            yield from layer["wk"].named(f"{p}.self_attn.k_proj")
+            yield from layer["wv"].named(f"{p}.self_attn.v_proj")
+            yield from layer["wo"].named(f"{p}.self_attn.o_proj")
+            yield f"{p}.post_attention_layernorm.weight", layer["mlp_norm"]
+            yield from layer["gate"].named(f"{p}.mlp.gate_proj")
+            yield from layer["up"].named(f"{p}.mlp.up_proj")
+            yield from layer["down"].named(f"{p}.mlp.down_proj")
+        yield "model.norm.weight", self.final_norm
 
     def params(self):
-        out = []
-        for layer in self.layers:
-            for name in ("wq", "wk", "wv", "wo", "gate", "up", "down"):
-                out += layer[name].params()
-        return out
+        """The parameters that train (TrainSpec)."""
+        return [p for _, p in self.named_params() if p.requires_grad]
 
     def loss(self, tokens, targets):
         if self.backend == "cfops":

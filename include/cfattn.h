@@ -78,7 +78,8 @@ enum {
     CFATTN_ERR_ARG = 2,          /* NULL pointer, bad dtype, bad context */
     CFATTN_ERR_UNSUPPORTED = 3,  /* outside the documented limits */
     CFATTN_ERR_HIP = 4,          /* HIP runtime error (message has details) */
-    CFATTN_ERR_NOMEM = 5         /* device allocation failed */
+    CFATTN_ERR_NOMEM = 5,        /* device allocation failed */
+    CFATTN_ERR_IO = 6            /* file I/O failed or the file is malformed (cfio.h) */
 };
 
 /* ---- context ------------------------------------------------------------ */

@@ -59,6 +59,8 @@ void orc_linear_backward(const float* x, const float* xs, const float* dy, const
 uint16_t orc_f32_to_bf16(float f);
 void orc_round_bf16(const float* src, float* dst, size_t n);
 double orc_grad_close_metric(const float* a, const double* n, size_t len, size_t* worst_i);
+void orc_bf16_to_f32(const uint16_t* src, float* dst, size_t n);
+void orc_f16_to_f32(const uint16_t* src, float* dst, size_t n);
 #ifdef __cplusplus
 }
 #endif

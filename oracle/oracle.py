@@ -4,7 +4,7 @@ TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg, as the checker.  The product package
 (cpuforge_amd) never imports this module.
 
-Every function mirrors one in cforge_oracle.c or oracle_layer.c, which cite the reference
+Every function mirrors one in cforge_oracle.c, oracle_layer.c or oracle_io.c, which cite the reference
 file:line it restates.  Arrays are numpy, C-contiguous; the caller owns them,
 as in the reference where callers lend slices.
 """
@@ -24,6 +24,7 @@ _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
 _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
 _sz = C.c_size_t
 
 
@@ -78,6 +79,9 @@ def lib():
         L.orc_round_bf16.argtypes = [_f32p, _f32p, _sz]
         L.orc_grad_close_metric.restype = C.c_double
         L.orc_grad_close_metric.argtypes = [_f32p, _f64p, _sz, C.POINTER(C.c_size_t)]
+        for fn in (L.orc_bf16_to_f32, L.orc_f16_to_f32):
+            fn.restype = None
+            fn.argtypes = [_u16p, _f32p, _sz]
         L.orc_silu_mul_forward.restype = None
         L.orc_silu_mul_forward.argtypes = [_f32p] * 3 + [_sz]
         L.orc_silu_mul_backward.restype = None
@@ -328,3 +332,20 @@ def layer_prologue_backward(dq, dk, q_pre, k_pre, seq, nh, nkv, hd, cos, sin, ma
     rmsnorm_backward(dq, np.ascontiguousarray(q_pre, dtype=np.float32), q_norm, q_rstd, dq_pre, dqw, seq * nh, hd)
     rmsnorm_backward(dk, np.ascontiguousarray(k_pre, dtype=np.float32), k_norm, k_rstd, dk_pre, dkw, seq * nkv, hd)
     return dq_pre, dk_pre, dqw, dkw
+
+
+# ---------------------------------------------------------------- on-disk formats
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """crates/io/src/dtype.rs:3-5 over an array of uint16 patterns."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().orc_bf16_to_f32(bits.ravel(), out.ravel(), bits.size)
+    return out
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """crates/io/src/dtype.rs:7-33 over an array of uint16 patterns."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().orc_f16_to_f32(bits.ravel(), out.ravel(), bits.size)
+    return out

@@ -1,5 +1,5 @@
 """CPU tests of the C ABI (no GPU needed): libcfattn.so loads, exports every
-function include/cfattn.h and include/cfops.h declare, the ctypes table
+function include/cfattn.h, include/cfops.h and include/cfio.h declare, the ctypes table
 covers them, and the host-only helpers agree with the oracle."""
 import ctypes as C
 import os
@@ -12,7 +12,7 @@ from cpuforge_amd import _lib
 from oracle import oracle as O
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("cfattn.h", "cfops.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("cfattn.h", "cfops.h", "cfio.h")]
 
 
 def header_text():
@@ -20,7 +20,7 @@ def header_text():
 
 
 def declared_functions():
-    return sorted(set(re.findall(r"\b(cf(?:attn|ops)_\w+)\s*\(", header_text())))
+    return sorted(set(re.findall(r"\b(cf(?:attn|ops|io)_\w+)\s*\(", header_text())))
 
 
 def test_header_declares_the_reference_interface():
@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
 def declared_arities():
     """Parameter count of every function the headers declare."""
     out = {}
-    for name, params in re.findall(r"\b(cf(?:attn|ops)_\w+)\s*\(([^)]*)\)\s*;", header_text()):
+    for name, params in re.findall(r"\b(cf(?:attn|ops|io)_\w+)\s*\(([^)]*)\)\s*;", header_text()):
         params = params.strip()
         out[name] = 0 if params in ("", "void") else params.count(",") + 1
     return out
