@@ -77,6 +77,8 @@ def parse():
     ap.add_argument("--fused", action="store_true",
                     help="time the Layer-level path instead: q/k prologue (RoPE, Qwen3 norm) + attention, forward "
                          "and backward (cfattn_fused_fwd/bwd); prints its own JSON line")
+    ap.add_argument("--io", action="store_true",
+                    help="time the on-disk formats (include/cfio.h) at SmolLM-135M scale instead")
     ap.add_argument("--ops", action="store_true",
                     help="time the layer ops (include/cfops.h) at the SmolLM-135M train shape and the train step "
                          "with and without them; prints its own JSON line")
@@ -345,6 +347,174 @@ def layer_ops(a):
                       "train": train, "ops": out}), flush=True)
 
 
+def _smollm_tensors():
+    """(name, shape) of every SmolLM-135M parameter in visit_params order
+    (crates/model/src/model.rs:179-208; tied embeddings, no LM head)."""
+    from cpuforge_amd.train_bench import SMOLLM_135M as c
+    d, f, hd = c["d"], c["ffn"], c["head_dim"]
+    qd, kvd = c["heads"] * hd, c["kv_heads"] * hd
+    out = [("model.embed_tokens.weight", (c["vocab"], d))]
+    for i in range(30):
+        p = f"model.layers.{i}"
+        out += [(f"{p}.input_layernorm.weight", (d,)), (f"{p}.self_attn.q_proj.weight", (qd, d)),
+                (f"{p}.self_attn.k_proj.weight", (kvd, d)), (f"{p}.self_attn.v_proj.weight", (kvd, d)),
+                (f"{p}.self_attn.o_proj.weight", (d, qd)), (f"{p}.post_attention_layernorm.weight", (d,)),
+                (f"{p}.mlp.gate_proj.weight", (f, d)), (f"{p}.mlp.up_proj.weight", (f, d)),
+                (f"{p}.mlp.down_proj.weight", (d, f))]
+    return out + [("model.norm.weight", (d,))]
+
+
+def io_formats(a):
+    """Times the on-disk formats of include/cfio.h at SmolLM-135M scale:
+    the bf16 -> f32 widening kernel against HBM bandwidth (6 algorithmic
+    bytes per element), loading the model's bf16 checkpoint into f32 HBM
+    tensors (read_safetensors, crates/io/src/st.rs:19-45) and saving / loading
+    a full-training state of it (p, m, v of every parameter, f32;
+    train/src/state.rs) through the pinned staging chunks.  File throughput
+    is quoted against the measured pinned-host <-> HBM copy rate, the ceiling
+    of a page-cache-resident file.  cpu_baseline: the same load and save on
+    host memory with the safetensors crate the reference links (0.8.0, through
+    its Python binding) and the oracle's dtype.rs widening.  Prints its own
+    JSON line."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    from cpuforge_amd import st as S
+    from oracle import oracle as O
+    from safetensors.numpy import load_file as np_load_file
+    from safetensors.numpy import save_file as np_save_file
+    from safetensors.torch import save_file as torch_save_file
+
+    def timed(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return max(e0.elapsed_time(e1), (time.perf_counter() - w0) * 1e3) / n
+
+    def fresh_saves(save, n, tag):
+        """Mean seconds of `n` saves, each to a new path (replacing an existing
+        file adds the filesystem's replace-on-rename writeback to either
+        writer); the files are removed outside the timed region."""
+        total = 0.0
+        for i in range(n):
+            p = os.path.join(tmp, f"{tag}{i}.safetensors")
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            save(p)
+            total += time.perf_counter() - t0
+            os.remove(p)
+        return total / n
+
+    out = {}
+    # 1. the widening kernel, HBM-resident in and out, and torch's own
+    # bf16 -> f32 copy of the same tensor as a practical ceiling
+    n = 1 << 28
+    src = torch.randint(-32768, 32767, (n,), dtype=torch.int16, device="cuda")
+    dst = torch.empty(n, dtype=torch.float32, device="cuda")
+    for kind, fn in (("bf16", S.bf16_to_f32), ("f16", S.f16_to_f32)):
+        ms = timed(lambda: fn(src, dst), 20)
+        gbs = 6.0 * n / (ms * 1e-3) / 1e9
+        out[f"widen_{kind}"] = {"ms": round(ms, 4), "achieved": round(gbs, 1), "unit": "GB/s", "peak": PEAK_HBM_GBS,
+                                "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": 6 * n, "elements": n}
+    ms = timed(lambda: dst.copy_(src.view(torch.bfloat16)), 20)
+    out["torch_copy_bf16_to_f32"] = {"ms": round(ms, 4), "achieved": round(6.0 * n / (ms * 1e-3) / 1e9, 1)}
+    del src, dst
+    # 2. pinned host <-> HBM copy rates (the staging pipeline's ceiling)
+    nb = 256 << 20
+    hbuf = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
+    dbuf = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    h2d = nb / (timed(lambda: dbuf.copy_(hbuf, non_blocking=True), 10) * 1e-3) / 1e9
+    d2h = nb / (timed(lambda: hbuf.copy_(dbuf, non_blocking=True), 10) * 1e-3) / 1e9
+    del hbuf, dbuf
+    out["pinned_copy_gbs"] = {"h2d": round(h2d, 1), "d2h": round(d2h, 1)}
+
+    names = _smollm_tensors()
+    g = torch.Generator().manual_seed(3)
+    tmp = tempfile.mkdtemp(prefix="cfio_bench_")
+    try:
+        # 3. bf16 checkpoint -> f32 HBM tensors
+        ck = os.path.join(tmp, "model.safetensors")
+        host_bf16 = {nm: (torch.randn(shape, generator=g) * 0.02).to(torch.bfloat16) for nm, shape in names}
+        torch_save_file(host_bf16, ck)
+        ck_bytes = os.path.getsize(ck)
+        numel = sum(t.numel() for t in host_bf16.values())
+        del host_bf16
+        load_ms = timed(lambda: S.read_safetensors(ck), 3)
+        out["load_bf16_checkpoint"] = {"ms": round(load_ms, 2), "file_bytes": ck_bytes, "params": numel,
+                                       "file_gbs": round(ck_bytes / (load_ms * 1e-3) / 1e9, 2),
+                                       "frac_of_h2d": round(ck_bytes / (load_ms * 1e-3) / 1e9 / h2d, 3)}
+        # 4. full-training state, f32 p / m / v
+        dev_ts = [(f"{k}.{nm}", list(shape), torch.randn(shape, generator=g).cuda())
+                  for nm, shape in names for k in ("p", "m", "v")]
+        stp = os.path.join(tmp, "state.safetensors")
+        meta = {"step": "100", "consumed": "800", "opt_step": "100"}
+        S.write_safetensors(stp, dev_ts, meta)
+        st_bytes = os.path.getsize(stp)
+        save_s = fresh_saves(lambda p: S.write_safetensors(p, dev_ts, meta), 3, "ours")
+        ld = S.read_safetensors(stp)
+        ok = all(torch.equal(ld.tensors[nm], t) for nm, _, t in dev_ts)
+        del ld
+        read_ms = timed(lambda: S.read_safetensors(stp), 3)
+        out["state_f32"] = {"tensors": len(dev_ts), "file_bytes": st_bytes, "roundtrip_bitwise": ok,
+                            "save_ms": round(save_s * 1e3, 2), "save_gbs": round(st_bytes / save_s / 1e9, 2),
+                            "save_frac_of_d2h": round(st_bytes / save_s / 1e9 / d2h, 3),
+                            "load_ms": round(read_ms, 2), "load_gbs": round(st_bytes / (read_ms * 1e-3) / 1e9, 2),
+                            "load_frac_of_h2d": round(st_bytes / (read_ms * 1e-3) / 1e9 / h2d, 3)}
+        host_state = {nm: t.cpu().numpy() for nm, _, t in dev_ts}
+        del dev_ts
+        torch.cuda.empty_cache()
+        # 5. cpu baseline: the crate on host memory, the oracle's widening
+        cpu = {}
+        if not a.no_cpu:
+            from safetensors import safe_open
+
+            def crate_load():
+                with safe_open(ck, "pt") as f:
+                    tensors = {k: f.get_tensor(k) for k in f.keys()}
+                return {k: O.bf16_to_f32(v.view(torch.int16).numpy().view(np.uint16)) for k, v in tensors.items()}
+
+            crate_load()
+            t0 = time.perf_counter()
+            for _ in range(3):
+                crate_load()
+            cpu_load_s = (time.perf_counter() - t0) / 3
+            cpu_save_s = fresh_saves(lambda p: np_save_file(host_state, p, metadata=meta), 3, "crate")
+            t0 = time.perf_counter()
+            for _ in range(3):
+                np_load_file(stp)
+            cpu_read_s = (time.perf_counter() - t0) / 3
+            cpu = {"value": round(ck_bytes / cpu_load_s / 1e9, 3), "unit": "GB/s (bf16 checkpoint load)",
+                   "cores": 1, "kind": "port",
+                   "sample": "whole workload, mean of 3: SmolLM-135M bf16 checkpoint read by the safetensors crate "
+                             "0.8.0 (the reference's, via its Python binding) and widened by the oracle's dtype.rs "
+                             "restatement; the f32 state saved (fresh paths) and read on host memory",
+                   "state_save_gbs": round(st_bytes / cpu_save_s / 1e9, 3),
+                   "state_load_gbs": round(st_bytes / cpu_read_s / 1e9, 3)}
+        del host_state
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    w = out["widen_bf16"]
+    traffic = read_traffic(os.path.join(ROOT, "profiles", "hbm_traffic_io_widen.md"), "widen4_kernel<bf16>", "io")
+    print(json.dumps({"metric": "SmolLM-135M bf16 checkpoint load into f32 HBM tensors, GB/s of file",
+                      "value": out["load_bf16_checkpoint"]["file_gbs"], "unit": "GB/s", "n_gpus": 1,
+                      "higher_is_better": True, "vs_baseline": None, "dtype": "bf16->f32",
+                      "data": "synthetic (torch.randn), files in the box's temp dir (page cache)",
+                      "config": {"workload": "SmolLM-135M checkpoint and full-training state (cfio)",
+                                 "params": out["load_bf16_checkpoint"]["params"]},
+                      "roofline": {"bound": "hbm", "kernel": "widen4_kernel<bf16>", "achieved": w["achieved"],
+                                   "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": w["frac"], "traffic": traffic},
+                      "io": out, "cpu_baseline": cpu or None}), flush=True)
+
+
 def main():
     a = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -362,6 +532,9 @@ def main():
         return
     if a.ops:
         layer_ops(a)
+        return
+    if a.io:
+        io_formats(a)
         return
 
     import torch

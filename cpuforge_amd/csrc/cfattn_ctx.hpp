@@ -121,7 +121,7 @@ struct cfattn_ctx {
     // events), created on first use; released by cfattn_destroy.
     void* io = nullptr;
     void (*io_release)(void*) = nullptr;
-    size_t io_chunk = (size_t)32 << 20;
+    size_t io_chunk = (size_t)8 << 20;
 
     cfattn::Tuning tuning() const {
         cfattn::Tuning t;

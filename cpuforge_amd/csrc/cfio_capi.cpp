@@ -15,6 +15,7 @@
 
 #include <algorithm>
 #include <cerrno>
+#include <condition_variable>
 #include <cstring>
 #include <map>
 #include <string>
@@ -540,53 +541,112 @@ bool validate(cfio_file* f, uint64_t data_len, std::string* why) {
     return true;
 }
 
-// pread / pwrite of a whole range; ranges of 8 MiB and more are split over
-// four threads (the page-cache copy of one thread is slower than PCIe).
-bool file_range(bool write, int fd, uint8_t* buf, size_t len, uint64_t off, std::string* why) {
-    auto one = [fd, write](uint8_t* b, size_t n, uint64_t o, int* eno, bool* eof) {
-        while (n) {
-            const ssize_t r = write ? pwrite(fd, b, n, (off_t)o) : pread(fd, b, n, (off_t)o);
-            if (r < 0) {
-                if (errno == EINTR) continue;
-                *eno = errno;
-                return;
-            }
-            if (r == 0) {
-                *eof = true;
-                return;
-            }
-            b += r;
-            n -= (size_t)r;
-            o += (uint64_t)r;
+// pread / pwrite of a whole range on the calling thread.  Returns 0, an
+// errno, or -1 at an early end of file.
+int io_range(bool write, int fd, uint8_t* b, size_t n, uint64_t o) {
+    while (n) {
+        const ssize_t r = write ? pwrite(fd, b, n, (off_t)o) : pread(fd, b, n, (off_t)o);
+        if (r < 0) {
+            if (errno == EINTR) continue;
+            return errno;
         }
-    };
-    constexpr size_t kSplit = (size_t)8 << 20;
-    int nt = len >= kSplit ? 4 : 1;
-    int eno[4] = {0, 0, 0, 0};
-    bool eof[4] = {false, false, false, false};
-    if (nt == 1) {
-        one(buf, len, off, &eno[0], &eof[0]);
-    } else {
-        const size_t part = ((len / nt) + 4095) & ~(size_t)4095;
-        std::vector<std::thread> th;
-        for (int i = 0; i < nt; i++) {
-            const size_t b = std::min(len, part * (size_t)i), e = std::min(len, part * (size_t)(i + 1));
-            if (b < e) th.emplace_back(one, buf + b, e - b, off + b, &eno[i], &eof[i]);
-        }
-        for (auto& t : th) t.join();
+        if (r == 0) return -1;
+        b += r;
+        n -= (size_t)r;
+        o += (uint64_t)r;
     }
-    for (int i = 0; i < nt; i++) {
-        if (eno[i]) {
-            *why = os_error(eno[i]);
-            return false;
-        }
-        if (eof[i]) {
-            *why = write ? "failed to write whole buffer" : "failed to fill whole buffer";
-            return false;
-        }
-    }
-    return true;
+    return 0;
 }
+
+bool file_range(bool write, int fd, uint8_t* buf, size_t len, uint64_t off, std::string* why) {
+    const int r = io_range(write, fd, buf, len, off);
+    if (r == 0) return true;
+    *why = r > 0 ? os_error(r) : (write ? "failed to write whole buffer" : "failed to fill whole buffer");
+    return false;
+}
+
+// Worker threads that read a staging chunk's file ranges in parallel: one
+// thread's page-cache copy runs well below the PCIe rate.  (Writes stay on
+// the calling thread: parallel writes to one file measured no faster.)
+class ReadPool {
+   public:
+    struct Task {
+        uint8_t* buf;
+        size_t len;
+        uint64_t off;
+    };
+    explicit ReadPool(int n) {
+        for (int i = 0; i < n; i++) th_.emplace_back([this] { loop(); });
+    }
+    ~ReadPool() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto& t : th_) t.join();
+    }
+    // Reads every task from fd; returns 0, the first errno, or -1 at an early
+    // end of file.  The caller's thread takes part.
+    int run(int fd, const std::vector<Task>& tasks) {
+        if (tasks.empty()) return 0;
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            fd_ = fd;
+            tasks_ = &tasks;
+            next_ = 0;
+            done_ = 0;
+            err_ = 0;
+            ++gen_;
+        }
+        cv_.notify_all();
+        work();
+        std::unique_lock<std::mutex> lk(mu_);
+        done_cv_.wait(lk, [&] { return done_ == tasks.size(); });
+        tasks_ = nullptr;
+        return err_;
+    }
+
+   private:
+    std::vector<std::thread> th_;
+    std::mutex mu_;
+    std::condition_variable cv_, done_cv_;
+    const std::vector<Task>* tasks_ = nullptr;
+    int fd_ = -1;
+    size_t next_ = 0, done_ = 0;
+    int err_ = 0;
+    unsigned long gen_ = 0;
+    bool stop_ = false;
+
+    void work() {
+        while (true) {
+            Task t;
+            int fd;
+            {
+                std::lock_guard<std::mutex> lk(mu_);
+                if (!tasks_ || next_ >= tasks_->size()) return;
+                t = (*tasks_)[next_++];
+                fd = fd_;
+            }
+            const int r = io_range(false, fd, t.buf, t.len, t.off);
+            std::lock_guard<std::mutex> lk(mu_);
+            if (r && !err_) err_ = r;
+            if (++done_ == tasks_->size()) done_cv_.notify_all();
+        }
+    }
+    void loop() {
+        unsigned long seen = 0;
+        while (true) {
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
+                if (stop_) return;
+                seen = gen_;
+            }
+            work();
+        }
+    }
+};
 
 // Path::with_extension("tmp"): the file name's last extension (a dot not at
 // its start) replaced, or ".tmp" appended.
@@ -601,11 +661,15 @@ std::string tmp_path(const std::string& path) {
 
 // ---- pinned staging --------------------------------------------------------
 
+constexpr int kReadThreads = 8;        // pool workers besides the calling thread
+constexpr size_t kReadTask = (size_t)1 << 20;  // bytes per parallel read
+
 struct IoState {
     size_t chunk = 0;
     uint8_t* host[2] = {nullptr, nullptr};
     hipEvent_t ev[2] = {nullptr, nullptr};
     bool busy[2] = {false, false};
+    ReadPool pool{kReadThreads};
 };
 
 // One staging chunk: the data, then (256-byte aligned) its run table.
@@ -819,7 +883,7 @@ int cfio_st_read_f32(cfattn_ctx* c, const cfio_file* f, size_t count, const size
     if (!dev) return rc;
     const hipStream_t st = to_stream(stream);
     std::vector<IoPiece> pcs;
-    std::string why;
+    std::vector<ReadPool::Task> reads;
     size_t jj = 0;
     uint64_t done = 0;  // bytes of jobs[jj] already staged
     int k = 0;
@@ -828,6 +892,7 @@ int cfio_st_read_f32(cfattn_ctx* c, const cfio_file* f, size_t count, const size
         uint8_t* h = io->host[k];
         uint8_t* d = dev + (size_t)k * sb;
         pcs.clear();
+        reads.clear();
         size_t pos = 0;
         uint32_t blocks = 0;
         while (jj < jobs.size() && pcs.size() < (size_t)cfio::kMaxPieces) {
@@ -836,8 +901,9 @@ int cfio_st_read_f32(cfattn_ctx* c, const cfio_file* f, size_t count, const size
             const size_t room = (io->chunk - pos) & ~(size_t)15;
             if (room == 0) break;
             const uint64_t take = std::min<uint64_t>(total - done, room);
-            if (!file_range(false, f->fd, h + pos, take, f->data_start + J.t->begin + done, &why))
-                return fail(c, CFATTN_ERR_IO, "%s: %s", f->path.c_str(), why.c_str());
+            for (uint64_t b = 0; b < take; b += kReadTask)
+                reads.push_back({h + pos + b, (size_t)std::min<uint64_t>(kReadTask, take - b),
+                                 f->data_start + J.t->begin + done + b});
             IoPiece p{};
             p.dev = reinterpret_cast<uint64_t>(J.dst + done / J.esz * 4);
             p.off = (uint32_t)pos;
@@ -852,6 +918,11 @@ int cfio_st_read_f32(cfattn_ctx* c, const cfio_file* f, size_t count, const size
                 jj++;
                 done = 0;
             }
+        }
+        const int r = io->pool.run(f->fd, reads);
+        if (r) {
+            const std::string m = r > 0 ? os_error(r) : "failed to fill whole buffer";
+            return fail(c, CFATTN_ERR_IO, "%s: %s", f->path.c_str(), m.c_str());
         }
         const size_t toff = (pos + 255) & ~(size_t)255;
         memcpy(h + toff, pcs.data(), pcs.size() * sizeof(IoPiece));

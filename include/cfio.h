@@ -97,8 +97,9 @@ int cfio_st_write(cfattn_ctx* ctx, const char* path, size_t count, const char* c
                   const size_t* const* shapes, const float* const* data, size_t n_meta, const char* const* keys,
                   const char* const* values, void* stream);
 
-/* Size of each of the two pinned staging chunks (default 32 MiB, at least
- * 1 MiB); the device side holds two chunks of the same size. */
+/* Size of each of the two pinned staging chunks (default 8 MiB, at least
+ * 1 MiB); the device side holds two chunks of the same size.  A chunk's file
+ * ranges are read by a pool of eight threads and the caller's. */
 int cfio_set_chunk_bytes(cfattn_ctx* ctx, size_t bytes);
 
 #ifdef __cplusplus
