@@ -626,14 +626,27 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 // block instead of three).  NW waves per workgroup (query heads of one GQA
 // group x query blocks, as in attn_bwd_dq_bf16_kernel) share each K tile.
 // Both the K tile and each wave's dS blocks (2 KiB each, non-temporal: read
-// once) go straight to LDS one tile ahead, double-buffered in distinct
-// arrays (with a third stage the compiler loses track of which direct-to-LDS
-// loads a read depends on and waits for all of them before every read).
+// once) go straight to LDS two tiles ahead, in a three-stage ring.  Two tiles
+// in flight (96 KiB per CU) keep the HBM stream busy; one (48 KiB) left it at
+// two thirds of the bandwidth.  The loads are issued from inline assembly
+// (lds_load16_asm): with the builtin, the compiler's wait-count tracking lost
+// the ring's buffers at the loop head and waited for every load before the
+// first read.  Each step ends with an exact vmcnt wait and a bare barrier.
 // The dS blocks are read transposed: in 16-lane
 // group G, lane 4*kk + a supplies the 8-byte piece of key
 // 16*(u/2) + 4*kk + 2*(u%2) + hh and rows 16*(G%2) + 4*a.. for read u, so
 // lane l ends up with MFMA column l32 (query 32*qi + qperm(l32)) and, for
 // each k-index, the key the K^T operand read uses.
+// Workgroup barrier without the memory fence of __syncthreads: the caller
+// has already waited for exactly the loads and LDS reads the barrier must
+// cover.  The empty asm statements keep the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <int DP, int BN, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams p) {
     constexpr int CPR = DP / 8;
@@ -645,8 +658,13 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
     constexpr int SB = kDsBlock;
     __shared__ __attribute__((aligned(16))) bf16_bits sK0[L::SIZE];
     __shared__ __attribute__((aligned(16))) bf16_bits sK1[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sK2[L::SIZE];
     __shared__ __attribute__((aligned(16))) bf16_bits sS0[NW * NKB * SB];
     __shared__ __attribute__((aligned(16))) bf16_bits sS1[NW * NKB * SB];
+    __shared__ __attribute__((aligned(16))) bf16_bits sS2[NW * NKB * SB];
+    // Direct-to-LDS loads one wave issues per tile (its K blocks and the two
+    // halves of each of its dS blocks).
+    constexpr int kLoadsPerTile = CPW + 2 * NKB;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -699,8 +717,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
 #pragma unroll
             for (int i = 0; i < CPW; i++) {
                 const int blk = wv * CPW + i;
-                __builtin_amdgcn_global_load_lds(kg + base + (long)blk * kvrs + lane_off, Kd + blk * BSTRIDE, 16, 0,
-                                                 0);
+                lds_load16_asm(kg + base + (long)blk * kvrs + lane_off, Kd + blk * BSTRIDE);
             }
         } else {
 #pragma unroll
@@ -708,15 +725,15 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
                 const int blk = wv * CPW + i;
                 const int r = blk + L::NB * (lane / CPR);
                 const long off = (long)min(kt * BN + r, p.seq - 1) * kvrs + (lane % CPR) * 8;
-                __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
+                lds_load16_asm(kg + off, Kd + blk * BSTRIDE);
             }
         }
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
             const bf16_bits* src = dsg + (long)min(kt * NKB + kb, qi) * SB;
             bf16_bits* dst = Sd + (wv * NKB + kb) * SB;
-            __builtin_amdgcn_global_load_lds(src, dst, 16, 0, kCacheNT);
-            __builtin_amdgcn_global_load_lds(src + SB / 2, dst + SB / 2, 16, 0, kCacheNT);
+            lds_load16_nt_asm(src, dst);
+            lds_load16_nt_asm(src + SB / 2, dst + SB / 2);
         }
     };
 
@@ -724,8 +741,10 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
 #pragma unroll
     for (int i = 0; i < NDB; i++) dqt[i] = zero16();
 
+    // Step kt reads buffer kt % 3 and fills buffer (kt + 2) % 3, which the
+    // barrier closing step kt - 1 has freed.
     auto step = [&](int kt, const bf16_bits* Ks, const bf16_bits* Ss, bf16_bits* Kn, bf16_bits* Sn) {
-        if (kt + 1 < n_kt) dma(kt + 1, Kn, Sn);
+        if (kt + 2 < n_kt) dma(kt + 2, Kn, Sn);
         // Key blocks of the tile at or before the wave's query block.
         const int nkb = wave_active ? min(NKB, qi - kt * NKB + 1) : 0;
         if (nkb > 0) {
@@ -754,16 +773,28 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
                     if (kb < nkb) block(kb);
             }
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads for tile kt + 1 have landed
-        __syncthreads();
+        // This wave's loads for tile kt + 1 have landed (loads complete in
+        // issue order; tile kt + 2's may still be in flight) and its LDS
+        // reads of this step are done; then the bare barrier.  (__syncthreads
+        // would add a workgroup fence, whose vmcnt(0) also waits for tile
+        // kt + 2.)
+        if (kt + 2 < n_kt) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kLoadsPerTile) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        ring_barrier();
     };
 
     dma(0, sK0, sS0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    for (int kt = 0; kt < n_kt; kt += 2) {
-        step(kt, sK0, sS0, sK1, sS1);
+    if (n_kt > 1) {
+        dma(1, sK1, sS1);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoadsPerTile) : "memory");
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    ring_barrier();
+    for (int kt = 0; kt < n_kt; kt += 3) {
+        step(kt, sK0, sS0, sK2, sS2);
         if (kt + 1 < n_kt) step(kt + 1, sK1, sS1, sK0, sS0);
+        if (kt + 2 < n_kt) step(kt + 2, sK2, sS2, sK1, sS1);
     }
 
     if (!row_ok) return;

@@ -256,6 +256,28 @@ __device__ __forceinline__ int swz_off(int r, int c) {
     return r * DP + ((c ^ swz<DP>(r)) << 3);
 }
 
+// ------------------------------------------------- direct-to-LDS loads
+// global_load_lds_dwordx4 written as inline assembly: 64 lanes x 16 bytes
+// from per-lane global addresses to 1 KiB of consecutive LDS starting at
+// `lds` (wave-uniform; the instruction takes it in m0, which the compiler
+// loads for the asm operand).  Unlike the builtin, the compiler does not
+// see the LDS write, so it inserts no wait for it: the caller waits with
+// s_waitcnt vmcnt (these loads count there, in issue order) and then
+// barriers.  Used where the compiler's own tracking of several in-flight
+// buffers falls back to waiting for every load.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void lds_load16_asm(const void* g, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+}
+// The same with the non-temporal cache policy, for data read exactly once.
+__device__ __forceinline__ void lds_load16_nt_asm(const void* g, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+    asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(m0) : "memory");
+}
+
 // ------------------------------------------------- blocked bf16 LDS tiles
 // A tile of ROWS rows of DP bf16 (DP = 64 or 128) filled by direct-to-LDS
 // loads: one global_load_lds of 64 lanes x 16 bytes writes 1 KiB at
