@@ -571,10 +571,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                     pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lse2));
                     if (masked && kb0 + qperm((r >> 2) * 8 + hh * 4 + (r & 3)) > tq) pr[r] = 0.0f;
                 }
-                // dS^T without the softmax scale (applied once to dQ).
+                // dS^T without the softmax scale (applied once to dQ), from P
+                // rounded to bf16 as the dK/dV kernel forms it, so both dQ
+                // paths see the same dS.
                 float ds[16];
 #pragma unroll
-                for (int r = 0; r < 16; r++) ds[r] = pr[r] * (dp[r] - dlt);
+                for (int r = 0; r < 16; r++) ds[r] = (float)(__bf16)pr[r] * (dp[r] - dlt);
                 const bf16x8 d0 = cvt_bf16x8(&ds[0]), d1 = cvt_bf16x8(&ds[8]);
                 const bf16_bits* t0 = Ks + trow + kb * 2 * ROW16;
 #pragma unroll
@@ -810,7 +812,8 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
 // workgroup of one KV head; steps run over (query head of the group, query
 // tile of BM rows) in a fixed order, low key tiles (the most queries) first.
 //   P waves (0-3) hold K^T and the dV^T accumulators: S = Q K^T,
-//     P = exp2(S*scale*log2e - lse*log2e) (causally masked), P to LDS in f32,
+//     P = exp2(S*scale*log2e - lse*log2e) (causally masked), P to LDS as the
+//     bf16 operands of its own dV product (half the bytes of f32),
 //     then dV^T += dO^T P.
 //   dS waves (4-7) hold V^T and the dK^T accumulators: dP = dO V^T, then with
 //     P from LDS dS = P (dP - delta) and dK^T += Q^T dS.
@@ -841,8 +844,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __shared__ __attribute__((aligned(16))) bf16_bits sO1[L::SIZE];
     __shared__ __attribute__((aligned(16))) float sL[2][BM];  // lse * log2(e), by MFMA row
     __shared__ __attribute__((aligned(16))) float sD[2][BM];  // delta, by MFMA row
-    // P of each (key slice, query block): lane l's four values of row group g4.
-    __shared__ float4 sP[4][NQB][4][64];
+    // P of each (key slice, query block) as the P waves' bf16 MFMA operands:
+    // lane l's eight values of row groups 2h and 2h + 1 (h = 0, 1).
+    __shared__ uint4 sPb[4][NQB][2][64];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -1001,10 +1005,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                         if (masked && kw > q0 + qb * 32 + qperm(g4 * 8 + hh * 4 + i)) pv = 0.0f;
                         pr[g4 * 4 + i] = pv;
                     }
-                    sP[slice][qb][g4][lane] = make_float4(pr[g4 * 4], pr[g4 * 4 + 1], pr[g4 * 4 + 2], pr[g4 * 4 + 3]);
                 }
                 pbf[qb][0] = cvt_bf16x8(&pr[0]);
                 pbf[qb][1] = cvt_bf16x8(&pr[8]);
+                sPb[slice][qb][0][lane] = __builtin_bit_cast(uint4, pbf[qb][0]);
+                sPb[slice][qb][1][lane] = __builtin_bit_cast(uint4, pbf[qb][1]);
             };
             // Phase 1: S -> P (P waves) and dP (dS waves).
             if (full) {
@@ -1067,8 +1072,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             asm volatile("" ::: "memory");
             // Phase 2: dV^T += dO^T P (P waves), dS -> dK^T += Q^T dS (dS waves).
             // dS waves: P and delta of MFMA rows g4*8 + hh*4 + [0, 4) of block qb.
+            // P is the bf16 value the P wave's dV product used (widening is
+            // exact); dS = P (dP - delta) then rounds once more, to bf16.
             auto pd4 = [&](int qb, int g4, float4& p4, float4& d4) {
-                p4 = sP[slice][qb][g4][lane];
+                const uint2 h = reinterpret_cast<const uint2*>(&sPb[slice][qb][g4 >> 1][lane])[g4 & 1];
+                p4 = make_float4(__uint_as_float(h.x << 16), __uint_as_float(h.x & 0xffff0000u),
+                                 __uint_as_float(h.y << 16), __uint_as_float(h.y & 0xffff0000u));
                 d4 = *reinterpret_cast<const float4*>(&Ds[qb * 32 + g4 * 8 + hh * 4]);
             };
             auto phase2 = [&](int qb, const float4 (&p4s)[4], const float4 (&d4s)[4]) {
