@@ -302,6 +302,16 @@ int cfops_linear_forward(cfattn_ctx* c, const float* x, const float* w, const fl
     // linear.rs:58-69
     CF_TRY(gemm(c, CFOPS_NT, x, w, y, t, in, out, 1.0f, false, st));
     if (!lora_a) return CFATTN_OK;
+    const void* ptrs[] = {x, lora_a, lora_b, xs};
+    if (cfattn::lora_fused_applies(rank, t, in, out, ptrs, 4)) {
+        int rc = CFATTN_OK;
+        float* part = static_cast<float*>(
+            slot(c, cfattn_ctx::OPS_LORA, cfattn::lora_partial_floats(rank, t, in, out) * sizeof(float), &rc));
+        if (!part) return rc;
+        CF_HIP(c, cfattn::launch_lora_fwd(rank, x, lora_a, lora_b, lora_scale, t, in, out, y, xs, part, st),
+               "lora forward launch");
+        return CFATTN_OK;
+    }
     CF_TRY(gemm(c, CFOPS_NT, x, lora_a, xs, t, in, rank, lora_scale, false, st));
     return gemm(c, CFOPS_NT, xs, lora_b, y, t, rank, out, 1.0f, true, st);
 }
@@ -318,8 +328,20 @@ int cfops_linear_backward(cfattn_ctx* c, const float* x, const float* xs, const 
     CF_TRY(gemm(c, CFOPS_NN, dy, w, dx, t, out, in, 1.0f, true, st));
     if (gw) CF_TRY(gemm(c, CFOPS_TN, dy, x, gw, out, t, in, 1.0f, true, st));
     if (!lora_a) return CFATTN_OK;
-    if (gb) CF_TRY(gemm(c, CFOPS_TN, dy, xs, gb, out, t, rank, 1.0f, true, st));
     int rc = CFATTN_OK;
+    const void* ptrs[] = {x, xs, dy, lora_a, lora_b};
+    if (cfattn::lora_fused_applies(rank, t, in, out, ptrs, 5)) {
+        float* dxa = static_cast<float*>(slot(c, cfattn_ctx::OPS_DXA, t * rank * sizeof(float), &rc));
+        if (!dxa) return rc;
+        float* part = static_cast<float*>(
+            slot(c, cfattn_ctx::OPS_LORA, cfattn::lora_partial_floats(rank, t, in, out) * sizeof(float), &rc));
+        if (!part) return rc;
+        CF_HIP(c, cfattn::launch_lora_bwd(rank, x, xs, dy, lora_a, lora_b, lora_scale, t, in, out, dx, ga, gb, dxa,
+                                          part, st),
+               "lora backward launch");
+        return CFATTN_OK;
+    }
+    if (gb) CF_TRY(gemm(c, CFOPS_TN, dy, xs, gb, out, t, rank, 1.0f, true, st));
     float* dxa = static_cast<float*>(slot(c, cfattn_ctx::OPS_DXA, t * rank * sizeof(float), &rc));
     if (!dxa) return rc;
     CF_TRY(gemm(c, CFOPS_NN, dy, lora_b, dxa, t, out, rank, lora_scale, false, st));

@@ -42,7 +42,7 @@ def st():
 def small_chunks():
     st().set_chunk_bytes(1 << 20)
     yield
-    st().set_chunk_bytes(32 << 20)
+    st().set_chunk_bytes(8 << 20)
 
 
 def host(t):
@@ -256,7 +256,7 @@ def run(model, o, data, lr=1e-2):
         loss = model.loss(tokens, targets)
         loss.backward()
         o.update(model, lr)
-        losses.append(float(loss))
+        losses.append(loss.item())
     return losses
 
 

@@ -215,11 +215,22 @@ def test_matmul_k0_zeroes_or_keeps():  # matmul.rs:58-67
     assert torch.all(c == 1)
 
 
-@pytest.mark.parametrize("lora", [False, True])
-def test_linear_matches_oracle(lora):  # SmolLM-135M q projection, LoRA r=16
-    print(f"linear lora={lora}", flush=True)
+LINEAR_CASES = [  # (name, lora, rank, t, frozen adapters): SmolLM-135M q projection shapes
+    ("plain", False, 16, 512, False),
+    ("lora_r16", True, 16, 512, False),  # fused adapter kernels
+    ("lora_r8_ragged", True, 8, 509, False),
+    ("lora_r4", True, 4, 256, False),
+    ("lora_r3_gemm", True, 3, 512, False),  # a rank the fused kernels do not take: the GEMM path
+    ("lora_r16_frozen", True, 16, 300, True),  # no adapter gradients, dx only
+]
+
+
+@pytest.mark.parametrize("case", LINEAR_CASES, ids=[c[0] for c in LINEAR_CASES])
+def test_linear_matches_oracle(case):
+    name, lora, r, t, frozen = case
+    print(f"linear {name}", flush=True)
     P = ops()
-    t, inn, out, r, scale = 512, 576, 576, 16, 2.0
+    inn, out, scale = 576, 576, 2.0
     x, w, a, b, dy = rnd((t, inn), 23), rnd((out, inn), 24, 0.02), rnd((r, inn), 25, 0.04), rnd((out, r), 26, 0.1), \
         rnd((t, out), 27)
     A, B = (a, b) if lora else (None, None)
@@ -234,11 +245,12 @@ def test_linear_matches_oracle(lora):  # SmolLM-135M q projection, LoRA r=16
         assert metric(host(gxs), xs) <= 1e-4
     dx, gw, ga, gb = (rnd(s, 28 + i, 0.1) for i, s in enumerate(((t, inn), (out, inn), (r, inn), (out, r))))
     wdx, wgw, wga, wgb = dx.copy(), gw.copy(), ga.copy(), gb.copy()
+    grads = lora and not frozen
     O.linear_backward(x, xs if lora else None, dy, w, A, B, scale, t, inn, out, r, wdx, wgw,
-                      wga if lora else None, wgb if lora else None)
+                      wga if grads else None, wgb if grads else None)
     g = [dev(dx), dev(gw), dev(ga), dev(gb)]
     P.linear_backward(dev(x), dev(xs) if lora else None, dev(dy), dev(w), t, inn, out, g[0], g[1],
-                      g[2] if lora else None, g[3] if lora else None, gA, gB, scale)
+                      g[2] if grads else None, g[3] if grads else None, gA, gB, scale)
     # f64 gradients of the same f32 inputs (linear.rs:75-90)
     f = lambda z: z.astype(np.float64)  # noqa: E731
     r_dx = f(dx) + f(dy) @ f(w)
@@ -250,12 +262,33 @@ def test_linear_matches_oracle(lora):  # SmolLM-135M q projection, LoRA r=16
         r_gb = f(gb) + f(dy).T @ f(xs)
     got = [host(t_) for t_ in g]
     errs = {"dx": (metric(got[0], r_dx), metric(wdx, r_dx)), "gw": (metric(got[1], r_gw), metric(wgw, r_gw))}
-    if lora:
+    if grads:
         errs["ga"] = (metric(got[2], r_ga), metric(wga, r_ga))
         errs["gb"] = (metric(got[3], r_gb), metric(wgb, r_gb))
+    elif lora:  # frozen adapters: their gradient buffers are untouched
+        assert np.array_equal(got[2], ga) and np.array_equal(got[3], gb)
     print("gpu / oracle metric vs f64:", {k: f"{a_:.2e} / {b_:.2e}" for k, (a_, b_) in errs.items()}, flush=True)
     for k, (e_gpu, e_orc) in errs.items():
         assert e_gpu <= max(1e-4, 2 * e_orc), k
+
+
+def test_lora_linear_is_bitwise_repeatable():
+    """The fused adapter kernels sum in a fixed order: the same inputs give the
+    same bits (the checkpoint-recompute contract of the layer)."""
+    P = ops()
+    t, inn, out, r = 700, 1536, 576, 16
+    x, w, a, b, dy = (dev(rnd(s, 60 + i, sd)) for i, (s, sd) in
+                      enumerate((((t, inn), 1.0), ((out, inn), 0.02), ((r, inn), 0.04), ((out, r), 0.1),
+                                 ((t, out), 1.0))))
+    outs = []
+    for _ in range(2):
+        y, xs = torch.empty(t, out, device=DEV), torch.empty(t, r, device=DEV)
+        P.linear_forward(x, w, t, inn, out, y, a, b, 2.0, xs)
+        dx, ga, gb = torch.zeros(t, inn, device=DEV), torch.zeros(r, inn, device=DEV), torch.zeros(out, r, device=DEV)
+        P.linear_backward(x, xs, dy, w, t, inn, out, dx, None, ga, gb, a, b, 2.0)
+        outs.append([host(z) for z in (y, xs, dx, ga, gb)])
+    for u, v in zip(*outs):
+        assert np.array_equal(u, v)
 
 
 # ---------------------------------------------------------------- AdamW
