@@ -23,6 +23,8 @@
 // group's.  Each workgroup writes its dK/dV contribution to a scratch slot;
 // attn_f32_reduce_kernel adds the slots of a KV head in a fixed order (query
 // head, then query split), so results are reproducible bit for bit.
+#include <algorithm>
+
 #include "attn_params.hpp"
 #include "cfattn_common.hpp"
 #include "cfattn_kernels.hpp"
@@ -70,6 +72,23 @@ __device__ __forceinline__ void f32_tile_dma(const float* __restrict__ g, long r
     }
 }
 
+// Query tile, key split and split count of work unit u of one (sequence, KV
+// head, head subset).  Without a key split (ks == 0) unit u is tile
+// n_ttiles - 1 - u; with one, the units run over the tiles from the last
+// (longest) down and over a tile's ks-key-tile runs in order.
+struct F32Unit {
+    int tile, split, ns;
+};
+__device__ __forceinline__ F32Unit f32_unit(int u, int n_ttiles, int tt, int seq, int ks) {
+    if (ks == 0) return F32Unit{n_ttiles - 1 - u, 0, 1};
+    for (int t = n_ttiles - 1;; t--) {
+        const int n_kt = (min(seq, (t + 1) * tt) + 31) / 32;
+        const int ns = (n_kt + ks - 1) / ks;
+        if (u < ns || t == 0) return F32Unit{t, u, ns};
+        u -= ns;
+    }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ forward
@@ -90,18 +109,21 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
     const int wv = wave_uniform(wave);
 
     const int id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
-    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;  // longest tiles first
-    int rest = id / p.n_ttiles;
+    const int TT = 32 * p.tpw;
+    const F32Unit un = f32_unit(id % p.units, p.n_ttiles, TT, p.seq, p.ksplit);
+    const int tile = un.tile;  // longest tiles first
+    int rest = id / p.units;
     const int sub = rest % p.n_sub;
     rest /= p.n_sub;
     const int g = rest % p.nkv;
     const int b = rest / p.nkv;
     const int head = g * p.group + sub * p.hpw + wave % p.hpw;
-    const int TT = 32 * p.tpw;
     const int t_wave = tile * TT + (wave / p.hpw) * 32;
     const int tq = t_wave + l32;
     const int wg_end = min(p.seq, tile * TT + TT);
-    const int n_kt = (wg_end + BN - 1) / BN;
+    const int kt_all = (wg_end + BN - 1) / BN;
+    const int kt0 = un.ns > 1 ? un.split * p.ksplit : 0;
+    const int n_kt = un.ns > 1 ? min(kt_all, kt0 + p.ksplit) : kt_all;
     const bool wave_active = t_wave < p.seq;
     const int wave_last = min(t_wave + 31, p.seq - 1);
 
@@ -156,8 +178,8 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
                 if (masked && k0 + acc_row(r, hh) > tq) sc[r] = -INFINITY;
                 mx = fmaxf(mx, sc[r]);
             }
-            // Key k0 + 0 is unmasked for every query of the first tile, so m2
-            // is finite from the first tile on.
+            // Key k0 + 0 is unmasked for every query of the first tile the
+            // wave visits (k0 <= t_wave there), so m2 is finite from then on.
             mx = max_halves(mx) * p.sl2;
             const float mnew = mx > m2 + kLazy ? mx : m2;
             if (__any(mnew != m2)) {
@@ -186,10 +208,10 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
         __syncthreads();
     };
 
-    dma(0, sK0, sV0);
+    dma(kt0, sK0, sV0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    for (int kt = 0; kt < n_kt; kt += 2) {
+    for (int kt = kt0; kt < n_kt; kt += 2) {
         step(kt, sK0, sV0, sK1, sV1);
         if (kt + 1 < n_kt) step(kt + 1, sK1, sV1, sK0, sV0);
     }
@@ -197,6 +219,21 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
     if (!wave_active) return;
     const float ltot = sum_halves(lsum);
     if (tq >= p.seq) return;
+    if (un.ns > 1) {
+        // A partial: only waves that saw a key of this split (every query of
+        // such a wave did), unnormalised.
+        if (t_wave < kt0 * BN) return;
+        const long row = (long)un.split * p.part_rows + ((long)b * p.nh + head) * p.seq + tq;
+        float* prow = p.part + row * DP;
+#pragma unroll
+        for (int db = 0; db < NDB; db++)
+#pragma unroll
+            for (int rq = 0; rq < 4; rq++)
+                *reinterpret_cast<float4*>(prow + db * 32 + rq * 8 + hh * 4) =
+                    make_float4(oacc[db][rq * 4], oacc[db][rq * 4 + 1], oacc[db][rq * 4 + 2], oacc[db][rq * 4 + 3]);
+        if (hh == 0) p.part_ml[row] = make_float2(m2, ltot);
+        return;
+    }
     const float inv = 1.0f / ltot;
     float* orow = p.o + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
 #pragma unroll
@@ -230,18 +267,21 @@ attn_bwd_dq_f32_kernel(const BwdParams p) {
     const int wv = wave_uniform(wave);
 
     const int id = xcd_remap(blockIdx.x, p.n_wg_q, p.xcd);
-    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;
-    int rest = id / p.n_ttiles;
+    const int TT = 32 * p.tpw;
+    const F32Unit un = f32_unit(id % p.units_q, p.n_ttiles, TT, p.seq, p.ksplit);
+    const int tile = un.tile;
+    int rest = id / p.units_q;
     const int sub = rest % p.n_sub;
     rest /= p.n_sub;
     const int g = rest % p.nkv;
     const int b = rest / p.nkv;
     const int head = g * p.group + sub * p.hpw + wave % p.hpw;
-    const int TT = 32 * p.tpw;
     const int t_wave = tile * TT + (wave / p.hpw) * 32;
     const int tq = t_wave + l32;
     const int wg_end = min(p.seq, tile * TT + TT);
-    const int n_kt = (wg_end + BN - 1) / BN;
+    const int kt_all = (wg_end + BN - 1) / BN;
+    const int kt0 = un.ns > 1 ? un.split * p.ksplit : 0;
+    const int n_kt = un.ns > 1 ? min(kt_all, kt0 + p.ksplit) : kt_all;
     const bool wave_active = t_wave < p.seq;
     const int wave_last = min(t_wave + 31, p.seq - 1);
 
@@ -309,14 +349,29 @@ attn_bwd_dq_f32_kernel(const BwdParams p) {
         __syncthreads();
     };
 
-    dma(0, sK0, sV0);
+    dma(kt0, sK0, sV0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    for (int kt = 0; kt < n_kt; kt += 2) {
+    for (int kt = kt0; kt < n_kt; kt += 2) {
         step(kt, sK0, sV0, sK1, sV1);
         if (kt + 1 < n_kt) step(kt + 1, sK1, sV1, sK0, sV0);
     }
     if (!wave_active || tq >= p.seq) return;
+    if (un.ns > 1) {
+        // A partial (scaled), written only by waves that saw a key of this
+        // split; attn_f32_dq_merge_kernel adds the splits to dq in order.
+        if (t_wave < kt0 * BN) return;
+        float* prow =
+            p.qpart + ((long)un.split * p.part_rows + ((long)b * p.nh + head) * p.seq + tq) * DP;
+#pragma unroll
+        for (int db = 0; db < NDB; db++)
+#pragma unroll
+            for (int rq = 0; rq < 4; rq++)
+                *reinterpret_cast<float4*>(prow + db * 32 + rq * 8 + hh * 4) =
+                    make_float4(acc[db][rq * 4] * p.scale, acc[db][rq * 4 + 1] * p.scale,
+                                acc[db][rq * 4 + 2] * p.scale, acc[db][rq * 4 + 3] * p.scale);
+        return;
+    }
     float* row = p.dq + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
 #pragma unroll
     for (int db = 0; db < NDB; db++)
@@ -531,6 +586,72 @@ __global__ __launch_bounds__(256) void attn_f32_reduce_kernel(const float* __res
     *dv4 = y;
 }
 
+// ------------------------------------------------------------ key splits
+// Shared by the two merges: the number of splits holding row `tq` (0 when its
+// query tile has a single split and its workgroup wrote the final result).
+// Split s holds the row iff the row's 32-query block qb reaches it
+// (s * ks <= qb), the condition under which the kernels wrote it.
+__device__ __forceinline__ int f32_row_splits(int tq, int seq, int tt, int ks) {
+    const int t = tq / tt;
+    const int n_kt = (min(seq, (t + 1) * tt) + 31) / 32;
+    if (n_kt <= ks) return 0;
+    return (tq >> 5) / ks + 1;
+}
+
+// O and lse of the rows of split query tiles: m = max_s m_s, w_s =
+// 2^(m_s - m), l = sum_s w_s l_s, O = sum_s w_s O_s / l, lse = (m + log2 l) ln 2,
+// splits in order.  DP/4 threads per row, four head dims each.
+template <int DP>
+__global__ __launch_bounds__(256) void attn_f32_fwd_merge_kernel(const FwdParams p) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long row = i / (DP / 4);
+    if (row >= p.part_rows) return;
+    const int c = (int)(i % (DP / 4));
+    const int tq = (int)(row % p.seq);
+    const int ns = f32_row_splits(tq, p.seq, 32 * p.tpw, p.ksplit);
+    if (ns == 0) return;
+    float m = -INFINITY;
+    for (int s = 0; s < ns; s++) m = fmaxf(m, p.part_ml[s * p.part_rows + row].x);
+    float l = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s = 0; s < ns; s++) {
+        const float2 ml = p.part_ml[s * p.part_rows + row];
+        const float w = __builtin_amdgcn_exp2f(ml.x - m);
+        const float4 o = reinterpret_cast<const float4*>(p.part + (s * p.part_rows + row) * DP)[c];
+        l += w * ml.y;
+        acc.x += w * o.x, acc.y += w * o.y, acc.z += w * o.z, acc.w += w * o.w;
+    }
+    const float inv = 1.0f / l;
+    const long bh = row / p.seq;  // sequence * nh + head
+    const long b = bh / p.nh, head = bh % p.nh;
+    float* orow = p.o + b * p.q_bs + (long)tq * p.nh * DP + head * DP;
+    reinterpret_cast<float4*>(orow)[c] = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    if (c == 0) p.lse[row] = (m + __log2f(l)) * kLn2;
+}
+
+// dq += sum over the splits of a row, in split order.
+template <int DP>
+__global__ __launch_bounds__(256) void attn_f32_dq_merge_kernel(const BwdParams p) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long row = i / (DP / 4);
+    if (row >= p.part_rows) return;
+    const int c = (int)(i % (DP / 4));
+    const int tq = (int)(row % p.seq);
+    const int ns = f32_row_splits(tq, p.seq, 32 * p.tpw, p.ksplit);
+    if (ns == 0) return;
+    float4 sum = reinterpret_cast<const float4*>(p.qpart + row * DP)[c];
+    for (int s = 1; s < ns; s++) {
+        const float4 v = reinterpret_cast<const float4*>(p.qpart + (s * p.part_rows + row) * DP)[c];
+        sum.x += v.x, sum.y += v.y, sum.z += v.z, sum.w += v.w;
+    }
+    const long bh = row / p.seq;
+    const long b = bh / p.nh, head = bh % p.nh;
+    float4* dst = reinterpret_cast<float4*>(p.dq + b * p.q_bs + (long)tq * p.nh * DP + head * DP) + c;
+    float4 v = *dst;
+    v.x += sum.x, v.y += sum.y, v.z += sum.z, v.w += sum.w;
+    *dst = v;
+}
+
 // ------------------------------------------------------------- launchers
 static bool f32_fast_ok(int hd) { return hd == 64 || hd == 128; }
 
@@ -544,23 +665,92 @@ static int f32_qsplits(const Dims& d) {
     return qs;
 }
 
+// Grid of the forward and dQ kernels: hpw heads x tpw 32-query blocks per
+// workgroup, and the key split.  A causal grid is as slow as its longest query
+// tile, and at one wave per SIMD the kernels also wait on every load; when
+// the grid gives fewer than two waves per SIMD (kSplitWaves on 256 CUs), the
+// key tiles of a query tile are cut into runs of ks (halved from below the
+// longest tile's count until the grid reaches that, not below 2), and a merge
+// combines the runs.
+struct F32Plan {
+    int hpw, tpw, n_sub, n_ttiles;
+    int ks, units, max_ns;  // ks == 0: no split, units == n_ttiles
+};
+constexpr long kSplitWaves = 2048;
+
+static int f32_units(const Dims& d, int tt, int n_ttiles, int ks) {
+    int u = 0;
+    for (int t = 0; t < n_ttiles; t++) {
+        const int n_kt = (std::min(d.seq, (t + 1) * tt) + 31) / 32;
+        u += (n_kt + ks - 1) / ks;
+    }
+    return u;
+}
+
+static F32Plan f32_plan(const Dims& d, int group) {
+    F32Plan pl{};
+    pl.hpw = f32_hpw(group);
+    pl.tpw = 4 / pl.hpw;
+    pl.n_sub = group / pl.hpw;
+    pl.n_ttiles = (d.seq + 32 * pl.tpw - 1) / (32 * pl.tpw);
+    pl.ks = 0;
+    pl.units = pl.n_ttiles;
+    pl.max_ns = 1;
+    const long per_unit = (long)d.nkv * pl.n_sub * d.batch;
+    const int kt_max = (d.seq + 31) / 32;
+    if (4L * pl.n_ttiles * per_unit >= kSplitWaves || kt_max <= 2) return pl;
+    int ks = 1;
+    while (2 * ks < kt_max) ks *= 2;
+    for (; ks >= 2; ks /= 2) {
+        pl.ks = ks;
+        pl.units = f32_units(d, 32 * pl.tpw, pl.n_ttiles, ks);
+        if (4L * pl.units * per_unit >= kSplitWaves) break;
+    }
+    pl.max_ns = (kt_max + pl.ks - 1) / pl.ks;
+    return pl;
+}
+
+static size_t f32_rows(const Dims& d) { return (size_t)d.batch * d.nh * d.seq; }
+
 size_t attn_f32_scratch_bytes(const Dims& d) {
-    if (!f32_fast_ok(d.hd) || d.batch <= 0 || d.seq <= 0) return 0;
+    if (!f32_fast_ok(d.hd) || d.batch <= 0 || d.seq <= 0 || d.nkv <= 0) return 0;
     const size_t half = (size_t)d.batch * d.seq * d.nkv * d.hd;
     const size_t slots = (size_t)(d.nh / d.nkv) * f32_qsplits(d);
-    return 2 * slots * half * sizeof(float);
+    const size_t dkdv = 2 * slots * half * sizeof(float);
+    // The dQ split reuses the region once the dK/dV sum has read it.
+    const F32Plan pl = f32_plan(d, d.nh / d.nkv);
+    const size_t dq = pl.ks ? (size_t)pl.max_ns * f32_rows(d) * d.hd * sizeof(float) : 0;
+    return std::max(dkdv, dq);
+}
+
+size_t attn_f32_fwd_scratch_bytes(const Dims& d) {
+    if (!f32_fast_ok(d.hd) || d.batch <= 0 || d.seq <= 0 || d.nkv <= 0) return 0;
+    const F32Plan pl = f32_plan(d, d.nh / d.nkv);
+    if (!pl.ks) return 0;
+    return (size_t)pl.max_ns * f32_rows(d) * (d.hd + 2) * sizeof(float);
 }
 
 bool attn_f32_fast_applies(const Dims& d, int vec_ok, int o_vec_ok) {
     return f32_fast_ok(d.hd) && vec_ok && o_vec_ok;
 }
 
-hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, hipStream_t st, KernelTimer* tm) {
-    p.hpw = f32_hpw(p.group);
-    p.tpw = 4 / p.hpw;
-    p.n_sub = p.group / p.hpw;
-    p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
-    const long n_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+// `scratch` (attn_f32_fwd_scratch_bytes(d) bytes) holds the key splits'
+// partial results; without it the grid runs unsplit.
+hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t scratch_bytes, hipStream_t st,
+                               KernelTimer* tm) {
+    F32Plan pl = f32_plan(d, p.group);
+    const size_t need = attn_f32_fwd_scratch_bytes(d);
+    if (pl.ks && (scratch == nullptr || scratch_bytes < need)) pl.ks = 0, pl.units = pl.n_ttiles;
+    p.hpw = pl.hpw;
+    p.tpw = pl.tpw;
+    p.n_sub = pl.n_sub;
+    p.n_ttiles = pl.n_ttiles;
+    p.ksplit = pl.ks;
+    p.units = pl.units;
+    p.part_rows = (long)f32_rows(d);
+    p.part = pl.ks ? static_cast<float*>(scratch) : nullptr;
+    p.part_ml = pl.ks ? reinterpret_cast<float2*>(p.part + (size_t)pl.max_ns * p.part_rows * d.hd) : nullptr;
+    const long n_wg = (long)pl.units * d.nkv * p.n_sub * d.batch;
     if (n_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
     p.n_wg = (int)n_wg;
     TimedLaunch tl(tm, kKernFwd, st);
@@ -568,6 +758,14 @@ hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, hipStream_t st, Kerne
         hipLaunchKernelGGL(attn_fwd_f32_kernel<128>, dim3(p.n_wg), dim3(256), 0, st, p);
     else
         hipLaunchKernelGGL(attn_fwd_f32_kernel<64>, dim3(p.n_wg), dim3(256), 0, st, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !pl.ks) return e;
+    const long threads = p.part_rows * (d.hd / 4);
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    if (d.hd == 128)
+        hipLaunchKernelGGL(attn_f32_fwd_merge_kernel<128>, dim3(grid), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL(attn_f32_fwd_merge_kernel<64>, dim3(grid), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 
@@ -599,11 +797,16 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStr
         e = hipGetLastError();
     }
     if (e != hipSuccess) return e;
-    p.hpw = f32_hpw(p.group);
-    p.tpw = 4 / p.hpw;
-    p.n_sub = p.group / p.hpw;
-    p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
-    const long nq_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+    const F32Plan pl = f32_plan(d, p.group);
+    p.hpw = pl.hpw;
+    p.tpw = pl.tpw;
+    p.n_sub = pl.n_sub;
+    p.n_ttiles = pl.n_ttiles;
+    p.ksplit = pl.ks;
+    p.units_q = pl.units;
+    p.part_rows = (long)f32_rows(d);
+    p.qpart = pl.ks ? static_cast<float*>(scratch) : nullptr;  // read by the sum above, free now
+    const long nq_wg = (long)pl.units * d.nkv * p.n_sub * d.batch;
     if (nq_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
     p.n_wg_q = (int)nq_wg;
     TimedLaunch tl(tm, kKernBwdDq, st);
@@ -611,6 +814,14 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStr
         hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<128>, dim3(p.n_wg_q), dim3(256), 0, st, p);
     else
         hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<64>, dim3(p.n_wg_q), dim3(256), 0, st, p);
+    e = hipGetLastError();
+    if (e != hipSuccess || !pl.ks) return e;
+    const long threads = p.part_rows * (d.hd / 4);
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    if (d.hd == 128)
+        hipLaunchKernelGGL(attn_f32_dq_merge_kernel<128>, dim3(grid), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL(attn_f32_dq_merge_kernel<64>, dim3(grid), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 

@@ -473,8 +473,10 @@ static hipError_t fwd_dp(const Dims& d, FwdParams p, hipStream_t st, int nwaves,
         return fwd_dispatch<T, DP, 32>(d, p, st, nwaves, tm);
 }
 
+size_t attn_fwd_scratch_bytes(Dtype dt, const Dims& d) { return dt == kF32 ? attn_f32_fwd_scratch_bytes(d) : 0; }
+
 hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k, const void* v, float* o,
-                           float* lse, hipStream_t st, const Tuning& tu) {
+                           float* lse, hipStream_t st, const Tuning& tu, void* scratch, size_t scratch_bytes) {
     if (d.batch == 0 || d.seq == 0 || d.nh == 0) return hipSuccess;
     FwdParams p{};
     p.q = q;
@@ -526,7 +528,7 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
     }
     if (dt == kF32 && attn_f32_fast_applies(d, p.vec_ok, p.o_vec_ok) && tu.fwd_heads_per_wg == 0 &&
         tu.fwd_tblocks_per_wg == 0)
-        return launch_attn_fwd_f32(d, p, st, tu.timer);
+        return launch_attn_fwd_f32(d, p, scratch, scratch_bytes, st, tu.timer);
     const int nwaves = p.hpw * p.tpw;
     const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;
     if (dt == kBF16) {

@@ -20,6 +20,15 @@ struct FwdParams {
     float sl2;  // softmax scale * log2(e)
     long q_bs, kv_bs;
     int vec_ok, o_vec_ok, xcd;
+    // Key split of the fp32 kernel (0: none): a query tile's key tiles are
+    // cut into runs of `ksplit`, one workgroup each; `units` workgroups per
+    // (sequence, KV head, head subset).  Split s of a row writes its
+    // unnormalised O to part[s][row][hd] and (max, sum) to
+    // part_ml[s][row], row = (sequence * nh + head) * seq + query.
+    int ksplit, units;
+    long part_rows;  // batch * nh * seq
+    float* part;
+    float2* part_ml;
 };
 
 struct BwdParams {
@@ -46,6 +55,11 @@ struct BwdParams {
     // causal triangle, block qi*(qi+1)/2 + ki, 2 KiB each (kDsBlock).
     uint16_t* ds;
     long ds_ntri;  // blocks per (sequence, head)
+    // Key split of the fp32 dQ kernel, as FwdParams: split s of a row writes
+    // its scaled dQ to qpart[s][row][hd] unless the query tile has one split.
+    int ksplit, units_q;
+    long part_rows;
+    float* qpart;
 };
 
 // fp32 fast path (attn_f32.hip): head_dim 64 or 128, 16-byte aligned rows.
@@ -53,7 +67,10 @@ bool attn_f32_fast_applies(const Dims& d, int vec_ok, int o_vec_ok);
 // Scratch of the fp32 dK/dV path: the per-head (and per query split)
 // contributions before their fixed-order sum.
 size_t attn_f32_scratch_bytes(const Dims& d);
-hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, hipStream_t st, KernelTimer* tm);
+// Scratch of the fp32 forward's key split (0 when the grid needs none).
+size_t attn_f32_fwd_scratch_bytes(const Dims& d);
+hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t scratch_bytes, hipStream_t st,
+                               KernelTimer* tm);
 hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStream_t st, KernelTimer* tm);
 
 }  // namespace cfattn

@@ -44,6 +44,23 @@ void* ds_scratch(cfattn_ctx* c, Dtype dt, const Dims& d, size_t* bytes) {
 
 // AttnShape::check plus the head-dim / size limits of the kernels
 // (core/src/ops/attention.rs:35-38).
+// Scratch for the forward's key split, or null (the grid runs unsplit) when
+// the shape needs none, it is over the context's limit, or allocation fails.
+void* fwd_scratch(cfattn_ctx* c, Dtype dt, const Dims& d, size_t* bytes) {
+    *bytes = cfattn::attn_fwd_scratch_bytes(dt, d);
+    if (*bytes == 0 || *bytes > c->ds_limit) {
+        *bytes = 0;
+        return nullptr;
+    }
+    int rc = CFATTN_OK;
+    void* p = slot(c, cfattn_ctx::FWD_SPLIT, *bytes, &rc);
+    if (!p) {
+        c->err.clear();
+        *bytes = 0;
+    }
+    return p;
+}
+
 int check_shape(cfattn_ctx* c, const cfattn_shape& s) {
     if (!(s.n_kv > 0 && s.n_heads % s.n_kv == 0))
         return fail(c, CFATTN_ERR_SHAPE, "n_heads must be a multiple of n_kv (n_heads=%zu, n_kv=%zu)", s.n_heads,
@@ -131,8 +148,10 @@ int forward_host(cfattn_ctx* c, const float* q, size_t q_len, const float* k, si
     if (!dout) return rc;
     float* dlse = static_cast<float*>(slot(c, cfattn_ctx::LSE, lse_len * 4, &rc));
     if (!dlse) return rc;
+    size_t fs_bytes = 0;
+    void* fs = fwd_scratch(c, bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), &fs_bytes);
     CF_HIP(c, cfattn::launch_attn_fwd(bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), dq, dk, dv, dout, dlse,
-                                      c->stream, c->tuning()),
+                                      c->stream, c->tuning(), fs, fs_bytes),
            "attention forward launch");
     CF_HIP(c, hipMemcpyAsync(o, dout, o_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H o");
     CF_HIP(c, hipMemcpyAsync(lse, dlse, lse_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H lse");
@@ -320,8 +339,10 @@ static int cfattn_fwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dt
         return fail(c, CFATTN_ERR_UNSUPPORTED, "batch*seq*n_heads too large");
     if (!q || !k || !v || !o || !lse) return fail(c, CFATTN_ERR_ARG, "null buffer");
     DeviceGuard dg(c->device);
+    size_t fs_bytes = 0;
+    void* fs = fwd_scratch(c, (Dtype)dtype, dims_of(s, batch), &fs_bytes);
     CF_HIP(c, cfattn::launch_attn_fwd((Dtype)dtype, dims_of(s, batch), q, k, v, o, lse, pick_stream(c, stream),
-                                      c->tuning()),
+                                      c->tuning(), fs, fs_bytes),
            "attention forward launch");
     return CFATTN_OK;
 }
@@ -502,11 +523,13 @@ int cfattn_set_ds_limit(cfattn_ctx* c, size_t bytes) {
     std::lock_guard<std::mutex> lk(c->mu);
     c->err.clear();
     c->ds_limit = bytes;
-    if (c->buf[cfattn_ctx::DS] && c->cap[cfattn_ctx::DS] > bytes) {
-        DeviceGuard dg(c->device);
-        (void)hipFree(c->buf[cfattn_ctx::DS]);
-        c->buf[cfattn_ctx::DS] = nullptr;
-        c->cap[cfattn_ctx::DS] = 0;
+    for (int sl : {(int)cfattn_ctx::DS, (int)cfattn_ctx::FWD_SPLIT}) {
+        if (c->buf[sl] && c->cap[sl] > bytes) {
+            DeviceGuard dg(c->device);
+            (void)hipFree(c->buf[sl]);
+            c->buf[sl] = nullptr;
+            c->cap[sl] = 0;
+        }
     }
     return CFATTN_OK;
 }

@@ -58,8 +58,15 @@ struct TimedLaunch {
     }
 };
 
+// `scratch` is optional: with f32 inputs on small grids the forward splits
+// long query tiles over key ranges and merges the parts, which needs
+// attn_fwd_scratch_bytes(dt, d) bytes (0: no split for this shape).  Without
+// the scratch the grid runs unsplit; both give the same result up to f32
+// rounding.
+size_t attn_fwd_scratch_bytes(Dtype dt, const Dims& d);
 hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k, const void* v, float* o,
-                           float* lse, hipStream_t st, const Tuning& tu);
+                           float* lse, hipStream_t st, const Tuning& tu, void* scratch = nullptr,
+                           size_t scratch_bytes = 0);
 
 // Backward.  `delta` is caller-provided scratch of batch*n_heads*seq floats.
 // dq, dk, dv are accumulated (+=).

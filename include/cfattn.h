@@ -185,8 +185,12 @@ int cfattn_f32_to_bf16(cfattn_ctx* ctx, const float* src, uint16_t* dst, size_t 
  * batch * n_heads * nb*(nb+1)/2 * 2 KiB with nb = ceil(seq/32) (2.2 GB at
  * seq 8192, 32 heads).  With it, dQ is one product over the stored dS instead
  * of a second softmax recompute; results agree to bf16 rounding of dS, which
- * both paths apply.  Larger shapes, or limit 0, use the recompute.  Lowering
- * the limit below the kept scratch frees it.  Default: 8 GiB. */
+ * both paths apply.  Larger shapes, or limit 0, use the recompute.  The same
+ * limit bounds the f32 path's scratch: the backward's per-head dK/dV and
+ * key-split dQ parts (without it the f32 backward takes the generic kernels)
+ * and the forward's key-split parts on small grids (without it the forward
+ * runs unsplit; results agree to f32 rounding).  Lowering the limit below
+ * the kept scratch frees it.  Default: 8 GiB. */
 int cfattn_set_ds_limit(cfattn_ctx* ctx, size_t bytes);
 size_t cfattn_get_ds_limit(const cfattn_ctx* ctx);
 

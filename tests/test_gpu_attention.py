@@ -309,16 +309,55 @@ def test_f32_fast_path_shapes(cf, shape, scratch):
 
 
 def test_f32_fast_path_is_bitwise_repeatable(cf):
-    """Fixed-order slot sums: the same fp32 backward twice gives the same bits."""
+    """Fixed-order slot sums and key-split merges: the same fp32 forward and
+    backward twice give the same bits."""
     import torch
     from cpuforge_amd import device as D
     mod, ctx = cf
     _, (q, k, v, g) = _fast_inputs((2, 300, 9, 3, 64), seed=800, mode="f32")
+    fwds = [[x.cpu().numpy() for x in D.fwd(q, k, v, ctx=ctx)] for _ in range(2)]
+    for a, b in zip(*fwds):
+        assert np.array_equal(a, b)
     o, lse = D.fwd(q, k, v, ctx=ctx)
     runs = [[x.cpu().numpy() for x in D.bwd(g, q, k, v, o, lse, ctx=ctx)] for _ in range(2)]
     torch.cuda.synchronize()
     for a, b in zip(*runs):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("shape", [(8, 512, 9, 3, 64), (1, 2048, 4, 1, 128), (1, 1000, 8, 8, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_f32_key_split_matches_oracle_and_unsplit(cf, shape):
+    """Small grids split long query tiles over key runs (four key tiles at
+    the SmolLM-135M train shape, batch 8 x seq 512, 9/3 heads) and merge the
+    parts in split order.  O, lse and dQ of the split path against the oracle
+    on the first and last sequence, and the forward against the unsplit grid
+    (scratch limit 0) on every sequence."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    B, S, Hq, Hk, Dh = shape
+    print(f"f32 key split {shape}", flush=True)
+    host, (q, k, v, g) = _fast_inputs(shape, seed=900, mode="f32")
+    o, lse = D.fwd(q, k, v, ctx=ctx)
+    dq, dk, dv = D.bwd(g, q, k, v, o, lse, ctx=ctx)
+    with _DsLimit(ctx, 0):
+        o1, lse1 = D.fwd(q, k, v, ctx=ctx)
+    torch.cuda.synchronize()
+    assert max_abs(o.cpu().numpy().reshape(-1), o1.cpu().numpy().reshape(-1)) <= 1e-5
+    assert max_abs(lse.cpu().numpy().reshape(-1), lse1.cpu().numpy().reshape(-1)) <= 1e-5
+    o, lse, dq, dk, dv = (x.cpu().numpy() for x in (o, lse, dq, dk, dv))
+    for b in sorted({0, B - 1}):
+        hq, hk, hv, hg = host[b]
+        ro = np.zeros(S * Hq * Dh, np.float32)
+        rl = np.zeros(Hq * S, np.float32)
+        O.attention_forward_blocked(hq, hk, hv, ro, rl, S, Hq, Hk, Dh, 128)
+        rq, rk, rv = np.zeros_like(ro), np.zeros(S * Hk * Dh, np.float32), np.zeros(S * Hk * Dh, np.float32)
+        O.attention_backward_blocked(hg, hq, hk, hv, ro, rl, rq, rk, rv, S, Hq, Hk, Dh, 128)
+        for name, a, r in (("o", o[b], ro), ("lse", lse[b], rl), ("dq", dq[b], rq), ("dk", dk[b], rk),
+                           ("dv", dv[b], rv)):
+            e = max_abs(a.reshape(-1), r)
+            assert e <= F32_TOL, f"{shape} seq {b} {name}: {e}"
 
 
 @pytest.mark.parametrize("shape", [(1, 300, 8, 2, 128), (2, 97, 4, 4, 64), (1, 1000, 4, 1, 128)],
