@@ -393,13 +393,23 @@ attn_bwd_dq_f32_kernel(const BwdParams p) {
 // the query tiles qt_begin + qs, + QS, ... that can see its keys.  Per step:
 // S = Q K^T, dP = dO V^T, P = exp2(S*scale*log2e - lse*log2e), dS = P (dP -
 // delta), dV^T += dO^T P, dK^T += Q^T dS.  The result goes to scratch slot
-// (h % group) * QS + qs of the KV head, dK already scaled.
+// (h % group) * qs_n + qs of the KV head, dK already scaled.  QS depends on
+// the key tile: low key tiles see more query tiles and get more splits, so
+// every workgroup has at most qt_run steps (f32_kv_splits).
 struct F32DkdvArgs {
     float* part;     // dK slots [slots][batch][seq][nkv][DP], then the dV slots
     long part_half;  // floats per slot
-    int qs_n;        // query splits QS
-    int slots;       // group * QS
+    int qs_n;        // slot stride: the largest QS (key tile 0)
+    int slots;       // group * qs_n
+    int qt_run;      // query tiles per split at most
+    int units;       // workgroups per (sequence, query head)
 };
+
+// Query splits of 128-key tile kvt: its n_qt - 4 kvt query tiles in runs of
+// at most qt_run.
+__device__ __forceinline__ int f32_kv_splits(int kvt, int n_qt, int qt_run) {
+    return (n_qt - 4 * kvt + qt_run - 1) / qt_run;
+}
 
 template <int DP>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams p, const F32DkdvArgs a) {
@@ -416,11 +426,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams 
     const int l32 = lane & 31, hh = lane >> 5;
     const int wv = wave_uniform(wave);
 
+    const int n_qt = (p.seq + BM - 1) / BM;
     const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
-    const int kvt = id % p.n_kvtiles;  // low key tiles see the most queries: first
-    int rest = id / p.n_kvtiles;
-    const int qs = rest % a.qs_n;
-    rest /= a.qs_n;
+    int u = id % a.units, kvt = 0, qs_n = 1;  // low key tiles see the most queries: first
+    for (;; kvt++) {
+        qs_n = f32_kv_splits(kvt, n_qt, a.qt_run);
+        if (u < qs_n || kvt == p.n_kvtiles - 1) break;
+        u -= qs_n;
+    }
+    const int qs = u;
+    int rest = id / a.units;
     const int h = rest % p.nh;
     const int b = rest / p.nh;
     const int g = h / p.group;
@@ -451,10 +466,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams 
 #pragma unroll
     for (int i = 0; i < NDB; i++) dkt[i] = zero16(), dvt[i] = zero16();
 
-    const int n_qt = (p.seq + BM - 1) / BM;
     const int qt_first = wg_key0 / BM + qs;
-    const int n_steps = qt_first < n_qt ? (n_qt - qt_first + a.qs_n - 1) / a.qs_n : 0;
-    auto step_q0 = [&](int s) { return (qt_first + s * a.qs_n) * BM; };
+    const int n_steps = qt_first < n_qt ? (n_qt - qt_first + qs_n - 1) / qs_n : 0;
+    auto step_q0 = [&](int s) { return (qt_first + s * qs_n) * BM; };
 
     float pl = 0.0f;
     auto dma = [&](int s, float* Qd, float* Od) {
@@ -561,22 +575,29 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams 
 }
 
 // dk += sum over slots (query head of the group, then query split) of the
-// dK slots, dv likewise; four floats per thread.  Every workgroup writes its
-// slot for all of its keys (zeros where it saw no query), so every slot row
-// below seq is defined.
-__global__ __launch_bounds__(256) void attn_f32_reduce_kernel(const float* __restrict__ part, long half, int slots,
+// dK slots, dv likewise; four floats per thread.  The workgroups of a key
+// tile's splits write their slots for all of its keys (zeros where they saw
+// no query), so the slots read here are defined; the splits beyond the key
+// tile's count are neither written nor read.
+__global__ __launch_bounds__(256) void attn_f32_reduce_kernel(const float* __restrict__ part, const F32DkdvArgs a,
+                                                              int seq, int row_floats, int group,
                                                               float* __restrict__ dk, float* __restrict__ dv) {
     const long i4 = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long half = a.part_half;
     if (i4 * 4 >= half) return;
+    const int key = (int)((i4 * 4 / row_floats) % seq);
+    const int qs_n = f32_kv_splits(key / 128, (seq + 31) / 32, a.qt_run);
     const float4* pk = reinterpret_cast<const float4*>(part) + i4;
-    const float4* pv = reinterpret_cast<const float4*>(part + (long)slots * half) + i4;
+    const float4* pv = reinterpret_cast<const float4*>(part + (long)a.slots * half) + i4;
     const long stride = half / 4;
     float4 sk = pk[0], sv = pv[0];
-    for (int s = 1; s < slots; s++) {
-        const float4 a = pk[s * stride], c = pv[s * stride];
-        sk.x += a.x, sk.y += a.y, sk.z += a.z, sk.w += a.w;
-        sv.x += c.x, sv.y += c.y, sv.z += c.z, sv.w += c.w;
-    }
+    for (int hg = 0; hg < group; hg++)
+        for (int q = hg == 0 ? 1 : 0; q < qs_n; q++) {
+            const long s = (long)hg * a.qs_n + q;
+            const float4 x = pk[s * stride], c = pv[s * stride];
+            sk.x += x.x, sk.y += x.y, sk.z += x.z, sk.w += x.w;
+            sv.x += c.x, sv.y += c.y, sv.z += c.z, sv.w += c.w;
+        }
     float4* dk4 = reinterpret_cast<float4*>(dk) + i4;
     float4* dv4 = reinterpret_cast<float4*>(dv) + i4;
     float4 x = *dk4, y = *dv4;
@@ -657,12 +678,25 @@ static bool f32_fast_ok(int hd) { return hd == 64 || hd == 128; }
 
 static int f32_hpw(int group) { return group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1; }
 
-// Query splits of the dK/dV grid: enough workgroups for two waves per SIMD.
-static int f32_qsplits(const Dims& d) {
-    const long base = (long)((d.seq + 127) / 128) * d.nh * d.batch;
-    int qs = 1;
-    while (qs < 4 && base * qs * 4 < 2048) qs *= 2;
-    return qs;
+// Query splits of the dK/dV grid: the query tiles a key tile sees are cut
+// into runs of at most qt_run, halved from the longest (key tile 0) until the
+// grid gives two waves per SIMD, with at most 8 splits.
+struct F32KvPlan {
+    int qt_run, qs_max, units;
+};
+static F32KvPlan f32_kv_plan(const Dims& d) {
+    const int n_qt = (d.seq + 31) / 32, n_kvt = (d.seq + 127) / 128;
+    const long per = (long)d.nh * d.batch;
+    F32KvPlan pl{n_qt, 1, n_kvt};
+    for (int run = n_qt; run >= 1; run = (run + 1) / 2) {
+        const int qs_max = (n_qt + run - 1) / run;
+        if (qs_max > 8) break;
+        int units = 0;
+        for (int t = 0; t < n_kvt; t++) units += (n_qt - 4 * t + run - 1) / run;
+        pl = F32KvPlan{run, qs_max, units};
+        if (4L * units * per >= 2048 || run == 1) break;
+    }
+    return pl;
 }
 
 // Grid of the forward and dQ kernels: hpw heads x tpw 32-query blocks per
@@ -715,7 +749,7 @@ static size_t f32_rows(const Dims& d) { return (size_t)d.batch * d.nh * d.seq; }
 size_t attn_f32_scratch_bytes(const Dims& d) {
     if (!f32_fast_ok(d.hd) || d.batch <= 0 || d.seq <= 0 || d.nkv <= 0) return 0;
     const size_t half = (size_t)d.batch * d.seq * d.nkv * d.hd;
-    const size_t slots = (size_t)(d.nh / d.nkv) * f32_qsplits(d);
+    const size_t slots = (size_t)(d.nh / d.nkv) * f32_kv_plan(d).qs_max;
     const size_t dkdv = 2 * slots * half * sizeof(float);
     // The dQ split reuses the region once the dK/dV sum has read it.
     const F32Plan pl = f32_plan(d, d.nh / d.nkv);
@@ -773,13 +807,16 @@ hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t
 // attn_f32_scratch_bytes(d) bytes.
 hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStream_t st, KernelTimer* tm) {
     F32DkdvArgs a;
-    a.qs_n = f32_qsplits(d);
+    const F32KvPlan kp = f32_kv_plan(d);
+    a.qs_n = kp.qs_max;
+    a.qt_run = kp.qt_run;
+    a.units = kp.units;
     a.part = static_cast<float*>(scratch);
     a.part_half = (long)d.batch * d.seq * d.nkv * d.hd;
     const int slots = p.group * a.qs_n;
     a.slots = slots;
     p.n_kvtiles = (d.seq + 127) / 128;
-    const long nkv_wg = (long)p.n_kvtiles * a.qs_n * d.nh * d.batch;
+    const long nkv_wg = (long)kp.units * d.nh * d.batch;
     if (nkv_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
     p.n_wg_kv = (int)nkv_wg;
     hipError_t e;
@@ -792,8 +829,8 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStr
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         const long n4 = a.part_half / 4;
-        hipLaunchKernelGGL(attn_f32_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, a.part,
-                           a.part_half, slots, p.dk, p.dv);
+        hipLaunchKernelGGL(attn_f32_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, a.part, a,
+                           d.seq, d.nkv * d.hd, p.group, p.dk, p.dv);
         e = hipGetLastError();
     }
     if (e != hipSuccess) return e;
