@@ -97,6 +97,55 @@ class LinearFn(torch.autograd.Function):
         return dx.view(*dy.shape[:-1], inn), gw, ga, gb, None
 
 
+class SharedInputLinearsFn(torch.autograd.Function):
+    """Several linears of one input (the q/k/v projections of a layer, or its
+    gate and up projections): each forward as LinearFn, and one backward that
+    accumulates every linear's dx into one zeroed buffer in order, as the
+    reference's Layer::backward does for dn2 (crates/model/src/layer.rs:170-171)
+    and dn1 (layer.rs:208-211).  `flat` holds (w, a, b) per linear."""
+
+    @staticmethod
+    def forward(ctx, x, scales, *flat):
+        inn = flat[0].shape[1]
+        x2 = _flat(x, inn)
+        t = x2.shape[0]
+        ys, xss = [], []
+        for i, scale in enumerate(scales):
+            w, a, b = flat[3 * i:3 * i + 3]
+            y = torch.empty(t, w.shape[0], device=x.device, dtype=torch.float32)
+            xs = torch.empty(t, a.shape[0], device=x.device, dtype=torch.float32) if a is not None else None
+            P.linear_forward(x2, w, t, inn, w.shape[0], y, a, b, scale, xs)
+            ys.append(y.view(*x.shape[:-1], w.shape[0]))
+            xss.append(xs)
+        ctx.save_for_backward(x2, *flat, *[xs if xs is not None else torch.empty(0) for xs in xss])
+        ctx.scales = scales
+        ctx.has_xs = [xs is not None for xs in xss]
+        ctx.shape = x.shape
+        return tuple(ys)
+
+    @staticmethod
+    def backward(ctx, *dys):
+        saved = ctx.saved_tensors
+        n = len(ctx.scales)
+        x2, flat, xss = saved[0], saved[1:1 + 3 * n], saved[1 + 3 * n:]
+        t, inn = x2.shape
+        need = ctx.needs_input_grad[2:]
+        likes = [x2]
+        for i in range(3 * n):
+            likes.append(flat[i] if flat[i] is not None and need[i] else None)
+        bufs = _zeros(*likes)
+        dx, grads = bufs[0], bufs[1:]
+        for i, scale in enumerate(ctx.scales):
+            w, a, b = flat[3 * i:3 * i + 3]
+            if dys[i] is None:
+                continue
+            gw, ga, gb = grads[3 * i:3 * i + 3]
+            xs = xss[i] if ctx.has_xs[i] else None
+            P.linear_backward(x2, xs, _flat(dys[i], w.shape[0]), w, t, inn, w.shape[0], dx, gw, ga, gb, a, b,
+                              scale)
+        return (dx.view(ctx.shape), None, *grads)
+
+
 class LMHeadCEFn(torch.autograd.Function):
     """Mean cross-entropy of logits = hn head^T (model.rs:436-457); the
     forward already forms dhn (and dhead), as cross_entropy_fwd_bwd does."""
@@ -130,6 +179,13 @@ def silu_mul(g, u):
 
 def linear(x, w, a=None, b=None, scale=1.0):
     return LinearFn.apply(x, w, a, b, scale)
+
+
+def shared_input_linears(x, specs):
+    """[(w, a, b, scale), ...] -> the linears' outputs for input x, with one
+    accumulated dx in the backward."""
+    flat = [t for w, a, b, _ in specs for t in (w, a, b)]
+    return SharedInputLinearsFn.apply(x, tuple(float(s) for *_, s in specs), *flat)
 
 
 def lm_head_ce(hn, head, targets):

@@ -71,6 +71,10 @@ class LoRALinear:
             return y
         return y + (self.scale * (x @ self.a.t())) @ self.b.t()
 
+    def spec(self):
+        """(w, a, b, scale) for the shared-input linears."""
+        return self.w, self.a, self.b, self.scale
+
     def named(self, prefix: str):
         """visit_linear (crates/model/src/model.rs:164-173)."""
         yield f"{prefix}.weight", self.w
@@ -200,13 +204,15 @@ class SmolLM:
         x = self.embed[tokens]
         for layer in self.layers:
             n1 = A.rmsnorm(x, layer["attn_norm"], c["eps"])
-            q = layer["wq"](n1, cf).view(B, S, c["heads"], c["head_dim"])
-            k = layer["wk"](n1, cf).view(B, S, c["kv_heads"], c["head_dim"])
-            v = layer["wv"](n1, cf).view(B, S, c["kv_heads"], c["head_dim"])
+            q, k, v = A.shared_input_linears(n1, [layer[n].spec() for n in ("wq", "wk", "wv")])
+            q = q.view(B, S, c["heads"], c["head_dim"])
+            k = k.view(B, S, c["kv_heads"], c["head_dim"])
+            v = v.view(B, S, c["kv_heads"], c["head_dim"])
             o = self.attention(q, k, v.to(self.attn_dtype), self.rope)
             x = x + layer["wo"](o.view(B, S, -1), cf)
             n2 = A.rmsnorm(x, layer["mlp_norm"], c["eps"])
-            x = x + layer["down"](A.silu_mul(layer["gate"](n2, cf), layer["up"](n2, cf)), cf)
+            g, u = A.shared_input_linears(n2, [layer[n].spec() for n in ("gate", "up")])
+            x = x + layer["down"](A.silu_mul(g, u), cf)
         hn = A.rmsnorm(x, self.final_norm, c["eps"])
         return A.lm_head_ce(hn, self.embed, targets)
 
