@@ -92,7 +92,17 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_fwd_kernel(const float* _
     if ((int)threadIdx.x < nr) {
         const float* row = sx + threadIdx.x * ld;
         float ss = 0.0f;
-        for (int i = 0; i < dim; i++) ss = radd(ss, rmul(row[i], row[i]));
+        // Eight LDS reads issued ahead of each eight in-order adds: the sum's
+        // order stays the element order, the reads leave the add chain.
+        int i = 0;
+        for (; i + 8 <= dim; i += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = row[i + j];
+#pragma unroll
+            for (int j = 0; j < 8; j++) ss = radd(ss, rmul(v[j], v[j]));
+        }
+        for (; i < dim; i++) ss = radd(ss, rmul(row[i], row[i]));
         const float ms = rdiv(ss, (float)dim);
         const float inv = rdiv(1.0f, rsqrt_cr(radd(ms, eps)));
         sinv[threadIdx.x] = inv;
@@ -166,7 +176,15 @@ __global__ __launch_bounds__(kRmsThreads) void rmsnorm_bwd_kernel(const float* _
         const float* gr = sdy + threadIdx.x * ld;
         const float inv = sinv[threadIdx.x];
         float dot = 0.0f;
-        for (int i = 0; i < dim; i++) dot = radd(dot, rmul(rmul(rmul(gr[i], sw[i]), xr[i]), inv));
+        int i = 0;
+        for (; i + 8 <= dim; i += 8) {
+            float t[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) t[j] = rmul(rmul(rmul(gr[i + j], sw[i + j]), xr[i + j]), inv);
+#pragma unroll
+            for (int j = 0; j < 8; j++) dot = radd(dot, t[j]);
+        }
+        for (; i < dim; i++) dot = radd(dot, rmul(rmul(rmul(gr[i], sw[i]), xr[i]), inv));
         smean[threadIdx.x] = rdiv(dot, (float)dim);
     }
     __syncthreads();
