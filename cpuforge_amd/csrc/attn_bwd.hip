@@ -24,7 +24,26 @@
 
 namespace cfattn {
 
-// delta[b][h][t] = sum_d dO[b,t,h,d] * O[b,t,h,d]; 16 lanes per row.
+// Eight consecutive values as f32 (16-byte aligned source).
+__device__ __forceinline__ void load8(const bf16_bits* g, float* v) {
+    const uint4 u = *reinterpret_cast<const uint4*>(g);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+__device__ __forceinline__ void load8(const float* g, float* v) {
+    const float4 a = reinterpret_cast<const float4*>(g)[0], b = reinterpret_cast<const float4*>(g)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+
+// delta[b][h][t] = sum_d dO[b,t,h,d] * O[b,t,h,d]; 16 lanes per row.  With
+// head_dim a multiple of 8 and 16-byte aligned rows, lane l sums its runs of
+// eight consecutive head dims (8l .. 8l + 7, then + 128) with 16-byte loads;
+// otherwise every 16th head dim.  The lanes' sums meet in a fixed shuffle
+// tree.
 template <typename T>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams p) {
     const long rows = (long)p.batch * p.seq * p.nh;
@@ -34,7 +53,18 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams p) 
     if (row < rows) {
         const T* g = static_cast<const T*>(p.d_o) + row * p.hd;
         const float* o = p.o + row * p.hd;
-        for (int d = sl; d < p.hd; d += 16) acc += to_f32<T>(g[d]) * o[d];
+        const bool vec = p.hd % 8 == 0 && (((uintptr_t)p.d_o | (uintptr_t)p.o) & 15) == 0;
+        if (vec) {
+            for (int d = sl * 8; d < p.hd; d += 128) {
+                float gv[8], ov[8];
+                load8(g + d, gv);
+                load8(o + d, ov);
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc += gv[i] * ov[i];
+            }
+        } else {
+            for (int d = sl; d < p.hd; d += 16) acc += to_f32<T>(g[d]) * o[d];
+        }
     }
 #pragma unroll
     for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
