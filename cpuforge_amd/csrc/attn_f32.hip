@@ -678,6 +678,10 @@ static bool f32_fast_ok(int hd) { return hd == 64 || hd == 128; }
 
 static int f32_hpw(int group) { return group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1; }
 
+// Waves below which the fp32 grids are split (the kernels run best at two or
+// more waves per SIMD).
+constexpr long kSplitWaves = 2048;
+
 // Query splits of the dK/dV grid: the query tiles a key tile sees are cut
 // into runs of at most qt_run, halved from the longest (key tile 0) until the
 // grid gives two waves per SIMD, with at most 8 splits.
@@ -694,7 +698,7 @@ static F32KvPlan f32_kv_plan(const Dims& d) {
         int units = 0;
         for (int t = 0; t < n_kvt; t++) units += (n_qt - 4 * t + run - 1) / run;
         pl = F32KvPlan{run, qs_max, units};
-        if (4L * units * per >= 2048 || run == 1) break;
+        if (4L * units * per >= kSplitWaves || run == 1) break;
     }
     return pl;
 }
@@ -710,7 +714,6 @@ struct F32Plan {
     int hpw, tpw, n_sub, n_ttiles;
     int ks, units, max_ns;  // ks == 0: no split, units == n_ttiles
 };
-constexpr long kSplitWaves = 2048;
 
 static int f32_units(const Dims& d, int tt, int n_ttiles, int ks) {
     int u = 0;
