@@ -286,7 +286,8 @@ def test_resume_continues_exactly_where_it_stopped(tmp_path):
     assert len(resumed) == 4
     for x, y in zip(straight_losses[4:], resumed):
         assert abs(x - y) < 1e-5, (x, y)
-    worst = max(float((a - b).abs().max()) for (_, a), (_, b) in zip(straight.named_params(), second.named_params()))
+    worst = max(float((a - b).detach().abs().max())
+                for (_, a), (_, b) in zip(straight.named_params(), second.named_params()))
     assert worst < 1e-5, worst
 
 
