@@ -360,7 +360,7 @@ def test_f32_key_split_matches_oracle_and_unsplit(cf, shape):
             assert e <= F32_TOL, f"{shape} seq {b} {name}: {e}"
 
 
-@pytest.mark.parametrize("shape", [(1, 300, 8, 2, 128), (2, 97, 4, 4, 64), (1, 1000, 4, 1, 128)],
+@pytest.mark.parametrize("shape", [(1, 300, 8, 2, 128), (2, 97, 4, 4, 128), (1, 1000, 4, 1, 128)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_stored_ds_matches_recompute(cf, shape):
     """dQ from the dS the dK/dV kernel stores against dQ with the softmax

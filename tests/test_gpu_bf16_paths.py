@@ -1,0 +1,233 @@
+"""GPU parity of the bf16 paths the fast-kernel tests do not reach, and of the
+backward's `+=` contract on the fast kernels.
+
+- The generic bf16 kernels (attn_fwd_kernel, attn_bwd_dkdv_kernel,
+  attn_bwd_dq_kernel on bf16 operands) run whenever head_dim is not 64/128
+  or a row is not 16-byte aligned: the reference's own CASES shapes
+  (crates/core/src/ops/attention.rs:321-322, seeds 10+i / 50+i / 70+i as its
+  tests use them), head dims 32, 96 and 256, and 64/128 through views two
+  bytes off 16-byte alignment.
+- The host-slice entry points in bf16 mode (cfattn_set_mode(CFATTN_BF16)):
+  f32 host slices rounded to bf16 on the device, fp32 accumulation.
+- Accumulation (core/src/ops/mod.rs:1-6): the fast bf16 and fp32 kernels
+  started from nonzero dq/dk/dv give init + the one-pass gradients.
+
+Bars (written in each test): bf16 mode max|a-r|/max|r| <= 2e-2 against the
+oracle's f32 restatement fed the same bf16-rounded inputs; a second identical
+call must give the same bits (the kernels use no atomics).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.cases import CASES, case, rel_err
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2  # bf16 parity bar (max relative)
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+
+    import cpuforge_amd as cf
+    from cpuforge_amd import device as D
+    ctx = cf.Context(0)
+    yield torch, cf, D, ctx
+    ctx.close()
+
+
+def _oracle(hq, hk, hv, hg, S, Hq, Hk, Dh):
+    ro = np.zeros(S * Hq * Dh, np.float32)
+    rl = np.zeros(Hq * S, np.float32)
+    O.attention_forward_blocked(hq, hk, hv, ro, rl, S, Hq, Hk, Dh, 128)
+    rq, rk, rv = np.zeros_like(ro), np.zeros(S * Hk * Dh, np.float32), np.zeros(S * Hk * Dh, np.float32)
+    O.attention_backward_blocked(hg, hq, hk, hv, ro, rl, rq, rk, rv, S, Hq, Hk, Dh, 128)
+    return ro, rl, rq, rk, rv
+
+
+def _to_dev(torch, arrs, shape, dtype, offset_elems=0):
+    """Stack host arrays into a device tensor of `shape`; with offset_elems > 0
+    the tensor is a contiguous view that starts that many elements into its
+    allocation (2 bytes per element off 16-byte alignment for bf16)."""
+    flat = torch.from_numpy(np.stack(arrs).reshape(-1)).to("cuda").to(dtype)
+    if offset_elems == 0:
+        return flat.view(shape)
+    buf = torch.empty(flat.numel() + offset_elems, dtype=dtype, device="cuda")
+    view = buf[offset_elems:]
+    view.copy_(flat)
+    return view.view(shape)
+
+
+def _run_device(env, shape, seeds, offset=0, std=1.0):
+    """bf16 forward + backward of `shape` through the batched device entry
+    points, twice; returns host inputs, both runs' outputs (as numpy) and
+    whether the second run repeated the first bit for bit."""
+    torch, cf, D, ctx = env
+    B, S, Hq, Hk, Dh = shape
+    host = []
+    for b in range(B):
+        # Seeds two apart: the reference Rng starts from seed ^ C | 1, so
+        # seeds 2k and 2k + 1 give the same stream (q would equal k).
+        sd = seeds + 16 * b
+        host.append(tuple(O.round_bf16(O.rand(S * h * Dh, sd + 2 * i, std))
+                          for i, h in enumerate((Hq, Hk, Hk, Hq))))
+    dev = [_to_dev(torch, [h[i] for h in host], (B, S, heads, Dh), torch.bfloat16, offset)
+           for i, heads in enumerate((Hq, Hk, Hk, Hq))]
+    q, k, v, g = dev
+    if offset:
+        assert all(t.data_ptr() % 16 != 0 for t in dev), "views must be off 16-byte alignment"
+    runs = []
+    for _ in range(2):
+        o, lse = D.fwd(q, k, v, ctx=ctx)
+        dq, dk, dv = D.bwd(g, q, k, v, o, lse, ctx=ctx)
+        torch.cuda.synchronize()
+        runs.append([x.cpu().numpy() for x in (o, lse, dq, dk, dv)])
+    same = all(np.array_equal(a, b) for a, b in zip(*runs))
+    return host, runs[0], same
+
+
+def _check(host, out, shape, label):
+    B, S, Hq, Hk, Dh = shape
+    o, lse, dq, dk, dv = out
+    worst = {}
+    for b in range(B):
+        ref = _oracle(*host[b], S, Hq, Hk, Dh)
+        for name, a, r in zip(("o", "lse", "dq", "dk", "dv"), (o[b], lse[b], dq[b], dk[b], dv[b]), ref):
+            worst[name] = max(worst.get(name, 0.0), rel_err(a.reshape(-1), r))
+    print(f"{label}: " + ", ".join(f"{n} {e:.2e}" for n, e in worst.items()), flush=True)
+    for name, e in worst.items():
+        assert e <= BF16_TOL, f"{label} {name}: {e}"
+
+
+@pytest.mark.parametrize("i", range(len(CASES)))
+def test_bf16_generic_reference_cases(env, i):
+    """The reference's CASES (head dims 4/6/8) in bf16 mode through the
+    generic kernels, with the reference tests' seeds (q/k/v from 10+i, dO
+    from 70+i, attention.rs:324-393)."""
+    torch, cf, D, ctx = env
+    seq, h, kv, hd, _ = CASES[i]
+    print(f"bf16 generic CASES[{i}] = {CASES[i]}", flush=True)
+    q, k, v = (O.round_bf16(x) for x in case(seq, h, kv, hd, 10 + i))
+    g = O.round_bf16(O.rand(seq * h * hd, 70 + i, 1.0))
+    host = [(q, k, v, g)]
+    shape = (1, seq, h, kv, hd)
+    dev = [_to_dev(torch, [x], (1, seq, heads, hd), torch.bfloat16) for x, heads in zip((q, k, v, g), (h, kv, kv, h))]
+    runs = []
+    for _ in range(2):
+        o, lse = D.fwd(dev[0], dev[1], dev[2], ctx=ctx)
+        dq, dk, dv = D.bwd(dev[3], dev[0], dev[1], dev[2], o, lse, ctx=ctx)
+        torch.cuda.synchronize()
+        runs.append([x.cpu().numpy() for x in (o, lse, dq, dk, dv)])
+    assert all(np.array_equal(a, b) for a, b in zip(*runs)), "second call differs"
+    _check(host, runs[0], shape, f"CASES[{i}] bf16")
+
+
+# (batch, seq, n_heads, n_kv, head_dim): head dims the fast kernels do not
+# take, ragged last tiles, GQA / MHA / MQA, several sequences.
+GENERIC_SHAPES = [(2, 45, 4, 2, 32), (1, 130, 6, 3, 96), (1, 77, 4, 1, 256), (2, 33, 2, 2, 256)]
+
+
+@pytest.mark.parametrize("shape", GENERIC_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_bf16_generic_head_dims(env, shape):
+    print(f"bf16 generic head dims {shape}", flush=True)
+    host, out, same = _run_device(env, shape, 1200)
+    assert same, "second call differs"
+    _check(host, out, shape, f"generic {shape}")
+
+
+@pytest.mark.parametrize("shape", [(1, 70, 4, 2, 64), (2, 41, 4, 1, 128)], ids=lambda s: "x".join(map(str, s)))
+def test_bf16_unaligned_views(env, shape):
+    """Head dims 64/128 whose rows are 2 bytes off 16-byte alignment: the
+    launchers must take the generic kernels, which read element by element
+    where a 16-byte load would be misaligned."""
+    print(f"bf16 unaligned views {shape}", flush=True)
+    host, out, same = _run_device(env, shape, 1300, offset=1)
+    assert same, "second call differs"
+    _check(host, out, shape, f"unaligned {shape}")
+
+
+# (seq, n_heads, n_kv, head_dim): the reference CASES plus shapes that reach
+# the fast kernels (64/128) through the host slices.
+HOST_SLICE_SHAPES = [c[:4] for c in CASES] + [(200, 9, 3, 64), (97, 4, 2, 128), (64, 2, 2, 32)]
+
+
+@pytest.mark.parametrize("shape", HOST_SLICE_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_host_slice_bf16_mode(env, shape):
+    """attention_forward / attention_backward on f32 host slices with the
+    context in bf16 mode: the device rounds q, k, v, dO to bf16; the oracle
+    gets the same rounded values.  o and lse pass back as f32, and the
+    backward accumulates into the caller's dq/dk/dv."""
+    torch, cf, D, ctx = env
+    seq, h, kv, hd = shape
+    print(f"host-slice bf16 {shape}", flush=True)
+    # An odd base seed: q and k then come from different streams (seeds 2k
+    # and 2k + 1 share one), so the softmax is not one-hot on MHA shapes.
+    q, k, v = case(seq, h, kv, hd, 61)
+    g = O.rand(seq * h * hd, 64, 1.0)
+    s = cf.AttnShape(seq, h, kv, hd)
+    ctx.set_mode("bf16")
+    try:
+        runs = []
+        for _ in range(2):
+            o = np.zeros(seq * h * hd, np.float32)
+            lse = np.zeros(h * seq, np.float32)
+            cf.attention_forward(q, k, v, o, lse, s, ctx)
+            dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+            cf.attention_backward(g, q, k, v, o, lse, dq, dk, dv, s, ctx)
+            runs.append((o, lse, dq, dk, dv))
+    finally:
+        ctx.set_mode("f32")
+    assert all(np.array_equal(a, b) for a, b in zip(*runs)), "second call differs"
+    rq_, rk_, rv_, rg_ = (O.round_bf16(x) for x in (q, k, v, g))
+    ref = _oracle(rq_, rk_, rv_, rg_, seq, h, kv, hd)
+    errs = {n: rel_err(a, r) for n, a, r in zip(("o", "lse", "dq", "dk", "dv"), runs[0], ref)}
+    print("  " + ", ".join(f"{n} {e:.2e}" for n, e in errs.items()), flush=True)
+    for n, e in errs.items():
+        assert e <= BF16_TOL, f"{shape} {n}: {e}"
+
+
+class _DsLimit:
+    def __init__(self, ctx, nbytes):
+        self.ctx, self.nbytes = ctx, nbytes
+
+    def __enter__(self):
+        self.old = self.ctx.ds_limit
+        self.ctx.ds_limit = self.nbytes
+
+    def __exit__(self, *exc):
+        self.ctx.ds_limit = self.old
+
+
+ACC_SHAPES = [(2, 33, 4, 2, 64), (1, 100, 8, 2, 128), (2, 130, 3, 3, 128), (3, 64, 9, 3, 64)]
+
+
+@pytest.mark.parametrize("ds", ["stored", "recompute"])
+@pytest.mark.parametrize("mode", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", ACC_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_fast_backward_accumulates(env, shape, mode, ds):
+    """dq/dk/dv start nonzero: the fast kernels' read-modify-write (bf16 dK/dV
+    and dQ, the fp32 slot sum and key-split merge) must give init + the
+    gradients of a pass from zero (core/src/ops/mod.rs:1-6)."""
+    torch, cf, D, ctx = env
+    B, S, Hq, Hk, Dh = shape
+    print(f"accumulate {shape} {mode} dS {ds}", flush=True)
+    tdt = torch.bfloat16 if mode == "bf16" else torch.float32
+    rnd = O.round_bf16 if mode == "bf16" else (lambda x: x)
+    t = [torch.from_numpy(np.stack([rnd(O.rand(S * h * Dh, 1400 + 16 * b + 2 * i, 1.0)) for b in range(B)]))
+         .view(B, S, h, Dh).to("cuda").to(tdt) for i, h in enumerate((Hq, Hk, Hk, Hq))]
+    q, k, v, g = t
+    init = [torch.from_numpy(O.rand(B * S * h * Dh, 1500 + 2 * i, 0.7)).view(B, S, h, Dh).to("cuda")
+            for i, h in enumerate((Hq, Hk, Hk))]
+    with _DsLimit(ctx, ctx.ds_limit if ds == "stored" else 0):
+        o, lse = D.fwd(q, k, v, ctx=ctx)
+        once = D.bwd(g, q, k, v, o, lse, ctx=ctx)
+        acc = [x.clone() for x in init]
+        D.bwd(g, q, k, v, o, lse, *acc, ctx=ctx)
+        torch.cuda.synchronize()
+    for name, a, i0, g1 in zip(("dq", "dk", "dv"), acc, init, once):
+        a, want = a.cpu().numpy().astype(np.float64), (i0.cpu().numpy().astype(np.float64) +
+                                                     g1.cpu().numpy().astype(np.float64))
+        err = np.abs(a - want).max() / (1.0 + np.abs(want).max())
+        assert err <= 1e-6, f"{shape} {mode} {ds} {name}: {err}"
