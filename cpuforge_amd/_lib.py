@@ -53,6 +53,7 @@ SIGNATURES = {
     "cfattn_attention_backward_blocked": (C.c_int, [_vp] + [_vp, _sz] * 9 + [Shape, _sz]),
     "cfattn_fwd": (C.c_int, [_vp, Shape, _sz, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp]),
     "cfattn_bwd": (C.c_int, [_vp, Shape, _sz, C.c_int] + [_vp] * 10),
+    "cfattn_bwd_noalloc": (C.c_int, [_vp, Shape, _sz, C.c_int] + [_vp] * 10),
     "cfattn_prologue_fwd": (C.c_int, [_vp, Shape, _sz, C.c_int, C.POINTER(PrologueC)] + [_vp] * 7),
     "cfattn_prologue_bwd": (C.c_int, [_vp, Shape, _sz, C.POINTER(PrologueC)] + [_vp] * 11),
     "cfattn_fused_fwd": (C.c_int, [_vp, Shape, _sz, C.c_int, C.POINTER(PrologueC)] + [_vp] * 10),

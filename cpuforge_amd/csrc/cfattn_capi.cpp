@@ -257,6 +257,10 @@ int cfattn_create(int device, cfattn_ctx** out) {
         delete c;
         return CFATTN_ERR_HIP;
     }
+    // The fixed scratch of cfattn_bwd_noalloc on this device (looked up once
+    // per device; a failure here is reported by that entry point, which
+    // retries the lookup).
+    (void)cfattn::noalloc_init_device(device);
     *out = c;
     return CFATTN_OK;
 }
@@ -381,6 +385,40 @@ int cfattn_bwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const voi
     std::lock_guard<std::mutex> lk(c->mu);
     c->err.clear();
     return cfattn_bwd_locked(c, s, batch, dtype, d_o, q, k, v, o, lse, dq, dk, dv, stream);
+}
+
+int cfattn_bwd_noalloc(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const void* d_o, const void* q,
+                       const void* k, const void* v, const float* o, const float* lse, float* dq, float* dk, float* dv,
+                       void* stream) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    CF_TRY(check_dtype(c, dtype));
+    if (batch == 0 || s.seq == 0) return CFATTN_OK;
+    CF_TRY(check_shape(c, s));
+    if (batch * s.seq * s.n_heads >= ((size_t)1 << 31))
+        return fail(c, CFATTN_ERR_UNSUPPORTED, "batch*seq*n_heads too large");
+    if (!d_o || !q || !k || !v || !o || !lse || !dq || !dk || !dv) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    // The only scratch of this path is delta, one float per (sequence,
+    // query head, token).
+    const size_t need = batch * s.n_heads * s.seq * sizeof(float);
+    if (need > cfattn::kNoAllocScratchBytes)
+        return fail(c, CFATTN_ERR_UNSUPPORTED,
+                    "cfattn_bwd_noalloc: batch*n_heads*seq = %zu needs %zu bytes of scratch, above its fixed %zu",
+                    batch * s.n_heads * s.seq, need, cfattn::kNoAllocScratchBytes);
+    DeviceGuard dg(c->device);
+    if (!dg.ok) return fail(c, CFATTN_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+    CF_HIP(c, cfattn::noalloc_init_device(c->device), "scratch symbol lookup");
+    float* delta = static_cast<float*>(cfattn::noalloc_scratch(c->device));
+    if (!delta) return fail(c, CFATTN_ERR_HIP, "no scratch address for device %d", c->device);
+    // No timer (its events are created on demand) and no dS / slot scratch:
+    // the bf16 backward recomputes the softmax for dQ, the fp32 backward
+    // runs the generic kernels.
+    cfattn::Tuning tu;
+    CF_HIP(c, cfattn::launch_attn_bwd((Dtype)dtype, dims_of(s, batch), d_o, q, k, v, o, lse, delta, dq, dk, dv,
+                                      pick_stream(c, stream), tu, nullptr, 0),
+           "attention backward launch");
+    return CFATTN_OK;
 }
 
 static int cfattn_prologue_fwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const cfattn_prologue* pr,

@@ -117,4 +117,14 @@ hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t st);
 // Largest head_dim the kernels take.
 constexpr int kMaxHeadDim = 256;
 
+// Fixed per-device scratch of the entry points that allocate nothing
+// (noalloc.hip).  8 MiB: the backward's delta rows, batch*n_heads*seq
+// floats, up to 2^21 rows.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+// Looks up the scratch array's address on `device`, which must be current;
+// idempotent per device.
+hipError_t noalloc_init_device(int device);
+// The address noalloc_init_device found for `device`, or null before it.
+void* noalloc_scratch(int device);
+
 }  // namespace cfattn

@@ -137,6 +137,19 @@ int cfattn_bwd(cfattn_ctx* ctx, cfattn_shape s, size_t batch, int dtype, const v
                const void* k, const void* v, const float* o, const float* lse, float* dq, float* dk, float* dv,
                void* stream);
 
+/* No reference counterpart.  cfattn_bwd that allocates nothing, for callers
+ * that cannot call hipMalloc (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  The same arguments, results and
+ * accumulation as cfattn_bwd; its only scratch (delta, batch*n_heads*seq
+ * floats) is a fixed 8 MiB device array of the library, one per device, so
+ * batch*n_heads*seq must not exceed 2^21 (CFATTN_ERR_UNSUPPORTED otherwise).
+ * It never stores dS: in bf16, dQ recomputes the softmax (equal to
+ * cfattn_bwd with cfattn_set_ds_limit(ctx, 0)); in f32 it runs the generic
+ * kernels.  Calls that overlap on one device race on the shared array. */
+int cfattn_bwd_noalloc(cfattn_ctx* ctx, cfattn_shape s, size_t batch, int dtype, const void* d_o, const void* q,
+                       const void* k, const void* v, const float* o, const float* lse, float* dq, float* dk,
+                       float* dv, void* stream);
+
 /* ---- fused prologue ------------------------------------------------------ */
 /* Layer::forward's prologue (model/src/layer.rs:104-116): from f32 q_pre
  * [batch, seq, n_heads, D] and k_pre [batch, seq, n_kv, D] writes q_out and
