@@ -19,12 +19,18 @@ INCLUDE = os.path.join(ROOT, "include")
 OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcfattn.so")
 
-HIP_SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "attn_f32.hip", "prologue.hip", "layer_ops.hip", "lora.hip",
+HIP_SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "attn_dkdv.hip", "attn_f32.hip", "prologue.hip", "layer_ops.hip", "lora.hip",
                "io_kernels.hip", "noalloc.hip", "cfattn_capi.cpp", "cfops_capi.cpp", "cfio_capi.cpp"]
 ARCH = "gfx950"
 COMMON = ["-std=c++17", "-fPIC", "-O3", f"--offload-arch={ARCH}", f"-I{INCLUDE}", f"-I{CSRC}",
           "-Wall", "-Wno-unused-result",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Per-file additions.  attn_dkdv.hip: MFMA results in the architectural VGPR
+# form (its score products are read by VALU code; its long-lived
+# accumulators are kept in AGPRs by inline assembly).  Left to choose, the
+# compiler puts every MFMA of that one-wave-per-SIMD kernel in the AGPR form
+# and copies the scores and accumulators between the two files each step.
+EXTRA = {"attn_dkdv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc() -> str:
@@ -49,7 +55,7 @@ def build(verbose: bool = False) -> str:
     for src in HIP_SOURCES:
         obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
-        cmd = [cc, *COMMON, "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [cc, *COMMON, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))

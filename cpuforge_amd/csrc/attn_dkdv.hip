@@ -1,0 +1,757 @@
+// Causal GQA attention backward on gfx950: dK/dV at head_dim 128 (bf16
+// inputs, fp32 accumulation) with one wave per SIMD.
+//
+// Reference semantics (crates/core/src/ops/attention.rs:197-258): with P
+// recomputed from the saved log-sum-exp,
+//   dV_g += P^T dO,   dP = dO V^T,   dS = P * (dP - delta) * scale,
+//   dK_g += dS^T Q,
+// accumulated (+=) into the caller's dk, dv (ops/mod.rs:1-6).
+//
+// A workgroup is four waves, one per SIMD, owning 128 keys of one KV head;
+// each wave holds 64 keys (two 32-key MFMA blocks), so every Q / dO operand
+// it reads from LDS feeds two MFMAs -- half the LDS bytes per product of
+// the two-waves-per-SIMD kernel (attn_bwd_dkdv_ws_kernel), whose register
+// budget leaves room for only 32 keys per wave.
+//   waves 0, 1 (P waves; keys 0-63 / 64-127 of the tile) hold K^T and the
+//     dV^T accumulators: S = Q K^T, P = exp2(S*scale*log2e - lse*log2e)
+//     (causally masked), P to LDS as bf16 MFMA operands, dV^T += dO^T P;
+//   waves 2, 3 (dS waves; the same keys) hold V^T and the dK^T
+//     accumulators: dP = dO V^T, then with P from LDS dS = P (dP - delta)
+//     and dK^T += Q^T dS.
+// Steps (query head, 64-query tile = query blocks 0 and 1) run in
+// attn_bwd_dkdv_ws_kernel's order and every element's products are summed
+// in its order, so dK, dV and the stored dS are bitwise equal to that
+// kernel's.
+//
+// One barrier per step; "interval t" is the time between barriers t - 1 and
+// t.  Each role issues 64 MFMAs per interval in four regions of 16, and the
+// VALU work (softmax, dS) is spread over all four so that it issues in the
+// MFMAs' shadow: one wave hides only about three VALU instructions per
+// 32x32x16 MFMA.  In interval t (a "quarter" is one 32x32 block's 16
+// elements per lane, key block 0 = keys 0-31 of the wave):
+//   P wave:  R1  S of (t, block 1)      | softmax of (t, block 0, key block 1)
+//            R2  dV of (t, block 0)     | softmax of (t, block 1, key block 0)
+//            R3  S of (t+1, block 0)    | softmax of (t, block 1, key block 1)
+//            R4  dV of (t, block 1)     | softmax of (t+1, block 0, key block 0)
+//   dS wave: R1  dP of (t, block 0)     | dS of (t-1, block 0)
+//            R2  dK of (t-1, block 0)   | dS of (t-1, block 1, key block 0)
+//            R3  dP of (t, block 1)     | dS of (t-1, block 1, key block 1), dP - delta of (t, block 0)
+//            R4  dK of (t-1, block 1)   | dP - delta of (t, block 1), the stored dS of t-1
+// P of step t is in LDS at barrier t; the dS wave uses it in interval t + 1.
+// Diagonal and ragged steps (a few per head) take a plain, unpipelined path.
+//
+// Buffers: Q (and lse) of step t are read in intervals t - 1, t and t + 1
+// and loaded in interval t - 2: four buffers.  dO (and delta) of step t are
+// read in interval t and loaded in interval t - 1: two buffers (three for
+// delta).  P of step t is written in interval t and read in t + 1: two
+// buffers.  A load issued in interval t has landed before barrier t (each
+// wave waits for its own loads before the barrier) and overwrites a buffer
+// whose last reader passed barrier t - 1.
+#include "cfattn_common.hpp"
+#include "attn_params.hpp"
+#include "attn_bwd_common.hpp"
+
+#include <type_traits>
+
+namespace cfattn {
+
+namespace {
+
+// No instruction is scheduled across this point.
+#define CF_FENCE() __builtin_amdgcn_sched_barrier(0)
+// A fence with two wait states in it: the operand registers a VALU
+// instruction wrote just before must not be read by an MFMA issued from
+// inline assembly (which the compiler's hazard checks do not see) in the
+// next two cycles.
+#define CF_HAZARD_FENCE()                  \
+    do {                                   \
+        __builtin_amdgcn_sched_barrier(0); \
+        asm volatile("s_nop 1");           \
+        __builtin_amdgcn_sched_barrier(0); \
+    } while (0)
+
+// acc += a * b with acc held in AGPRs for the whole kernel.  Inline assembly
+// because the compiler gives every MFMA of a function one register form,
+// and this kernel needs its score products (read by VALU code) in VGPRs and
+// its long-lived accumulators (read only at the end) in AGPRs.  Back-to-back
+// MFMAs accumulating into the same registers need no wait states; the
+// operands' hazards are covered by CF_HAZARD_FENCE and the final read by
+// acc_drain.
+__device__ __forceinline__ void mfma_acc(f32x16& acc, const bf16x8& a, const bf16x8& b) {
+    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Keeps a value in AGPRs from here on (ties its registers to an empty asm).
+__device__ __forceinline__ void agpr_pin(f32x16& acc) { asm volatile("" : "+a"(acc)); }
+
+}  // namespace
+
+template <bool WDS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_bwd_dkdv_k64_kernel(
+    const BwdParams p) {
+    constexpr int DP = 128, BM = 64;
+    constexpr int CPR = DP / 8;
+    using L = BlkTile<DP, BM>;
+    constexpr int NBL = L::NB;  // 1 KiB load blocks per tile
+    constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16, TSZ = L::SIZE;
+    constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NKB = 2;
+    constexpr int BPW = NBL / 4;                 // blocks of each tile one wave loads
+    constexpr int NQBUF = 4, NOBUF = 2, NDBUF = 3;  // Q, dO and delta buffers
+    static_assert(NBL % 4 == 0 && BM == 64, "tile must split evenly over the four waves");
+    __shared__ __attribute__((aligned(16))) bf16_bits sQ[NQBUF * TSZ];
+    __shared__ __attribute__((aligned(16))) bf16_bits sO[NOBUF * TSZ];  // dO rows
+    __shared__ __attribute__((aligned(16))) float sL[NQBUF][BM];        // lse, by MFMA row
+    __shared__ __attribute__((aligned(16))) float sD[NDBUF][BM];        // delta, by MFMA row
+    // P as the P waves' bf16 MFMA operands: [buffer][pair][qb][kb][half][lane].
+    __shared__ uint4 sP[2][2][2][NKB][2][64];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int pair = wave & 1;
+    const bool pwave = wave < 2;
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
+    const int kvt = id % p.n_kvtiles;  // low key tiles see the most queries: first
+    const int rest = id / p.n_kvtiles;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+    const int wg_key0 = kvt * p.kv_tile;
+    const int key0 = wg_key0 + pair * 64;
+    const bool pair_live = key0 < p.seq;
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const bf16_bits* qg = static_cast<const bf16_bits*>(p.q) + (long)b * p.q_bs;
+    const bf16_bits* og = static_cast<const bf16_bits*>(p.d_o) + (long)b * p.q_bs;
+    const long lrow_base = (long)b * p.nh * p.seq;
+
+    // Row reads: lane (l32, hh) reads MFMA row l32 (tile row qperm(l32)),
+    // chunks hh*NKD + kd.  Transposed reads: in each 16-lane group G, lane
+    // 4k + m supplies head dims 16*(G%2) + 4m + [0, 4) of MFMA row 4*hh + k
+    // (+8, +16, +24), that is tile row 4k + hh (+2, +16, +18).
+    const int rrow = L::row(qperm(l32)) + hh * HALF;
+    const int G = lane >> 4, jj = lane & 15;
+    const int trow = L::row(4 * (jj >> 2) + hh) + 16 * (G & 1) + 4 * (jj & 3);
+    // Stored dS (kDsBlock layout): lane l writes its first eight values to
+    // 16-byte slot l ^ hh and the other eight to slot 64 + (l ^ (2 + hh)).
+    const int ds_off0 = (lane ^ hh) * 8, ds_off1 = (64 + (lane ^ (2 + hh))) * 8;
+
+    const int n_qt = (p.seq + BM - 1) / BM;
+    const int qt_begin = wg_key0 / BM;
+    const int n_steps = p.group * (n_qt - qt_begin);
+    // A step: query tile [q0, q0 + BM) of query head h.  Steps run over the
+    // query tiles qt_begin.. of each head of the group in turn, and each
+    // wave walks them with a cursor (no divisions in the loop).
+    struct Pos {
+        int q0, h;
+    };
+    const Pos first{qt_begin * BM, g * p.group};
+    auto next_pos = [&](Pos x) {
+        x.q0 += BM;
+        if (x.q0 >= n_qt * BM) {
+            x.q0 = qt_begin * BM;
+            x.h++;
+        }
+        return x;
+    };
+    // The wave's keys meet at least one query of the step.
+    auto pos_act = [&](Pos x) { return pair_live && x.q0 + BM - 1 >= key0; };
+    // Every query of the step is past every key of the wave and inside the
+    // sequence: no mask, and every block is on or below the diagonal.
+    auto pos_full = [&](Pos x) { return x.q0 >= key0 + 63 && x.q0 + BM <= p.seq; };
+
+    const int wv = wave_uniform(wave);
+    // Tile loads: wave w loads blocks w*BPW.. of a Q and a dO tile, lane l of
+    // block bk reading chunk l % CPR of tile row bk + NB*(l / CPR); rows past
+    // the end read the last row (finite values, masked below).  Wave 0 also
+    // loads lse and wave 1 delta, one value per MFMA row (MFMA row `lane`:
+    // tile row (lane & 32) + qperm(lane & 31)).  Each load is a scalar base
+    // (the tile) plus a per-lane byte offset, set once per interval.
+    const int lane_row = NBL * (lane / CPR), lane_col = (lane % CPR) * 8;
+    const int lrow = (lane & 32) + qperm(lane & 31);
+    constexpr int kLoadsP = 2 * BPW + 1, kLoadsDs = 2 * BPW;
+    struct Loads {
+        const bf16_bits* q;  // the Q tile
+        const bf16_bits* o;  // the dO tile
+        const float* ld;     // lse row of the Q step (wave 0) or delta row of the dO step (wave 1)
+        uint32_t qoff[BPW], ooff[BPW], lvoff;
+        int qbuf, obuf, lbuf;
+    };
+    // Byte offsets of this wave's blocks in a whole tile; a tile cut by the
+    // end of the sequence clamps them to the last row: min over rows of
+    // row*stride + column is min(offset, last row*stride + column).
+    uint32_t full_off[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; i++) full_off[i] = (uint32_t)(((lane_row + wv * BPW + i) * (int)qrs + lane_col) * 2);
+    auto tile_offsets = [&](int q0, uint32_t (&off)[BPW]) {
+        const uint32_t cap = ((uint32_t)(p.seq - 1 - q0) * (uint32_t)qrs + (uint32_t)lane_col) * 2u;
+#pragma unroll
+        for (int i = 0; i < BPW; i++) off[i] = min(full_off[i], cap);
+    };
+    auto set_loads = [&](Pos xq, int qbuf, Pos xo, int obuf, int dbuf) {
+        Loads l;
+        l.q = qg + (long)xq.q0 * qrs + (long)xq.h * DP;
+        l.o = og + (long)xo.q0 * qrs + (long)xo.h * DP;
+        tile_offsets(xq.q0, l.qoff);
+        tile_offsets(xo.q0, l.ooff);
+        const Pos xl = wv == 0 ? xq : xo;
+        l.ld = (wv == 0 ? p.lse : p.delta) + lrow_base + (long)xl.h * p.seq;
+        l.lvoff = (uint32_t)(min(xl.q0 + lrow, p.seq - 1) * 4);
+        l.qbuf = qbuf;
+        l.obuf = obuf;
+        l.lbuf = wv == 0 ? qbuf : dbuf;
+        return l;
+    };
+    // Load i of this wave's share: Q blocks, dO blocks, then lse / delta.
+    auto issue_load = [&](int i, const Loads& l) {
+        if (i < BPW) {
+            lds_load16_sv(l.q, l.qoff[i], sQ + l.qbuf * TSZ + (wv * BPW + i) * BSTRIDE);
+        } else if (i < 2 * BPW) {
+            lds_load16_sv(l.o, l.ooff[i - BPW], sO + l.obuf * TSZ + (wv * BPW + i - BPW) * BSTRIDE);
+        } else {
+            lds_load4_sv(l.ld, l.lvoff, wv == 0 ? sL[l.lbuf] : sD[l.lbuf]);
+        }
+    };
+    auto issue_all = [&](const Loads& l, auto n) {
+#pragma unroll
+        for (int i = 0; i < decltype(n)::value; i++) issue_load(i, l);
+    };
+    // This wave's loads have landed and its LDS accesses are done; then the
+    // workgroup barrier (no fence: the waits above are exactly the ones the
+    // barrier must cover).
+    auto step_barrier = [&]() {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    // Operands, read ahead of their use.  Row operand (kd) of query block qb
+    // of tile A.
+    auto rd_row = [&](const bf16_bits* A, int qb, int kd) {
+        return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(A + rrow + qb * 2 * ROW16 + kd * 8));
+    };
+    // Transposed operand o = 2*db + sub (sub 0: MFMA rows 4hh..+3 and
+    // 8+4hh..+3; 1: 16 more) of query block qb of tile A.
+    auto rd_tr = [&](const bf16_bits* A, int qb, int o) {
+        const bf16_bits* t = A + trow + qb * 2 * ROW16 + (o >> 1) * 32 + (o & 1) * ROW16;
+        return join_bf16x4(ds_read_tr16(t), ds_read_tr16(t + 2 * BSTRIDE));
+    };
+    // x[kb] = rows of query block qb of tile A times the wave's K^T / V^T
+    // operands (S or dP of the block), unscheduled (masked steps).
+    auto score = [&](const bf16_bits* A, int qb, const bf16x8 (&xf)[NKB][NKD], f32x16 (&x)[NKB]) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) x[kb] = zero16();
+#pragma unroll
+        for (int kd = 0; kd < NKD; kd++) {
+            const bf16x8 a = rd_row(A, qb, kd);
+#pragma unroll
+            for (int kb = 0; kb < NKB; kb++) x[kb] = mfma32(a, xf[kb][kd], x[kb]);
+        }
+    };
+    // acc[db][kb] += (tile A, query block qb)^T op[kb], unscheduled.
+    auto products = [&](const bf16_bits* A, int qb, const bf16x8 (&op)[NKB][2], f32x16 (&acc)[NDB][NKB]) {
+#pragma unroll
+        for (int o = 0; o < 2 * NDB; o++) {
+            const bf16x8 t = rd_tr(A, qb, o);
+#pragma unroll
+            for (int kb = 0; kb < NKB; kb++) mfma_acc(acc[o >> 1][kb], t, op[kb][o & 1]);
+        }
+    };
+
+    // K^T (P waves) or V^T (dS waves) operands: key key0 + 32*kb + l32,
+    // head dims hh*HALF + kd*8 + [0, 8).
+    auto load_keys = [&](const void* src_, bf16x8 (&xf)[NKB][NKD]) {
+        const bf16_bits* src = static_cast<const bf16_bits*>(src_) + (long)b * p.kv_bs + (long)g * DP + hh * HALF;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const int kw = key0 + kb * 32 + l32;
+            const bool ok = kw < p.seq;
+            const bf16_bits* xr = src + (long)(ok ? kw : 0) * kvrs;
+#pragma unroll
+            for (int kd = 0; kd < NKD; kd++)
+                xf[kb][kd] =
+                    __builtin_bit_cast(bf16x8, ok ? *reinterpret_cast<const uint4*>(xr + kd * 8) : make_uint4(0, 0, 0, 0));
+        }
+    };
+    auto zero_acc = [&](f32x16 (&acc)[NDB][NKB]) {
+#pragma unroll
+        for (int db = 0; db < NDB; db++)
+#pragma unroll
+            for (int kb = 0; kb < NKB; kb++) {
+                acc[db][kb] = zero16();
+                agpr_pin(acc[db][kb]);
+            }
+    };
+    // After a wave's last step: its last loads (a step past the end, into an
+    // unused buffer) have landed before it can leave the workgroup's LDS,
+    // and the last MFMA writing an accumulator completes before anything
+    // reads it: 34 wait states (a 32x32x16 MFMA takes 8 passes of 4
+    // cycles), tied to every accumulator so that no read is scheduled above
+    // them.
+    auto acc_drain = [&](f32x16 (&acc)[NDB][NKB]) {
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 15\n\ts_nop 15\n\ts_nop 3"
+                     : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[1][0]), "+a"(acc[1][1]), "+a"(acc[2][0]),
+                       "+a"(acc[2][1]), "+a"(acc[3][0]), "+a"(acc[3][1]));
+    };
+    auto store_rows = [&](float* dst, f32x16 (&acc)[NDB][NKB], bool scale) {
+        if (!pair_live) return;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            const int kw = key0 + kb * 32 + l32;
+            if (kw >= p.seq) continue;
+            float* row = dst + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
+#pragma unroll
+            for (int db = 0; db < NDB; db++) {
+                if (scale) acc[db][kb] *= p.scale;  // dS was accumulated without the softmax scale
+                add_row_block(row, acc[db][kb], db * 32, hh, DP, true);
+            }
+        }
+    };
+    // Per-row values (lse or delta) of MFMA rows 8*g4 + 4*hh + [0, 4) of
+    // query block qb: elements 4*g4 .. 4*g4 + 3 of a lane's 16.
+    auto row_vals4 = [&](const float* src, int qb, int g4) {
+        return *reinterpret_cast<const float4*>(&src[qb * 32 + g4 * 8 + hh * 4]);
+    };
+
+    // ------------------------------------------------------------ P waves
+    auto run_p = [&]() {
+        bf16x8 xf[NKB][NKD];
+        load_keys(p.k, xf);
+        f32x16 acc[NDB][NKB];  // dV^T, in AGPRs
+        zero_acc(acc);
+
+        // P of an element: exp2(S*scale*log2e - lse*log2e).
+        auto p_elem = [&](float s, float lv) { return __builtin_amdgcn_exp2f(__builtin_fmaf(s, p.sl2, -lv)); };
+        auto lse_part = [&](const float* Ls, int qb, int g4, float (&lv)[16]) {
+            const float4 l = row_vals4(Ls, qb, g4);
+            lv[g4 * 4 + 0] = l.x * kLog2e;
+            lv[g4 * 4 + 1] = l.y * kLog2e;
+            lv[g4 * 4 + 2] = l.z * kLog2e;
+            lv[g4 * 4 + 3] = l.w * kLog2e;
+        };
+        auto publish = [&](int pbuf, int qb, int kb, const bf16x8 (&pb)[2]) {
+            sP[pbuf][pair][qb][kb][0][lane] = __builtin_bit_cast(uint4, pb[0]);
+            sP[pbuf][pair][qb][kb][1][lane] = __builtin_bit_cast(uint4, pb[1]);
+        };
+
+        // Masked step (diagonal or ragged): everything in program order.
+        // Element r of block (qb, kb) is MFMA row g4*8 + hh*4 + i (r = 4*g4 + i)
+        // and key key0 + 32*kb + l32; masked are keys past the query and rows
+        // past the sequence.
+        auto masked_step = [&](Pos x, int qbuf, int obuf, int pbuf) {
+            const bf16_bits* Qs = sQ + qbuf * TSZ;
+            const bf16_bits* Os = sO + obuf * TSZ;
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                f32x16 sc[NKB];
+                bf16x8 pq[NKB][2];
+                float lv[16];
+                score(Qs, qb, xf, sc);
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) lse_part(sL[qbuf], qb, g4, lv);
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) {
+                    const int kw = key0 + kb * 32 + l32;
+                    float pr[16];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        float pv = p_elem(sc[kb][r], lv[r]);
+                        const int q = x.q0 + qb * 32 + qperm((r >> 2) * 8 + hh * 4 + (r & 3));
+                        if (kw > q || q >= p.seq) pv = 0.0f;
+                        pr[r] = pv;
+                    }
+                    pq[kb][0] = cvt_bf16x8(&pr[0]);
+                    pq[kb][1] = cvt_bf16x8(&pr[8]);
+                    publish(pbuf, qb, kb, pq[kb]);
+                }
+                CF_HAZARD_FENCE();
+                products(Os, qb, pq, acc);
+            }
+        };
+
+        // Pipeline state entering a full step t: S of (t, block 0, key block
+        // 1), lse*log2e of block 0's rows, and P of (t, block 0, key block 0)
+        // as operands (published in R1 of interval t, where its LDS buffer is
+        // free).  Two copies, for even and odd steps: each step reads one and
+        // forms the other in place.
+        struct PState {
+            f32x16 s01;
+            float lv0[16];
+            bf16x8 p00[2];
+        };
+        PState st0, st1;
+        // Forms the state of full step x (unscheduled: after a masked step).
+        auto prime = [&](int qbuf, PState& o) {
+            f32x16 sc[NKB];
+            score(sQ + qbuf * TSZ, 0, xf, sc);
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) lse_part(sL[qbuf], 0, g4, o.lv0);
+            float pr[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) pr[r] = p_elem(sc[0][r], o.lv0[r]);
+            o.p00[0] = cvt_bf16x8(&pr[0]);
+            o.p00[1] = cvt_bf16x8(&pr[8]);
+            o.s01 = sc[1];
+        };
+
+        // Full step t in regions R1-R4, fenced in slots of one MFMA and the
+        // work that issues in its shadow (a second MFMA right behind would
+        // block issue until the pipe frees).  EARLY: step t + 1 is full too,
+        // and its S of block 0 and first softmax quarter are formed here.
+        auto full_step = [&](auto early_tag, int qbuf, int obuf, int pbuf, int nqbuf, const Loads& ld,
+                             const PState& in, PState& out) {
+            constexpr bool EARLY = decltype(early_tag)::value;
+            const bf16_bits* Qs = sQ + qbuf * TSZ;
+            const bf16_bits* Qn = sQ + nqbuf * TSZ;  // Q of step t + 1
+            const bf16_bits* Os = sO + obuf * TSZ;
+            bf16x8 qr[NKD], tr[2 * NDB];
+            float lv1[16], pr[16];
+            f32x16 s1[NKB], sn0;
+            bf16x8 p01[2], p10[2], p11[2];
+            // Element e of a softmax quarter per slot; the quarter's halves
+            // are rounded to bf16 operands after elements 7 and 15 (and
+            // published unless the quarter belongs to the next step).
+            auto sm = [&](int e, const f32x16& sc, const float (&lv)[16], bf16x8 (&pb)[2], int qb, int kb, bool pub) {
+                pr[e] = p_elem(sc[e], lv[e]);
+                if ((e & 7) == 7) {
+                    pb[e >> 3] = cvt_bf16x8(&pr[e & 8]);
+                    if (pub) sP[pbuf][pair][qb][kb][e >> 3][lane] = __builtin_bit_cast(uint4, pb[e >> 3]);
+                }
+            };
+            // R1: S of (t, 1) | softmax (t, 0, 1); P (t, 0, 0) published;
+            // lse of block 1; this interval's loads.
+            qr[0] = rd_row(Qs, 1, 0);
+            qr[1] = rd_row(Qs, 1, 1);
+            publish(pbuf, 0, 0, in.p00);
+            CF_FENCE();
+#pragma unroll
+            for (int k = 0; k < 2 * NKD; k++) {
+                const int kd = k >> 1, kb = k & 1;
+                if (kb == 0 && kd + 2 < NKD) qr[kd + 2] = rd_row(Qs, 1, kd + 2);
+                if (k < 4) lse_part(sL[qbuf], 1, k, lv1);
+                if (k >= 2 * NKD - 2) tr[k - (2 * NKD - 2)] = rd_tr(Os, 0, k - (2 * NKD - 2));
+                s1[kb] = mfma32(qr[kd], xf[kb][kd], kd == 0 ? zero16() : s1[kb]);
+                sm(k, in.s01, in.lv0, p01, 0, 1, true);
+                if (kb == 0) issue_load(kd, ld);
+                CF_FENCE();
+            }
+            CF_HAZARD_FENCE();
+            // R2: dV of (t, 0) | softmax (t, 1, 0).
+#pragma unroll
+            for (int k = 0; k < 2 * NKD; k++) {
+                const int o = k >> 1, kb = k & 1;
+                if (kb == 0 && o + 2 < 2 * NDB) tr[o + 2] = rd_tr(Os, 0, o + 2);
+                if (EARLY && kb == 0 && o >= 2 * NDB - 2) qr[o - (2 * NDB - 2)] = rd_row(Qn, 0, o - (2 * NDB - 2));
+                mfma_acc(acc[o >> 1][kb], tr[o], kb == 0 ? in.p00[o & 1] : p01[o & 1]);
+                sm(k, s1[0], lv1, p10, 1, 0, true);
+                if (k == 0) issue_load(NKD, ld);
+                CF_FENCE();
+            }
+            // R3: S of (t+1, 0) | softmax (t, 1, 1); lse of (t+1, 0).
+#pragma unroll
+            for (int k = 0; k < 2 * NKD; k++) {
+                const int kd = k >> 1, kb = k & 1;
+                if (EARLY) {
+                    if (kb == 0 && kd + 2 < NKD) qr[kd + 2] = rd_row(Qn, 0, kd + 2);
+                    if (k < 4) lse_part(sL[nqbuf], 0, k, out.lv0);
+                }
+                if (k >= 2 * NKD - 2) tr[k - (2 * NKD - 2)] = rd_tr(Os, 1, k - (2 * NKD - 2));
+                if (EARLY) {
+                    if (kb == 0)
+                        sn0 = mfma32(qr[kd], xf[0][kd], kd == 0 ? zero16() : sn0);
+                    else
+                        out.s01 = mfma32(qr[kd], xf[1][kd], kd == 0 ? zero16() : out.s01);
+                }
+                sm(k, s1[1], lv1, p11, 1, 1, true);
+                CF_FENCE();
+            }
+            CF_HAZARD_FENCE();
+            // R4: dV of (t, 1) | softmax (t+1, 0, 0), kept for the next
+            // interval.
+#pragma unroll
+            for (int k = 0; k < 2 * NKD; k++) {
+                const int o = k >> 1, kb = k & 1;
+                if (kb == 0 && o + 2 < 2 * NDB) tr[o + 2] = rd_tr(Os, 1, o + 2);
+                mfma_acc(acc[o >> 1][kb], tr[o], kb == 0 ? p10[o & 1] : p11[o & 1]);
+                if (EARLY) sm(k, sn0, out.lv0, out.p00, 0, 0, false);
+                CF_FENCE();
+            }
+        };
+
+        Pos cur = first, n1 = next_pos(first), n2 = next_pos(n1);
+        int qbuf = 0, obuf = 0, dbuf = 0;  // buffers of the current step
+        if (pos_full(cur)) prime(qbuf, st0);
+        // Step s with state `in` (formed by the previous step), forming `out`.
+        auto step = [&](int s, const PState& in, PState& out) {
+            const int pbuf = s & 1;
+            const int nqbuf = (qbuf + 1) & 3, lqbuf = (qbuf + 2) & 3;
+            const int nobuf = obuf ^ 1, ndbuf = dbuf == 2 ? 0 : dbuf + 1;
+            // Loads of interval s: Q of step s + 2, dO of step s + 1 (a step
+            // past the last reloads step s, unused).
+            const Loads ld = set_loads(s + 2 < n_steps ? n2 : cur, lqbuf, s + 1 < n_steps ? n1 : cur, nobuf, ndbuf);
+            const bool full = pos_full(cur);
+            const bool next_full = s + 1 < n_steps && pos_full(n1);
+            if (full && next_full) {
+                full_step(std::true_type{}, qbuf, obuf, pbuf, nqbuf, ld, in, out);
+            } else if (full) {
+                full_step(std::false_type{}, qbuf, obuf, pbuf, nqbuf, ld, in, out);
+            } else {
+                issue_all(ld, std::integral_constant<int, kLoadsP>{});
+                if (pos_act(cur)) masked_step(cur, qbuf, obuf, pbuf);
+                if (next_full) prime(nqbuf, out);
+            }
+            step_barrier();
+            cur = n1;
+            n1 = n2;
+            n2 = next_pos(n2);
+            qbuf = nqbuf;
+            obuf = nobuf;
+            dbuf = ndbuf;
+        };
+        for (int s = 0; s < n_steps; s += 2) {
+            step(s, st0, st1);
+            if (s + 1 < n_steps) step(s + 1, st1, st0);
+        }
+        acc_drain(acc);
+        store_rows(p.dv, acc, false);
+    };
+
+    // ----------------------------------------------------------- dS waves
+    auto run_ds = [&]() {
+        bf16x8 xf[NKB][NKD];
+        load_keys(p.v, xf);
+        f32x16 acc[NDB][NKB];  // dK^T, in AGPRs
+        zero_acc(acc);
+
+        // dS of element r of a block: P (the bf16 value the P wave's dV
+        // product used; widening is exact) times dP - delta.  w: the block's
+        // two published halves as eight words.
+        auto ds_elem = [&](const uint32_t (&w)[8], int r, float dpd) {
+            const uint32_t word = w[r >> 1];
+            return __uint_as_float((r & 1) ? (word & 0xffff0000u) : (word << 16)) * dpd;
+        };
+        auto p_words = [&](int pbuf, int qb, int kb, uint32_t (&w)[8]) {
+            const uint4 a = sP[pbuf][pair][qb][kb][0][lane], c = sP[pbuf][pair][qb][kb][1][lane];
+            w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = c.x, w[5] = c.y, w[6] = c.z, w[7] = c.w;
+        };
+        auto delta16 = [&](int dbuf_, int qb, float (&dl)[16]) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const float4 d = row_vals4(sD[dbuf_], qb, g4);
+                dl[g4 * 4 + 0] = d.x, dl[g4 * 4 + 1] = d.y, dl[g4 * 4 + 2] = d.z, dl[g4 * 4 + 3] = d.w;
+            }
+        };
+        // One 16-byte piece (qb, kb, half h) of a step's dS (rounded to bf16)
+        // to the stored-dS scratch: blocks on or below the causal diagonal
+        // only (the layout has no others), non-temporal (the dQ kernel reads
+        // each once).
+        auto ds_store = [&](Pos x, int qb, int kb, int h, const bf16x8& v, bool check) {
+            const int qi = (x.q0 >> 5) + qb, ki = (key0 >> 5) + kb;
+            if (check && !(ki <= qi && x.q0 + qb * 32 < p.seq)) return;
+            const long ds_head = ((long)b * p.nh + x.h) * p.ds_ntri;
+            bf16_bits* blk = p.ds + (ds_head + (long)qi * (qi + 1) / 2 + ki) * kDsBlock;
+            __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v),
+                                        reinterpret_cast<u32x4*>(blk + (h ? ds_off1 : ds_off0)));
+        };
+
+        // dP - delta of the step whose dS comes next, by query block and key
+        // block.  Two copies, for even and odd steps: each iteration reads
+        // one and forms the other in place.
+        struct DState {
+            f32x16 d[2][NKB];
+        };
+        DState st0, st1;
+        // Forms it for the step with dO in buffer obuf (unscheduled).
+        auto dp_of = [&](int obuf, int dbuf_, DState& o) {
+            score(sO + obuf * TSZ, 0, xf, o.d[0]);
+            score(sO + obuf * TSZ, 1, xf, o.d[1]);
+            float dl[16];
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                delta16(dbuf_, qb, dl);
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) o.d[qb][kb][r] -= dl[r];
+            }
+        };
+        // dS and dK of step x (unscheduled; its P in buffer pbuf).
+        auto ds_dk = [&](Pos x, int qbuf, int pbuf, bool check, const DState& in) {
+            const bf16_bits* Qs = sQ + qbuf * TSZ;
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++) {
+                bf16x8 dq[NKB][2];
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) {
+                    uint32_t w[8];
+                    p_words(pbuf, qb, kb, w);
+                    float ds[16];
+#pragma unroll
+                    for (int r = 0; r < 16; r++) ds[r] = ds_elem(w, r, in.d[qb][kb][r]);
+                    dq[kb][0] = cvt_bf16x8(&ds[0]);
+                    dq[kb][1] = cvt_bf16x8(&ds[8]);
+                    if constexpr (WDS) {
+                        ds_store(x, qb, kb, 0, dq[kb][0], check);
+                        ds_store(x, qb, kb, 1, dq[kb][1], check);
+                    }
+                }
+                CF_HAZARD_FENCE();
+                products(Qs, qb, dq, acc);
+            }
+        };
+
+        // Iteration t (interval t + 1): dS and dK of step t, dP - delta of
+        // step t + 1, in regions R1-R4 (see the file header).  Step t is
+        // unmasked and step t + 1 active.
+        auto full_iter = [&](Pos x, int qbuf, int pbuf, int nobuf, int ndbuf, const Loads& ld, const DState& in,
+                             DState& out) {
+            const bf16_bits* Qs = sQ + qbuf * TSZ;
+            const bf16_bits* On = sO + nobuf * TSZ;  // dO of step t + 1
+            bf16x8 orow[NKD], tr[2 * NDB];
+            uint32_t w[NKB][8];
+            float ds[NKB][16], dl[16];
+            bf16x8 d0[NKB][2], d1[NKB][2];
+            // dS element e of (t, qb, kb) per slot, rounded after 7 and 15.
+            auto dse = [&](int qb, int kb, int e, bf16x8 (&dd)[NKB][2]) {
+                ds[kb][e] = ds_elem(w[kb], e, in.d[qb][kb][e]);
+                if ((e & 7) == 7) dd[kb][e >> 3] = cvt_bf16x8(&ds[kb][e & 8]);
+            };
+            // Piece i of the step's stored dS: (qb, kb, half) = (i / 4, (i / 2) % 2, i % 2).
+            auto store_piece = [&](int i) {
+                const int sq = i >> 2, skb = (i >> 1) & 1, sh = i & 1;
+                ds_store(x, sq, skb, sh, sq ? d1[skb][sh] : d0[skb][sh], false);
+            };
+            orow[0] = rd_row(On, 0, 0);
+            orow[1] = rd_row(On, 0, 1);
+            p_words(pbuf, 0, 0, w[0]);
+            p_words(pbuf, 0, 1, w[1]);
+            CF_FENCE();
+            // R1: dP of (t+1, 0) | dS of (t, 0); this interval's loads.
+#pragma unroll
+            for (int k = 0; k < 2 * NKD; k++) {
+                const int kd = k >> 1, kb = k & 1;
+                if (kb == 0 && kd + 2 < NKD) orow[kd + 2] = rd_row(On, 0, kd + 2);
+                if (k >= 2 * NKD - 2) tr[k - (2 * NKD - 2)] = rd_tr(Qs, 0, k - (2 * NKD - 2));
+                out.d[0][kb] = mfma32(orow[kd], xf[kb][kd], kd == 0 ? zero16() : out.d[0][kb]);
+                dse(0, 0, k, d0);
+                dse(0, 1, k, d0);
+                if (kb == 0) issue_load(kd, ld);
+                CF_FENCE();
+            }
+            // Block 1's P words for R2/R3, and delta of (t+1, 0).
+            p_words(pbuf, 1, 0, w[0]);
+            p_words(pbuf, 1, 1, w[1]);
+            delta16(ndbuf, 0, dl);
+            CF_HAZARD_FENCE();
+            // R2: dK of (t, 0) | dS of (t, 1, 0).
+#pragma unroll
+            for (int k = 0; k < 2 * NKD; k++) {
+                const int o = k >> 1, kb = k & 1;
+                if (kb == 0 && o + 2 < 2 * NDB) tr[o + 2] = rd_tr(Qs, 0, o + 2);
+                if (kb == 0 && o >= 2 * NDB - 2) orow[o - (2 * NDB - 2)] = rd_row(On, 1, o - (2 * NDB - 2));
+                mfma_acc(acc[o >> 1][kb], tr[o], d0[kb][o & 1]);
+                dse(1, 0, k, d1);
+                if constexpr (WDS) {
+                    if ((k & 3) == 2) store_piece(k >> 2);
+                }
+                CF_FENCE();
+            }
+            // R3: dP of (t+1, 1) | dS of (t, 1, 1); dP - delta of (t+1, 0).
+#pragma unroll
+            for (int k = 0; k < 2 * NKD; k++) {
+                const int kd = k >> 1, kb = k & 1;
+                if (kb == 0 && kd + 2 < NKD) orow[kd + 2] = rd_row(On, 1, kd + 2);
+                if (k >= 2 * NKD - 2) tr[k - (2 * NKD - 2)] = rd_tr(Qs, 1, k - (2 * NKD - 2));
+                out.d[1][kb] = mfma32(orow[kd], xf[kb][kd], kd == 0 ? zero16() : out.d[1][kb]);
+                dse(1, 1, k, d1);
+                out.d[0][0][k] -= dl[k];
+                out.d[0][1][k] -= dl[k];
+                CF_FENCE();
+            }
+            delta16(ndbuf, 1, dl);
+            CF_HAZARD_FENCE();
+            // R4: dK of (t, 1) | dP - delta of (t+1, 1); the step's dS stores.
+#pragma unroll
+            for (int k = 0; k < 2 * NKD; k++) {
+                const int o = k >> 1, kb = k & 1;
+                if (kb == 0 && o + 2 < 2 * NDB) tr[o + 2] = rd_tr(Qs, 1, o + 2);
+                mfma_acc(acc[o >> 1][kb], tr[o], d1[kb][o & 1]);
+                out.d[1][0][k] -= dl[k];
+                out.d[1][1][k] -= dl[k];
+                if constexpr (WDS) {
+                    if ((k & 3) == 2) store_piece(4 + (k >> 2));
+                }
+                CF_FENCE();
+            }
+        };
+
+        // Interval 0: dP - delta of step 0 and this wave's loads of interval
+        // 0 (Q of step 2, dO of step 1).
+        Pos cur = first, n1 = next_pos(first), n2 = next_pos(n1), n3 = next_pos(n2);
+        issue_all(set_loads(n_steps > 2 ? n2 : first, 2, n_steps > 1 ? n1 : first, 1, 1),
+                  std::integral_constant<int, kLoadsDs>{});
+        if (pos_act(cur)) dp_of(0, 0, st0);
+        // Iteration s runs in interval s + 1, whose loads are Q of step s + 3
+        // and dO of step s + 2.
+        int qbuf = 0, dbuf = 0;  // buffers of step s
+        auto iter = [&](int s, const DState& in, DState& out) {
+            step_barrier();
+            const int pbuf = s & 1;
+            const int nobuf = (s + 1) & 1, ndbuf = dbuf == 2 ? 0 : dbuf + 1;
+            const int lqbuf = (qbuf + 3) & 3, lobuf = s & 1, ldbuf = ndbuf == 2 ? 0 : ndbuf + 1;
+            const Loads ld = set_loads(s + 3 < n_steps ? n3 : cur, lqbuf, s + 2 < n_steps ? n2 : cur, lobuf, ldbuf);
+            const bool act = pos_act(cur);
+            const bool act_n = s + 1 < n_steps && pos_act(n1);
+            if (act && act_n && pos_full(cur)) {
+                full_iter(cur, qbuf, pbuf, nobuf, ndbuf, ld, in, out);
+            } else {
+                issue_all(ld, std::integral_constant<int, kLoadsDs>{});
+                if (act) ds_dk(cur, qbuf, pbuf, !pos_full(cur), in);
+                if (act_n) dp_of(nobuf, ndbuf, out);
+            }
+            cur = n1;
+            n1 = n2;
+            n2 = n3;
+            n3 = next_pos(n3);
+            qbuf = (qbuf + 1) & 3;
+            dbuf = ndbuf;
+        };
+        for (int s = 0; s < n_steps; s += 2) {
+            iter(s, st0, st1);
+            if (s + 1 < n_steps) iter(s + 1, st1, st0);
+        }
+        acc_drain(acc);
+        store_rows(p.dk, acc, true);
+    };
+
+    // Interval 0 needs Q (and lse) of steps 0 and 1, dO (and delta) of step 0.
+    {
+        const Loads l0 = set_loads(first, 0, first, 0, 0);
+        if (pwave)
+            issue_all(l0, std::integral_constant<int, kLoadsP>{});
+        else
+            issue_all(l0, std::integral_constant<int, kLoadsDs>{});
+        const Loads l1 = set_loads(n_steps > 1 ? next_pos(first) : first, 1, first, 0, 0);
+#pragma unroll
+        for (int i = 0; i < BPW; i++) issue_load(i, l1);
+        if (wv == 0) issue_load(2 * BPW, l1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (pwave)
+        run_p();
+    else
+        run_ds();
+}
+
+#undef CF_FENCE
+#undef CF_HAZARD_FENCE
+
+void launch_attn_bwd_dkdv_k64(const BwdParams& p, bool wds, hipStream_t st) {
+    if (wds)
+        hipLaunchKernelGGL((attn_bwd_dkdv_k64_kernel<true>), dim3(p.n_wg_kv), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL((attn_bwd_dkdv_k64_kernel<false>), dim3(p.n_wg_kv), dim3(256), 0, st, p);
+}
+
+}  // namespace cfattn

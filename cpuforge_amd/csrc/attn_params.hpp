@@ -72,5 +72,8 @@ size_t attn_f32_fwd_scratch_bytes(const Dims& d);
 hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t scratch_bytes, hipStream_t st,
                                KernelTimer* tm);
 hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStream_t st, KernelTimer* tm);
+// bf16 dK/dV at head_dim 128, one wave per SIMD (attn_dkdv.hip); with
+// `wds` it also stores dS for the stored-dS dQ kernel.  p.kv_tile is 128.
+void launch_attn_bwd_dkdv_k64(const BwdParams& p, bool wds, hipStream_t st);
 
 }  // namespace cfattn

@@ -277,6 +277,21 @@ __device__ __forceinline__ void lds_load16_nt_asm(const void* g, const void* lds
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
     asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(m0) : "memory");
 }
+// The same loads addressed as a scalar base plus a 32-bit per-lane byte
+// offset (the saddr form: no 64-bit address arithmetic per lane).
+__device__ __forceinline__ void lds_load16_sv(const void* sbase, uint32_t voff, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+__device__ __forceinline__ void lds_load4_sv(const void* sbase, uint32_t voff, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+    asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+// 64 lanes x 4 bytes to 256 consecutive bytes of LDS (one float per lane).
+__device__ __forceinline__ void lds_load4_asm(const void* g, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+    asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+}
 
 // ------------------------------------------------- blocked bf16 LDS tiles
 // A tile of ROWS rows of DP bf16 (DP = 64 or 128) filled by direct-to-LDS

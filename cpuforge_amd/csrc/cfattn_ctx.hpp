@@ -7,6 +7,8 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -126,6 +128,10 @@ struct cfattn_ctx {
     cfattn::Tuning tuning() const {
         cfattn::Tuning t;
         t.timer = timer;
+        // CFATTN_DKDV_KERNEL=ws selects the two-waves-per-SIMD dK/dV kernel
+        // (bitwise equal results; kept for comparison and measurement).
+        const char* v = std::getenv("CFATTN_DKDV_KERNEL");
+        if (v && std::strcmp(v, "ws") == 0) t.dkdv_variant = cfattn::kDkdvWaveSpecialised;
         return t;
     }
 };

@@ -36,12 +36,19 @@ struct KernelTimer {
     virtual ~KernelTimer() = default;
 };
 
+// dK/dV kernel of the bf16 fast path at head_dim 128.
+enum DkdvVariant {
+    kDkdvAuto = 0,              // one wave per SIMD, 64 keys per wave
+    kDkdvWaveSpecialised = 1    // two waves per SIMD, 32 keys per wave (same results, bit for bit)
+};
+
 // Tuning knobs of one launch; defaults are chosen by the launchers.
 struct Tuning {
     int xcd_remap = 1;  // XCD-aware workgroup ordering
     int fwd_heads_per_wg = 0;  // 0 = automatic
     int fwd_tblocks_per_wg = 0;
     int bwd_kv_waves = 0;
+    int dkdv_variant = kDkdvAuto;
     KernelTimer* timer = nullptr;
 };
 

@@ -383,3 +383,31 @@ def test_stored_ds_matches_recompute(cf, shape):
     e = rel_err(sq.reshape(-1), rq.reshape(-1))
     print(f"  dq rel diff {e:.3e}, bitwise equal {np.array_equal(sq, rq)}", flush=True)
     assert e <= 1e-5
+
+
+@pytest.mark.parametrize("ds", ["stored", "recompute"])
+@pytest.mark.parametrize("shape", [(1, 1000, 8, 2, 128), (2, 300, 4, 4, 128), (1, 2048, 32, 8, 128),
+                                   (3, 129, 6, 3, 128), (1, 64, 4, 1, 128), (1, 1, 4, 1, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_dkdv_one_wave_per_simd_matches_wave_specialised(cf, shape, ds, monkeypatch):
+    """The head_dim-128 dK/dV kernel with one wave per SIMD (64 keys per
+    wave) sums every element's products in the order of the two-waves-per-
+    SIMD kernel (CFATTN_DKDV_KERNEL=ws): dK, dV and dQ (from the stored dS,
+    or recomputed) must be bitwise equal."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    print(f"dK/dV kernels, shape {shape}, dS {ds}", flush=True)
+    _, (q, k, v, g) = _fast_inputs(shape, seed=1900)
+    o, lse = D.fwd(q, k, v, ctx=ctx)
+    out = {}
+    with _DsLimit(ctx, ctx.ds_limit if ds == "stored" else 0):
+        for kern in ("ws", "k64"):
+            if kern == "ws":
+                monkeypatch.setenv("CFATTN_DKDV_KERNEL", "ws")
+            else:
+                monkeypatch.delenv("CFATTN_DKDV_KERNEL", raising=False)
+            out[kern] = [x.cpu().numpy() for x in D.bwd(g, q, k, v, o, lse, ctx=ctx)]
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv"), out["k64"], out["ws"]):
+        assert np.array_equal(a, b), f"{shape} {ds} {name}: max diff {np.abs(a - b).max()}"
