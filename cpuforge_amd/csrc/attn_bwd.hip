@@ -487,6 +487,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const bf16_bits* kg = static_cast<const bf16_bits*>(p.k) + (long)b * p.kv_bs + (long)g * DP;
     const bf16_bits* vg = static_cast<const bf16_bits*>(p.v) + (long)b * p.kv_bs + (long)g * DP;
 
+    // Q and -dO operands of the lane's query: the dP^T product accumulates
+    // the negated products onto delta, giving delta - dP (as the dK/dV
+    // kernels form it, so both dQ paths see the same dS).
     bf16x8 qf[NKD], of[NKD];
     {
         const bf16_bits* qr = static_cast<const bf16_bits*>(p.q) + qoff + hh * HALF;
@@ -495,8 +498,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         for (int kd = 0; kd < NKD; kd++) {
             qf[kd] = __builtin_bit_cast(bf16x8,
                                         row_ok ? *reinterpret_cast<const uint4*>(qr + kd * 8) : make_uint4(0, 0, 0, 0));
-            of[kd] = __builtin_bit_cast(bf16x8,
-                                        row_ok ? *reinterpret_cast<const uint4*>(orr + kd * 8) : make_uint4(0, 0, 0, 0));
+            uint4 u = row_ok ? *reinterpret_cast<const uint4*>(orr + kd * 8) : make_uint4(0, 0, 0, 0);
+            u.x ^= 0x80008000u, u.y ^= 0x80008000u, u.z ^= 0x80008000u, u.w ^= 0x80008000u;
+            of[kd] = __builtin_bit_cast(bf16x8, u);
         }
     }
     const long lrow = ((long)b * p.nh + head) * p.seq + tq;
@@ -552,7 +556,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             auto block = [&](int kb, bool masked) {
                 // S^T first, then dP^T: P = exp2(...) needs only S^T and runs
                 // while the dP^T products are in flight.
-                f32x16 sc = zero16(), dp = zero16();
+                f32x16 sc = zero16(), dp;
+#pragma unroll
+                for (int r = 0; r < 16; r++) dp[r] = dlt;
 #pragma unroll
                 for (int kd = 0; kd < NKD; kd++)
                     sc = mfma32(__builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
@@ -570,12 +576,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                     pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lse2));
                     if (masked && kb0 + qperm((r >> 2) * 8 + hh * 4 + (r & 3)) > tq) pr[r] = 0.0f;
                 }
-                // dS^T without the softmax scale (applied once to dQ), from P
-                // rounded to bf16 as the dK/dV kernel forms it, so both dQ
-                // paths see the same dS.
+                // dS^T = P^T * -(delta - dP^T) without the softmax scale
+                // (applied once to dQ), from P rounded to bf16 as the dK/dV
+                // kernel forms it, so both dQ paths see the same dS.
                 float ds[16];
 #pragma unroll
-                for (int r = 0; r < 16; r++) ds[r] = (float)(__bf16)pr[r] * (dp[r] - dlt);
+                for (int r = 0; r < 16; r++) ds[r] = (float)(__bf16)pr[r] * -dp[r];
                 const bf16x8 d0 = cvt_bf16x8(&ds[0]), d1 = cvt_bf16x8(&ds[8]);
                 const bf16_bits* t0 = Ks + trow + kb * 2 * ROW16;
 #pragma unroll
@@ -950,16 +956,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // copies pass the same barriers in the same order.
     auto run = [&](auto role) {
         constexpr bool PW = decltype(role)::value;
-        // K^T (P waves) or V^T (dS waves) operand: key kw, head dims hh*HALF + kd*8 + [0, 8).
+        // K^T (P waves) or -V^T (dS waves) operand: key kw, head dims
+        // hh*HALF + kd*8 + [0, 8).  The dS waves accumulate the negated
+        // products onto delta, so their dP product yields delta - dP (the
+        // negation is exact, and so it is in the dS rounding below).
         bf16x8 xf[NKD];
         {
             const long off = (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP + hh * HALF;
             const bf16_bits* xr = static_cast<const bf16_bits*>(PW ? p.k : p.v) + off;
             const bool ok = kw < p.seq;
+            const uint32_t sgn = PW ? 0u : 0x80008000u;
 #pragma unroll
-            for (int kd = 0; kd < NKD; kd++)
-                xf[kd] = __builtin_bit_cast(bf16x8,
-                                            ok ? *reinterpret_cast<const uint4*>(xr + kd * 8) : make_uint4(0, 0, 0, 0));
+            for (int kd = 0; kd < NKD; kd++) {
+                uint4 u = ok ? *reinterpret_cast<const uint4*>(xr + kd * 8) : make_uint4(0, 0, 0, 0);
+                u.x ^= sgn, u.y ^= sgn, u.z ^= sgn, u.w ^= sgn;
+                xf[kd] = __builtin_bit_cast(bf16x8, u);
+            }
         }
         f32x16 acc[NDB];  // dV^T (P waves) or dK^T (dS waves)
 #pragma unroll
@@ -982,7 +994,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const bf16_bits* A2 = PW ? Os : Qs;
             const long ds_head = ((long)b * p.nh + step_h(s)) * p.ds_ntri;
             bf16x8 pbf[NQB][2];  // P waves: P of each block as MFMA operands
-            f32x16 dpv[NQB];     // dS waves: dP of each block
+            f32x16 dpv[NQB];     // dS waves: delta - dP of each block
             bf16x8 dsv[NQB][2];  // dS waves with WDS: dS of each block, stored after the step
             auto row_read = [&](int qb, int kd) {
                 return __builtin_bit_cast(bf16x8,
@@ -992,6 +1004,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             // to LDS in f32 for the dS waves and to registers as bf16 operands.
             // lse of MFMA rows g4*8 + hh*4 + [0, 4) of block qb.
             auto lse4 = [&](int qb, int g4) { return *reinterpret_cast<const float4*>(&Ls[qb * 32 + g4 * 8 + hh * 4]); };
+            // Initial accumulator of block qb's product: 0 for S, delta of
+            // the lane's MFMA rows g4*8 + hh*4 + [0, 4) for the dS waves.
+            auto init16 = [&](int qb) {
+                f32x16 c = zero16();
+                if constexpr (!PW) {
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; g4++) {
+                        const float4 d4 = *reinterpret_cast<const float4*>(&Ds[qb * 32 + g4 * 8 + hh * 4]);
+                        c[g4 * 4 + 0] = d4.x, c[g4 * 4 + 1] = d4.y, c[g4 * 4 + 2] = d4.z, c[g4 * 4 + 3] = d4.w;
+                    }
+                }
+                return c;
+            };
             auto p_block = [&](int qb, const f32x16& sc, bool masked, const float4 (&l4s)[4]) {
                 float pr[16];
 #pragma unroll
@@ -1026,7 +1051,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 }
                 f32x16 sc[NQB];
 #pragma unroll
-                for (int qb = 0; qb < NQB; qb++) sc[qb] = zero16();
+                for (int qb = 0; qb < NQB; qb++) sc[qb] = init16(qb);
 #pragma unroll
                 for (int kd = 0; kd < NKD; kd++)
 #pragma unroll
@@ -1047,7 +1072,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 for (int qb = 0; qb < NQB; qb++) {
                     const int tq0 = q0 + qb * 32;
                     if (tq0 >= p.seq || tq0 + 31 < key0) continue;
-                    f32x16 sc = zero16();
+                    f32x16 sc = init16(qb);
 #pragma unroll
                     for (int kd = 0; kd < NKD; kd++) sc = mfma32(row_read(qb, kd), xf[kd], sc);
                     if constexpr (PW) {
@@ -1070,16 +1095,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
             // Phase 2: dV^T += dO^T P (P waves), dS -> dK^T += Q^T dS (dS waves).
-            // dS waves: P and delta of MFMA rows g4*8 + hh*4 + [0, 4) of block qb.
+            // dS waves: P of MFMA rows g4*8 + hh*4 + [0, 4) of block qb.
             // P is the bf16 value the P wave's dV product used (widening is
-            // exact); dS = P (dP - delta) then rounds once more, to bf16.
-            auto pd4 = [&](int qb, int g4, float4& p4, float4& d4) {
+            // exact); dS = P (dP - delta) = P * -(delta - dP) then rounds once
+            // more, to bf16.
+            auto pd4 = [&](int qb, int g4) {
                 const uint2 h = reinterpret_cast<const uint2*>(&sPb[slice][qb][g4 >> 1][lane])[g4 & 1];
-                p4 = make_float4(__uint_as_float(h.x << 16), __uint_as_float(h.x & 0xffff0000u),
-                                 __uint_as_float(h.y << 16), __uint_as_float(h.y & 0xffff0000u));
-                d4 = *reinterpret_cast<const float4*>(&Ds[qb * 32 + g4 * 8 + hh * 4]);
+                return make_float4(__uint_as_float(h.x << 16), __uint_as_float(h.x & 0xffff0000u),
+                                   __uint_as_float(h.y << 16), __uint_as_float(h.y & 0xffff0000u));
             };
-            auto phase2 = [&](int qb, const float4 (&p4s)[4], const float4 (&d4s)[4]) {
+            auto phase2 = [&](int qb, const float4 (&p4s)[4]) {
                 bf16x8 b0, b1;
                 if constexpr (PW) {
                     b0 = pbf[qb][0];
@@ -1088,12 +1113,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     float ds[16];
 #pragma unroll
                     for (int g4 = 0; g4 < 4; g4++) {
-                        const float4 d4 = d4s[g4];
                         const float4 p4 = p4s[g4];
-                        ds[g4 * 4 + 0] = p4.x * (dpv[qb][g4 * 4 + 0] - d4.x);
-                        ds[g4 * 4 + 1] = p4.y * (dpv[qb][g4 * 4 + 1] - d4.y);
-                        ds[g4 * 4 + 2] = p4.z * (dpv[qb][g4 * 4 + 2] - d4.z);
-                        ds[g4 * 4 + 3] = p4.w * (dpv[qb][g4 * 4 + 3] - d4.w);
+                        ds[g4 * 4 + 0] = p4.x * -dpv[qb][g4 * 4 + 0];
+                        ds[g4 * 4 + 1] = p4.y * -dpv[qb][g4 * 4 + 1];
+                        ds[g4 * 4 + 2] = p4.z * -dpv[qb][g4 * 4 + 2];
+                        ds[g4 * 4 + 3] = p4.w * -dpv[qb][g4 * 4 + 3];
                     }
                     b0 = cvt_bf16x8(&ds[0]);
                     b1 = cvt_bf16x8(&ds[8]);
@@ -1117,32 +1141,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 }
             };
             if (full) {
-                // dS waves read every P and delta value of the step first.
-                float4 p4s[NQB][4], d4s[NQB][4];
+                // dS waves read every P value of the step first.
+                float4 p4s[NQB][4];
                 if constexpr (!PW && NQB <= 2) {
 #pragma unroll
                     for (int qb = 0; qb < NQB; qb++)
 #pragma unroll
-                        for (int g4 = 0; g4 < 4; g4++) pd4(qb, g4, p4s[qb][g4], d4s[qb][g4]);
+                        for (int g4 = 0; g4 < 4; g4++) p4s[qb][g4] = pd4(qb, g4);
                     __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++) {
                     if constexpr (!PW && NQB > 2)
 #pragma unroll
-                        for (int g4 = 0; g4 < 4; g4++) pd4(qb, g4, p4s[qb][g4], d4s[qb][g4]);
-                    phase2(qb, p4s[qb], d4s[qb]);
+                        for (int g4 = 0; g4 < 4; g4++) p4s[qb][g4] = pd4(qb, g4);
+                    phase2(qb, p4s[qb]);
                 }
             } else if (act) {
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++) {
                     const int tq0 = q0 + qb * 32;
                     if (tq0 >= p.seq || tq0 + 31 < key0) continue;
-                    float4 p4s[4], d4s[4];
+                    float4 p4s[4];
                     if constexpr (!PW)
 #pragma unroll
-                        for (int g4 = 0; g4 < 4; g4++) pd4(qb, g4, p4s[g4], d4s[g4]);
-                    phase2(qb, p4s, d4s);
+                        for (int g4 = 0; g4 < 4; g4++) p4s[g4] = pd4(qb, g4);
+                    phase2(qb, p4s);
                 }
             }
             if constexpr (!PW)

@@ -15,9 +15,11 @@
 //   waves 0, 1 (P waves; keys 0-63 / 64-127 of the tile) hold K^T and the
 //     dV^T accumulators: S = Q K^T, P = exp2(S*scale*log2e - lse*log2e)
 //     (causally masked), P to LDS as bf16 MFMA operands, dV^T += dO^T P;
-//   waves 2, 3 (dS waves; the same keys) hold V^T and the dK^T
-//     accumulators: dP = dO V^T, then with P from LDS dS = P (dP - delta)
-//     and dK^T += Q^T dS.
+//   waves 2, 3 (dS waves; the same keys) hold -V^T and the dK^T
+//     accumulators: the dO (-V^T) products accumulate onto delta, giving
+//     m = delta - dP with no subtraction per element (negating bf16 is
+//     exact), then with P from LDS dS = P (dP - delta) = -P m and
+//     dK^T += Q^T dS.
 // Steps (query head, 64-query tile = query blocks 0 and 1) run in
 // attn_bwd_dkdv_ws_kernel's order and every element's products are summed
 // in its order, so dK, dV and the stored dS are bitwise equal to that
@@ -33,10 +35,11 @@
 //            R2  dV of (t, block 0)     | softmax of (t, block 1, key block 0)
 //            R3  S of (t+1, block 0)    | softmax of (t, block 1, key block 1)
 //            R4  dV of (t, block 1)     | softmax of (t+1, block 0, key block 0)
-//   dS wave: R1  dP of (t, block 0)     | dS of (t-1, block 0)
-//            R2  dK of (t-1, block 0)   | dS of (t-1, block 1, key block 0)
-//            R3  dP of (t, block 1)     | dS of (t-1, block 1, key block 1), dP - delta of (t, block 0)
-//            R4  dK of (t-1, block 1)   | dP - delta of (t, block 1), the stored dS of t-1
+//   dS wave: R1  m of (t, block 0)      | dS of (t-1, block 0)
+//            R2  dK of (t-1, block 0)   | dS of (t-1, block 1, key block 0), stored dS of (t-1, block 0)
+//            R3  m of (t, block 1)      | dS of (t-1, block 1, key block 1), stored dS of (t-1, 1, 0)
+//            R4  dK of (t-1, block 1)   | the last stored dS piece of t-1
+// (stores early in the interval: the barrier's wait covers them).
 // P of step t is in LDS at barrier t; the dS wave uses it in interval t + 1.
 // Diagonal and ragged steps (a few per head) take a plain, unpipelined path.
 //
@@ -95,6 +98,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16, TSZ = L::SIZE;
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NKB = 2;
     constexpr int BPW = NBL / 4;                 // blocks of each tile one wave loads
+    // LDS operands are read this many operands (2*LA MFMA slots) ahead of
+    // their MFMA, so that their latency hides behind the MFMAs in between.
+    constexpr int LA = 3;
     constexpr int NQBUF = 4, NOBUF = 2, NDBUF = 3;  // Q, dO and delta buffers
     static_assert(NBL % 4 == 0 && BM == 64, "tile must split evenly over the four waves");
     __shared__ __attribute__((aligned(16))) bf16_bits sQ[NQBUF * TSZ];
@@ -133,7 +139,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int trow = L::row(4 * (jj >> 2) + hh) + 16 * (G & 1) + 4 * (jj & 3);
     // Stored dS (kDsBlock layout): lane l writes its first eight values to
     // 16-byte slot l ^ hh and the other eight to slot 64 + (l ^ (2 + hh)).
-    const int ds_off0 = (lane ^ hh) * 8, ds_off1 = (64 + (lane ^ (2 + hh))) * 8;
+    // Byte offsets of the lane's two 16-byte pieces in a stored-dS block.
+    const uint32_t ds_off0 = (uint32_t)(lane ^ hh) * 16, ds_off1 = (uint32_t)(64 + (lane ^ (2 + hh))) * 16;
 
     const int n_qt = (p.seq + BM - 1) / BM;
     const int qt_begin = wg_key0 / BM;
@@ -237,9 +244,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     };
     // x[kb] = rows of query block qb of tile A times the wave's K^T / V^T
     // operands (S or dP of the block), unscheduled (masked steps).
-    auto score = [&](const bf16_bits* A, int qb, const bf16x8 (&xf)[NKB][NKD], f32x16 (&x)[NKB]) {
+    auto score = [&](const bf16_bits* A, int qb, const bf16x8 (&xf)[NKB][NKD], f32x16 (&x)[NKB],
+                     const f32x16& init) {
 #pragma unroll
-        for (int kb = 0; kb < NKB; kb++) x[kb] = zero16();
+        for (int kb = 0; kb < NKB; kb++) x[kb] = init;
 #pragma unroll
         for (int kd = 0; kd < NKD; kd++) {
             const bf16x8 a = rd_row(A, qb, kd);
@@ -259,7 +267,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     // K^T (P waves) or V^T (dS waves) operands: key key0 + 32*kb + l32,
     // head dims hh*HALF + kd*8 + [0, 8).
-    auto load_keys = [&](const void* src_, bf16x8 (&xf)[NKB][NKD]) {
+    auto load_keys = [&](const void* src_, bf16x8 (&xf)[NKB][NKD], bool negate) {
+        const uint32_t sgn = negate ? 0x80008000u : 0u;
         const bf16_bits* src = static_cast<const bf16_bits*>(src_) + (long)b * p.kv_bs + (long)g * DP + hh * HALF;
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
@@ -267,10 +276,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const bool ok = kw < p.seq;
             const bf16_bits* xr = src + (long)(ok ? kw : 0) * kvrs;
 #pragma unroll
-            for (int kd = 0; kd < NKD; kd++)
-                xf[kb][kd] =
-                    __builtin_bit_cast(bf16x8, ok ? *reinterpret_cast<const uint4*>(xr + kd * 8) : make_uint4(0, 0, 0, 0));
+            for (int kd = 0; kd < NKD; kd++) {
+                uint4 u = ok ? *reinterpret_cast<const uint4*>(xr + kd * 8) : make_uint4(0, 0, 0, 0);
+                u.x ^= sgn, u.y ^= sgn, u.z ^= sgn, u.w ^= sgn;
+                xf[kb][kd] = __builtin_bit_cast(bf16x8, u);
+            }
         }
+        // Wait for the operands here, with a wait the compiler sees: the
+        // loop's own waits are inline assembly, invisible to its wait-count
+        // tracking, which would otherwise put a full vmcnt(0) wait (on the
+        // tile loads just issued) before the first use in every step.
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     };
     auto zero_acc = [&](f32x16 (&acc)[NDB][NKB]) {
 #pragma unroll
@@ -315,12 +331,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // ------------------------------------------------------------ P waves
     auto run_p = [&]() {
         bf16x8 xf[NKB][NKD];
-        load_keys(p.k, xf);
+        load_keys(p.k, xf, false);
         f32x16 acc[NDB][NKB];  // dV^T, in AGPRs
         zero_acc(acc);
 
         // P of an element: exp2(S*scale*log2e - lse*log2e).
         auto p_elem = [&](float s, float lv) { return __builtin_amdgcn_exp2f(__builtin_fmaf(s, p.sl2, -lv)); };
+        // lse of the lane's 16 rows of query block qb, unscaled.
+        auto lse_raw = [&](const float* Ls, int qb, float (&lv)[16]) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const float4 l = row_vals4(Ls, qb, g4);
+                lv[g4 * 4 + 0] = l.x, lv[g4 * 4 + 1] = l.y, lv[g4 * 4 + 2] = l.z, lv[g4 * 4 + 3] = l.w;
+            }
+        };
         auto lse_part = [&](const float* Ls, int qb, int g4, float (&lv)[16]) {
             const float4 l = row_vals4(Ls, qb, g4);
             lv[g4 * 4 + 0] = l.x * kLog2e;
@@ -345,7 +369,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 f32x16 sc[NKB];
                 bf16x8 pq[NKB][2];
                 float lv[16];
-                score(Qs, qb, xf, sc);
+                score(Qs, qb, xf, sc, zero16());
 #pragma unroll
                 for (int g4 = 0; g4 < 4; g4++) lse_part(sL[qbuf], qb, g4, lv);
 #pragma unroll
@@ -382,7 +406,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // Forms the state of full step x (unscheduled: after a masked step).
         auto prime = [&](int qbuf, PState& o) {
             f32x16 sc[NKB];
-            score(sQ + qbuf * TSZ, 0, xf, sc);
+            score(sQ + qbuf * TSZ, 0, xf, sc, zero16());
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) lse_part(sL[qbuf], 0, g4, o.lv0);
             float pr[16];
@@ -418,29 +442,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 }
             };
             // R1: S of (t, 1) | softmax (t, 0, 1); P (t, 0, 0) published;
-            // lse of block 1; this interval's loads.
-            qr[0] = rd_row(Qs, 1, 0);
-            qr[1] = rd_row(Qs, 1, 1);
+            // lse of block 1 (read here, scaled one element per slot); this
+            // interval's loads.
+#pragma unroll
+            for (int i = 0; i < LA; i++) qr[i] = rd_row(Qs, 1, i);
+            lse_raw(sL[qbuf], 1, lv1);
             publish(pbuf, 0, 0, in.p00);
             CF_FENCE();
 #pragma unroll
             for (int k = 0; k < 2 * NKD; k++) {
                 const int kd = k >> 1, kb = k & 1;
-                if (kb == 0 && kd + 2 < NKD) qr[kd + 2] = rd_row(Qs, 1, kd + 2);
-                if (k < 4) lse_part(sL[qbuf], 1, k, lv1);
-                if (k >= 2 * NKD - 2) tr[k - (2 * NKD - 2)] = rd_tr(Os, 0, k - (2 * NKD - 2));
+                if (kb == 0 && kd + LA < NKD) qr[kd + LA] = rd_row(Qs, 1, kd + LA);
+                lv1[k] *= kLog2e;
+                if (k >= 2 * NKD - LA) tr[k - (2 * NKD - LA)] = rd_tr(Os, 0, k - (2 * NKD - LA));
                 s1[kb] = mfma32(qr[kd], xf[kb][kd], kd == 0 ? zero16() : s1[kb]);
                 sm(k, in.s01, in.lv0, p01, 0, 1, true);
                 if (kb == 0) issue_load(kd, ld);
                 CF_FENCE();
             }
+            // lse of (t+1, 0), raw, for R3.
+            if (EARLY) lse_raw(sL[nqbuf], 0, out.lv0);
             CF_HAZARD_FENCE();
-            // R2: dV of (t, 0) | softmax (t, 1, 0).
+            // R2: dV of (t, 0) | softmax (t, 1, 0); the first Q rows of
+            // (t+1, 0) for R3.
 #pragma unroll
             for (int k = 0; k < 2 * NKD; k++) {
                 const int o = k >> 1, kb = k & 1;
-                if (kb == 0 && o + 2 < 2 * NDB) tr[o + 2] = rd_tr(Os, 0, o + 2);
-                if (EARLY && kb == 0 && o >= 2 * NDB - 2) qr[o - (2 * NDB - 2)] = rd_row(Qn, 0, o - (2 * NDB - 2));
+                if (kb == 0 && o + LA < 2 * NDB) tr[o + LA] = rd_tr(Os, 0, o + LA);
+                if (EARLY && (k & 3) == 1 && (k >> 2) < LA) qr[k >> 2] = rd_row(Qn, 0, k >> 2);
                 mfma_acc(acc[o >> 1][kb], tr[o], kb == 0 ? in.p00[o & 1] : p01[o & 1]);
                 sm(k, s1[0], lv1, p10, 1, 0, true);
                 if (k == 0) issue_load(NKD, ld);
@@ -451,10 +480,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int k = 0; k < 2 * NKD; k++) {
                 const int kd = k >> 1, kb = k & 1;
                 if (EARLY) {
-                    if (kb == 0 && kd + 2 < NKD) qr[kd + 2] = rd_row(Qn, 0, kd + 2);
-                    if (k < 4) lse_part(sL[nqbuf], 0, k, out.lv0);
+                    if (kb == 0 && kd + LA < NKD) qr[kd + LA] = rd_row(Qn, 0, kd + LA);
+                    out.lv0[k] *= kLog2e;
                 }
-                if (k >= 2 * NKD - 2) tr[k - (2 * NKD - 2)] = rd_tr(Os, 1, k - (2 * NKD - 2));
+                if (k >= 2 * NKD - LA) tr[k - (2 * NKD - LA)] = rd_tr(Os, 1, k - (2 * NKD - LA));
                 if (EARLY) {
                     if (kb == 0)
                         sn0 = mfma32(qr[kd], xf[0][kd], kd == 0 ? zero16() : sn0);
@@ -470,7 +499,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int k = 0; k < 2 * NKD; k++) {
                 const int o = k >> 1, kb = k & 1;
-                if (kb == 0 && o + 2 < 2 * NDB) tr[o + 2] = rd_tr(Os, 1, o + 2);
+                if (kb == 0 && o + LA < 2 * NDB) tr[o + LA] = rd_tr(Os, 1, o + LA);
                 mfma_acc(acc[o >> 1][kb], tr[o], kb == 0 ? p10[o & 1] : p11[o & 1]);
                 if (EARLY) sm(k, sn0, out.lv0, out.p00, 0, 0, false);
                 CF_FENCE();
@@ -518,43 +547,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // ----------------------------------------------------------- dS waves
     auto run_ds = [&]() {
         bf16x8 xf[NKB][NKD];
-        load_keys(p.v, xf);
+        load_keys(p.v, xf, true);
         f32x16 acc[NDB][NKB];  // dK^T, in AGPRs
         zero_acc(acc);
 
         // dS of element r of a block: P (the bf16 value the P wave's dV
         // product used; widening is exact) times dP - delta.  w: the block's
         // two published halves as eight words.
-        auto ds_elem = [&](const uint32_t (&w)[8], int r, float dpd) {
+        // dS element r from the P words and m = delta - dP (the negated
+        // product's accumulator): P (dP - delta) = P * -m.
+        auto ds_elem = [&](const uint32_t (&w)[8], int r, float m) {
             const uint32_t word = w[r >> 1];
-            return __uint_as_float((r & 1) ? (word & 0xffff0000u) : (word << 16)) * dpd;
+            return __uint_as_float((r & 1) ? (word & 0xffff0000u) : (word << 16)) * -m;
         };
         auto p_words = [&](int pbuf, int qb, int kb, uint32_t (&w)[8]) {
             const uint4 a = sP[pbuf][pair][qb][kb][0][lane], c = sP[pbuf][pair][qb][kb][1][lane];
             w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = c.x, w[5] = c.y, w[6] = c.z, w[7] = c.w;
         };
-        auto delta16 = [&](int dbuf_, int qb, float (&dl)[16]) {
+        // delta of the lane's 16 rows of query block qb, as an accumulator.
+        auto delta16 = [&](int dbuf_, int qb) {
+            f32x16 dl;
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) {
                 const float4 d = row_vals4(sD[dbuf_], qb, g4);
                 dl[g4 * 4 + 0] = d.x, dl[g4 * 4 + 1] = d.y, dl[g4 * 4 + 2] = d.z, dl[g4 * 4 + 3] = d.w;
             }
+            return dl;
         };
         // One 16-byte piece (qb, kb, half h) of a step's dS (rounded to bf16)
         // to the stored-dS scratch: blocks on or below the causal diagonal
         // only (the layout has no others), non-temporal (the dQ kernel reads
         // each once).
+        // The block index is below 2^32 (the scratch would be 8 TiB), so it
+        // is formed in 32-bit scalar arithmetic and the store addressed as
+        // a scalar base plus the lane's byte offset.
         auto ds_store = [&](Pos x, int qb, int kb, int h, const bf16x8& v, bool check) {
             const int qi = (x.q0 >> 5) + qb, ki = (key0 >> 5) + kb;
             if (check && !(ki <= qi && x.q0 + qb * 32 < p.seq)) return;
-            const long ds_head = ((long)b * p.nh + x.h) * p.ds_ntri;
-            bf16_bits* blk = p.ds + (ds_head + (long)qi * (qi + 1) / 2 + ki) * kDsBlock;
+            const uint32_t blk = __builtin_amdgcn_readfirstlane(
+                ((uint32_t)b * (uint32_t)p.nh + (uint32_t)x.h) * (uint32_t)p.ds_ntri +
+                (uint32_t)(qi * (qi + 1) / 2 + ki));
+            const char* base = reinterpret_cast<const char*>(p.ds) + (size_t)blk * (kDsBlock * sizeof(bf16_bits));
             __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v),
-                                        reinterpret_cast<u32x4*>(blk + (h ? ds_off1 : ds_off0)));
+                                        reinterpret_cast<u32x4*>(const_cast<char*>(base) + (h ? ds_off1 : ds_off0)));
         };
 
-        // dP - delta of the step whose dS comes next, by query block and key
-        // block.  Two copies, for even and odd steps: each iteration reads
+        // delta - dP of the step whose dS comes next, by query block and key
+        // block: the products with the negated V^T operands accumulated onto
+        // delta.  Two copies, for even and odd steps: each iteration reads
         // one and forms the other in place.
         struct DState {
             f32x16 d[2][NKB];
@@ -562,17 +602,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         DState st0, st1;
         // Forms it for the step with dO in buffer obuf (unscheduled).
         auto dp_of = [&](int obuf, int dbuf_, DState& o) {
-            score(sO + obuf * TSZ, 0, xf, o.d[0]);
-            score(sO + obuf * TSZ, 1, xf, o.d[1]);
-            float dl[16];
-#pragma unroll
-            for (int qb = 0; qb < 2; qb++) {
-                delta16(dbuf_, qb, dl);
-#pragma unroll
-                for (int kb = 0; kb < NKB; kb++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) o.d[qb][kb][r] -= dl[r];
-            }
+            score(sO + obuf * TSZ, 0, xf, o.d[0], delta16(dbuf_, 0));
+            score(sO + obuf * TSZ, 1, xf, o.d[1], delta16(dbuf_, 1));
         };
         // dS and dK of step x (unscheduled; its P in buffer pbuf).
         auto ds_dk = [&](Pos x, int qbuf, int pbuf, bool check, const DState& in) {
@@ -608,7 +639,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             const bf16_bits* On = sO + nobuf * TSZ;  // dO of step t + 1
             bf16x8 orow[NKD], tr[2 * NDB];
             uint32_t w[NKB][8];
-            float ds[NKB][16], dl[16];
+            float ds[NKB][16];
             bf16x8 d0[NKB][2], d1[NKB][2];
             // dS element e of (t, qb, kb) per slot, rounded after 7 and 15.
             auto dse = [&](int qb, int kb, int e, bf16x8 (&dd)[NKB][2]) {
@@ -620,8 +651,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 const int sq = i >> 2, skb = (i >> 1) & 1, sh = i & 1;
                 ds_store(x, sq, skb, sh, sq ? d1[skb][sh] : d0[skb][sh], false);
             };
-            orow[0] = rd_row(On, 0, 0);
-            orow[1] = rd_row(On, 0, 1);
+            f32x16 dl = delta16(ndbuf, 0);
+#pragma unroll
+            for (int i = 0; i < LA; i++) orow[i] = rd_row(On, 0, i);
             p_words(pbuf, 0, 0, w[0]);
             p_words(pbuf, 0, 1, w[1]);
             CF_FENCE();
@@ -629,56 +661,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int k = 0; k < 2 * NKD; k++) {
                 const int kd = k >> 1, kb = k & 1;
-                if (kb == 0 && kd + 2 < NKD) orow[kd + 2] = rd_row(On, 0, kd + 2);
-                if (k >= 2 * NKD - 2) tr[k - (2 * NKD - 2)] = rd_tr(Qs, 0, k - (2 * NKD - 2));
-                out.d[0][kb] = mfma32(orow[kd], xf[kb][kd], kd == 0 ? zero16() : out.d[0][kb]);
+                if (kb == 0 && kd + LA < NKD) orow[kd + LA] = rd_row(On, 0, kd + LA);
+                if (k >= 2 * NKD - LA) tr[k - (2 * NKD - LA)] = rd_tr(Qs, 0, k - (2 * NKD - LA));
+                out.d[0][kb] = mfma32(orow[kd], xf[kb][kd], kd == 0 ? dl : out.d[0][kb]);
                 dse(0, 0, k, d0);
                 dse(0, 1, k, d0);
                 if (kb == 0) issue_load(kd, ld);
                 CF_FENCE();
             }
-            // Block 1's P words for R2/R3, and delta of (t+1, 0).
+            // Block 1's P words for R2/R3, and delta of (t+1, 1).
             p_words(pbuf, 1, 0, w[0]);
             p_words(pbuf, 1, 1, w[1]);
-            delta16(ndbuf, 0, dl);
+            dl = delta16(ndbuf, 1);
             CF_HAZARD_FENCE();
             // R2: dK of (t, 0) | dS of (t, 1, 0).
 #pragma unroll
             for (int k = 0; k < 2 * NKD; k++) {
                 const int o = k >> 1, kb = k & 1;
-                if (kb == 0 && o + 2 < 2 * NDB) tr[o + 2] = rd_tr(Qs, 0, o + 2);
-                if (kb == 0 && o >= 2 * NDB - 2) orow[o - (2 * NDB - 2)] = rd_row(On, 1, o - (2 * NDB - 2));
+                if (kb == 0 && o + LA < 2 * NDB) tr[o + LA] = rd_tr(Qs, 0, o + LA);
+                if ((k & 3) == 1 && (k >> 2) < LA) orow[k >> 2] = rd_row(On, 1, k >> 2);
                 mfma_acc(acc[o >> 1][kb], tr[o], d0[kb][o & 1]);
                 dse(1, 0, k, d1);
+                // Stores of (t, 0), early in the interval so that they have
+                // completed by the barrier's wait.
                 if constexpr (WDS) {
                     if ((k & 3) == 2) store_piece(k >> 2);
                 }
                 CF_FENCE();
             }
-            // R3: dP of (t+1, 1) | dS of (t, 1, 1); dP - delta of (t+1, 0).
+            // R3: dP of (t+1, 1) | dS of (t, 1, 1); stores of (t, 1, 0) and
+            // the first half of (t, 1, 1).
 #pragma unroll
             for (int k = 0; k < 2 * NKD; k++) {
                 const int kd = k >> 1, kb = k & 1;
-                if (kb == 0 && kd + 2 < NKD) orow[kd + 2] = rd_row(On, 1, kd + 2);
-                if (k >= 2 * NKD - 2) tr[k - (2 * NKD - 2)] = rd_tr(Qs, 1, k - (2 * NKD - 2));
-                out.d[1][kb] = mfma32(orow[kd], xf[kb][kd], kd == 0 ? zero16() : out.d[1][kb]);
+                if (kb == 0 && kd + LA < NKD) orow[kd + LA] = rd_row(On, 1, kd + LA);
+                if (k >= 2 * NKD - LA) tr[k - (2 * NKD - LA)] = rd_tr(Qs, 1, k - (2 * NKD - LA));
+                out.d[1][kb] = mfma32(orow[kd], xf[kb][kd], kd == 0 ? dl : out.d[1][kb]);
                 dse(1, 1, k, d1);
-                out.d[0][0][k] -= dl[k];
-                out.d[0][1][k] -= dl[k];
+                if constexpr (WDS) {
+                    if (k == 2 || k == 6 || k == 10) store_piece(4 + (k >> 2));
+                }
                 CF_FENCE();
             }
-            delta16(ndbuf, 1, dl);
             CF_HAZARD_FENCE();
-            // R4: dK of (t, 1) | dP - delta of (t+1, 1); the step's dS stores.
+            // R4: dK of (t, 1); the last store of (t, 1, 1).
 #pragma unroll
             for (int k = 0; k < 2 * NKD; k++) {
                 const int o = k >> 1, kb = k & 1;
-                if (kb == 0 && o + 2 < 2 * NDB) tr[o + 2] = rd_tr(Qs, 1, o + 2);
+                if (kb == 0 && o + LA < 2 * NDB) tr[o + LA] = rd_tr(Qs, 1, o + LA);
                 mfma_acc(acc[o >> 1][kb], tr[o], d1[kb][o & 1]);
-                out.d[1][0][k] -= dl[k];
-                out.d[1][1][k] -= dl[k];
                 if constexpr (WDS) {
-                    if ((k & 3) == 2) store_piece(4 + (k >> 2));
+                    if (k == 0) store_piece(7);
                 }
                 CF_FENCE();
             }

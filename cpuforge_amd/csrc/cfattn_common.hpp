@@ -265,32 +265,40 @@ __device__ __forceinline__ int swz_off(int r, int c) {
 // s_waitcnt vmcnt (these loads count there, in issue order) and then
 // barriers.  Used where the compiler's own tracking of several in-flight
 // buffers falls back to waiting for every load.
+//
+// The m0 write the compiler emits for the operand needs one wait state
+// before an LDS-DMA instruction reads it, which the compiler's hazard
+// checks do not see through the asm: hence the s_nop 0 in each.
+//
+// s_waitcnt immediate (gfx9 encoding) for vmcnt(0) alone, for a wait the
+// compiler's own wait-count tracking sees (__builtin_amdgcn_s_waitcnt).
+constexpr int kWaitVmcnt0 = 0x0F70;  // vmcnt 0, expcnt 7, lgkmcnt 15: no wait on the others
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 __device__ __forceinline__ void lds_load16_asm(const void* g, const void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
 }
 // The same with the non-temporal cache policy, for data read exactly once.
 __device__ __forceinline__ void lds_load16_nt_asm(const void* g, const void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
-    asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(m0) : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "{m0}"(m0) : "memory");
 }
 // The same loads addressed as a scalar base plus a 32-bit per-lane byte
 // offset (the saddr form: no 64-bit address arithmetic per lane).
 __device__ __forceinline__ void lds_load16_sv(const void* sbase, uint32_t voff, const void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
-    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
 __device__ __forceinline__ void lds_load4_sv(const void* sbase, uint32_t voff, const void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
-    asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
 // 64 lanes x 4 bytes to 256 consecutive bytes of LDS (one float per lane).
 __device__ __forceinline__ void lds_load4_asm(const void* g, const void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
-    asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "{m0}"(m0) : "memory");
 }
 
 // ------------------------------------------------- blocked bf16 LDS tiles
