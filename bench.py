@@ -16,7 +16,11 @@ Printed: one JSON line with the whole-step throughput (algorithmic TFLOP/s,
 most time (its algorithmic FLOPs per launch / its mean launch time, measured
 with hipEvents on its stream over the timed steps) and a `cpu_baseline`
 object: the oracle's restatement of the reference CPU algorithm timed on a
-bounded sample of the same workload on the host cores.
+bounded sample of the same workload on the host cores.  Beside them:
+`f32`, the same step at the reference's own precision (C2, f32 inputs, fp32
+MFMA; roofline against the fp32 matrix peak); `fused`, the Layer-level step
+of the headline config (q/k prologue + attention forward and backward through
+cfattn_fused_fwd/bwd); and `smollm_train`, the SmolLM-135M LoRA train step.
 """
 from __future__ import annotations
 
@@ -69,7 +73,10 @@ def parse():
     ap.add_argument("--cpu-single-heads", type=int, default=4,
                     help="query heads of sequence 0 in the single-thread CPU sample (0 skips it)")
     ap.add_argument("--no-train", action="store_true", help="skip the SmolLM-135M train tok/s leg")
-    ap.add_argument("--train-steps", type=int, default=3)
+    ap.add_argument("--train-steps", type=int, default=10)
+    ap.add_argument("--no-f32", action="store_true", help="skip the f32 (C2) sub-object")
+    ap.add_argument("--no-fused", action="store_true", help="skip the fused Layer-level sub-object")
+    ap.add_argument("--sub-steps", type=int, default=20, help="timed steps of the f32 and fused sub-objects")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB before timing (calibrates rocprofv3 byte counters)")
     ap.add_argument("--host-slices", action="store_true",
@@ -212,16 +219,27 @@ def host_slices(a, mode):
 
 
 def fused_layer(a, mode):
+    """Prints the JSON line of `fused_timing` for --config/--mode."""
+    r = fused_timing(a.config, mode, a.steps, a.warmup)
+    print(json.dumps({"metric": "Layer attention fwd+bwd (prologue + attention) TFLOP/s, attention FLOPs only",
+                      "value": r["value"], "unit": "TFLOP/s", "ms_per_step": r["ms_per_step"],
+                      "steps": a.steps, "warmup": a.warmup, "dtype": mode, "higher_is_better": True,
+                      "kernels_ms": r["kernels_ms"],
+                      "config": {"workload": WORKLOAD[a.config], "config": a.config, "path": "cfattn_fused_fwd/bwd"}}),
+          flush=True)
+
+
+def fused_timing(cfg, mode, steps, warmup):
     """Times cfattn_fused_fwd + cfattn_fused_bwd: Layer::forward/backward's
     attention part (crates/model/src/layer.rs:104-121, 183-206): pre-RoPE
     q/k in f32 -> [q/k RMSNorm] -> RoPE -> attention, and back to dq_pre,
-    dk_pre, dv (and the norm-gain gradients).  Prints its own JSON line, with
-    the time of each kernel."""
+    dk_pre, dv (and the norm-gain gradients).  Returns ms per step, the
+    attention-FLOP TFLOP/s and the time of each kernel."""
     import torch
 
     import cpuforge_amd as cf
     from cpuforge_amd import device as dev
-    B, S, Hq, Hk, D, theta, scaling, qk_norm = CONFIGS[a.config]
+    B, S, Hq, Hk, D, theta, scaling, qk_norm = CONFIGS[cfg]
     ctx = cf.Context(0)
     torch.manual_seed(1234)
     dt = torch.bfloat16 if mode == "bf16" else torch.float32
@@ -242,24 +260,22 @@ def fused_layer(a, mode):
         o, lse, q, k, qr, kr = dev.fused_fwd(q_pre, k_pre, v, pr, ctx=ctx)
         dev.fused_bwd(d_o, q_pre, k_pre, q, k, v, o, lse, qr, kr, pr, dq_pre, dk_pre, dv, ctx=ctx)
 
-    for _ in range(a.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     ctx.profile_enable(True)
     t0 = time.perf_counter()
-    for _ in range(a.steps):
+    for _ in range(steps):
         step()
     torch.cuda.synchronize()
-    per = (time.perf_counter() - t0) / a.steps
+    per = (time.perf_counter() - t0) / steps
     kernels = {n: round(ms / max(1, c), 4) for n, (ms, c) in ctx.profile_read().items() if c}
     ctx.close()
+    del q_pre, k_pre, v, d_o, dq_pre, dk_pre, dv, pr
+    torch.cuda.empty_cache()
     flops = 7.0 * B * Hq * D * S * (S + 1)
-    print(json.dumps({"metric": "Layer attention fwd+bwd (prologue + attention) TFLOP/s, attention FLOPs only",
-                      "value": round(flops / per / 1e12, 3), "unit": "TFLOP/s", "ms_per_step": round(per * 1e3, 3),
-                      "steps": a.steps, "warmup": a.warmup, "dtype": mode, "higher_is_better": True,
-                      "kernels_ms": kernels,
-                      "config": {"workload": WORKLOAD[a.config], "config": a.config, "path": "cfattn_fused_fwd/bwd"}}),
-          flush=True)
+    return {"value": round(flops / per / 1e12, 3), "unit": "TFLOP/s", "ms_per_step": round(per * 1e3, 4),
+            "kernels_ms": kernels}
 
 
 def layer_ops(a):
@@ -515,37 +531,17 @@ def io_formats(a):
                       "io": out, "cpu_baseline": cpu or None}), flush=True)
 
 
-def main():
-    a = parse()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if a.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU: the attention op runs on a single MI355X here and this build has no "
-              f"multi-GPU path (asked for --gpus {a.gpus}, WORLD_SIZE={world}).", file=sys.stderr)
-        sys.exit(2)
-    mode = a.mode or ("f32" if a.config == "C1" else "bf16")
-    B, S, Hq, Hk, D, theta, scaling, qk_norm = CONFIGS[a.config]
-    if a.host_slices:
-        host_slices(a, mode)
-        return
-    if a.fused:
-        fused_layer(a, mode)
-        return
-    if a.ops:
-        layer_ops(a)
-        return
-    if a.io:
-        io_formats(a)
-        return
-
+def attn_timing(cfg, mode, steps, warmup, ctx, traffic_file, copy_probe):
+    """Times `steps` attention steps (cfattn_fwd then cfattn_bwd on
+    device-resident tensors) of config `cfg` after `warmup` untimed ones.
+    Returns the step time (the larger of the hipEvent span and the host wall
+    clock, over the steps), the whole-step TFLOP/s and the roofline of the
+    kernel that takes the most time."""
     import torch
 
     import cpuforge_amd as cf
     from cpuforge_amd import device as dev
-
-    if not torch.cuda.is_available():
-        print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
-        sys.exit(1)
-    ctx = cf.Context(0)
+    B, S, Hq, Hk, D, theta, scaling, qk_norm = CONFIGS[cfg]
     torch.manual_seed(1234)
     dt = torch.bfloat16 if mode == "bf16" else torch.float32
     # Synthetic pre-RoPE q/k, v and upstream gradient, N(0,1).
@@ -572,17 +568,17 @@ def main():
         dev.fwd(q, k, v, o, lse, ctx=ctx)
         dev.bwd(d_o, q, k, v, o, lse, dq, dk, dv, ctx=ctx)
 
-    if a.copy_probe:
-        src = torch.empty(a.copy_probe << 18, device="cuda", dtype=torch.float32).fill_(1.0)
+    if copy_probe:
+        src = torch.empty(copy_probe << 18, device="cuda", dtype=torch.float32).fill_(1.0)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    for _ in range(a.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    print(f"bench: {a.config} {mode} warmup done ({a.warmup} steps)", file=sys.stderr, flush=True)
+    print(f"bench: {cfg} {mode} warmup done ({warmup} steps)", file=sys.stderr, flush=True)
 
     ctx.profile_enable(True)
     stream = torch.cuda.current_stream()
@@ -591,7 +587,7 @@ def main():
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     ev0.record(stream)
-    for _ in range(a.steps):
+    for _ in range(steps):
         step()
     ev1.record(stream)
     torch.cuda.synchronize()
@@ -599,10 +595,10 @@ def main():
     prof = ctx.profile_read()
     ctx.profile_enable(False)
     gpu_ms = ev0.elapsed_time(ev1)
-    ms_per_step = max(gpu_ms, wall * 1e3) / a.steps
+    ms_per_step = max(gpu_ms, wall * 1e3) / steps
     flops = 7.0 * B * Hq * D * S * (S + 1)
     tflops = flops / (ms_per_step * 1e-3) / 1e12
-    print(f"bench: timed {a.steps} steps, {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
+    print(f"bench: {cfg} {mode} timed {steps} steps, {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
 
     kernels = {n: (t / c if c else 0.0, c) for n, (t, c) in prof.items() if c}
     dom = max((n for n in kernels if n in ALGO_UNITS), key=lambda n: kernels[n][0] * kernels[n][1])
@@ -610,17 +606,56 @@ def main():
     dom_flops = ALGO_UNITS[dom] * B * Hq * D * S * (S + 1)
     achieved = dom_flops / (dom_ms * 1e-3) / 1e12
     peak = PEAK_TFLOPS[mode]
-    tpath = a.traffic_file or os.path.join(ROOT, "profiles", f"hbm_traffic_{a.config}_{mode}.md")
-    traffic = read_traffic(tpath, dom, f"{a.config}-{mode}")
+    tpath = traffic_file or os.path.join(ROOT, "profiles", f"hbm_traffic_{cfg}_{mode}.md")
+    traffic = read_traffic(tpath, dom, f"{cfg}-{mode}")
+    del q, k, v, d_o, o, lse, dq, dk, dv, pr
+    torch.cuda.empty_cache()
+    return {"value": round(tflops, 3), "ms_per_step": round(ms_per_step, 4),
+            "pct_peak": round(100.0 * tflops / peak, 2),
+            "kernels_ms": {n: round(m, 4) for n, (m, _) in kernels.items()},
+            "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 3), "peak": peak,
+                         "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic}}
 
+
+def main():
+    a = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the attention op runs on a single MI355X here and this build has no "
+              f"multi-GPU path (asked for --gpus {a.gpus}, WORLD_SIZE={world}).", file=sys.stderr)
+        sys.exit(2)
+    mode = a.mode or ("f32" if a.config == "C1" else "bf16")
+    B, S, Hq, Hk, D, theta, scaling, qk_norm = CONFIGS[a.config]
+    if a.host_slices:
+        host_slices(a, mode)
+        return
+    if a.fused:
+        fused_layer(a, mode)
+        return
+    if a.ops:
+        layer_ops(a)
+        return
+    if a.io:
+        io_formats(a)
+        return
+
+    import torch
+
+    import cpuforge_amd as cf
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
+        sys.exit(1)
+    ctx = cf.Context(0)
+    r = attn_timing(a.config, mode, a.steps, a.warmup, ctx, a.traffic_file, a.copy_probe)
     out = {
         "metric": "attention fwd+bwd TFLOP/s + % MFMA peak at 1 MI355X; SmolLM-135M train tok/s",
-        "value": round(tflops, 3),
+        "value": r["value"],
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -628,12 +663,29 @@ def main():
         "data": "synthetic (torch.randn N(0,1), RoPE prologue applied before timing)",
         "config": {"workload": WORKLOAD[a.config], "config": a.config, "batch": B, "seq": S, "n_heads": Hq,
                    "n_kv": Hk, "head_dim": D, "mode": mode, "causal": True},
-        "pct_peak": round(100.0 * tflops / peak, 2),
-        "kernels_ms": {n: round(m, 4) for n, (m, _) in kernels.items()},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 3), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic},
+        "pct_peak": r["pct_peak"],
+        "kernels_ms": r["kernels_ms"],
+        "roofline": r["roofline"],
     }
-    del q, k, v, d_o, o, lse, dq, dk, dv
+    if not a.no_f32:
+        # The reference's own precision: C2 (SmolLM-135M training batch) with
+        # f32 inputs through the fp32 MFMA kernels.
+        print("bench: C2 f32 ...", file=sys.stderr, flush=True)
+        f = attn_timing("C2", "f32", a.sub_steps, 3, ctx, None, 0)
+        out["f32"] = {"config": "C2", "workload": WORKLOAD["C2"], "dtype": "f32", "value": f["value"],
+                      "unit": "TFLOP/s", "ms_per_step": f["ms_per_step"], "steps": a.sub_steps,
+                      "pct_peak": f["pct_peak"], "kernels_ms": f["kernels_ms"], "roofline": f["roofline"]}
+    if not a.no_fused:
+        # The Layer-level step of the same config: the q/k prologue (RoPE,
+        # and the Qwen3 norm where the config has it) forward and backward
+        # around the attention.
+        print(f"bench: {a.config} fused layer ...", file=sys.stderr, flush=True)
+        fz = fused_timing(a.config, mode, a.sub_steps, 3)
+        out["fused"] = {"config": a.config, "dtype": mode, "path": "cfattn_fused_fwd/bwd",
+                        "value": fz["value"], "unit": "TFLOP/s (attention FLOPs only)",
+                        "ms_per_step": fz["ms_per_step"], "steps": a.sub_steps,
+                        "over_attention_ms": round(fz["ms_per_step"] - r["ms_per_step"], 4),
+                        "kernels_ms": fz["kernels_ms"]}
     if not a.no_train:
         # SmolLM-135M LoRA r=16 train step (cmd_bench.rs:52-99), seq 512, batch 8,
         # f32 like the reference, attention through the fused GPU path.

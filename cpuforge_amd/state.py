@@ -132,13 +132,33 @@ def load_state(path, model, opt):
 
 
 def json_f64(x: float) -> str:
-    """serde_json's text of an f64: shortest round-trip digits, ".0" on
-    integral values, exponent as "1e-7" / "1e16"; non-finite values are
-    null."""
+    """serde_json's text of an f64 (its ryu formatter): the shortest
+    round-trip digits d_1..d_n with the decimal point after kk digits, then
+      integral with kk <= 16       -> digits, zeros, ".0"   (1e15 -> "1000000000000000.0")
+      0 < kk <= 16                 -> "123.456"
+      -5 < kk <= 0                 -> "0.00005"
+      otherwise                    -> "1e-7", "1.5e16";
+    non-finite values are null."""
     if not math.isfinite(x):
         return "null"
     r = repr(float(x))
-    if "e" in r:
-        mant, exp = r.split("e")
-        return f"{mant}e{int(exp)}"
-    return r
+    sign = "-" if r.startswith("-") else ""
+    r = r.lstrip("-")
+    mant, exp = (r.split("e") + ["0"])[:2]
+    ip, fp = (mant.split(".") + [""])[:2]
+    full = ip + fp
+    z = len(full) - len(full.lstrip("0"))
+    digits = full[z:].rstrip("0")
+    if not digits:
+        return sign + "0.0"
+    kk = len(ip) - z + int(exp)  # value = 0.digits * 10**kk
+    n = len(digits)
+    if kk - n >= 0 and kk <= 16:
+        return sign + digits + "0" * (kk - n) + ".0"
+    if 0 < kk <= 16:
+        return sign + digits[:kk] + "." + digits[kk:]
+    if -5 < kk <= 0:
+        return sign + "0." + "0" * (-kk) + digits
+    if n == 1:
+        return f"{sign}{digits}e{kk - 1}"
+    return f"{sign}{digits[0]}.{digits[1:]}e{kk - 1}"

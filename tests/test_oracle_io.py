@@ -237,6 +237,21 @@ def test_json_f64_matches_serde_json_text():
     assert state.json_f64(float(np.float32(0.1))) == "0.10000000149011612"
     assert state.json_f64(1e-7) == "1e-7"
     assert state.json_f64(float("nan")) == "null"
+    # ryu keeps the decimal form down to 1e-5 (Python's repr leaves it at 1e-4)
+    assert state.json_f64(5e-5) == "0.00005"
+    assert state.json_f64(1.5e-5) == "0.000015"
+    assert state.json_f64(1e-5) == "0.00001"
+    assert state.json_f64(1e-6) == "1e-6"
+    assert state.json_f64(1.5e-6) == "1.5e-6"
+    assert state.json_f64(0.0001) == "0.0001"
+    assert state.json_f64(1e15) == "1000000000000000.0"
+    assert state.json_f64(1e16) == "1e16"
+    assert state.json_f64(1.5e16) == "1.5e16"
+    assert state.json_f64(123456.789) == "123456.789"
+    assert state.json_f64(-2.5) == "-2.5"
+    assert state.json_f64(-0.0) == "-0.0"
+    assert state.json_f64(1.7976931348623157e308) == "1.7976931348623157e308"
+    assert state.json_f64(5e-324) == "5e-324"
 
 
 def test_peft_config_text_is_serde_pretty_with_sorted_keys():
