@@ -620,12 +620,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
 
     if (!wave_active || !row_ok) return;
-    float* dqrow = p.dq + qoff;
 #pragma unroll
-    for (int db = 0; db < NDB; db++) {
-        dqt[db] *= p.scale;  // dS was accumulated without the softmax scale
-        add_row_block(dqrow, dqt[db], db * 32, hh, DP, true);
-    }
+    for (int db = 0; db < NDB; db++) dqt[db] *= p.scale;  // dS was accumulated without the softmax scale
+    write_grad_row<NDB>(p.dq + qoff, dqt, hh, tq, p);
 }
 
 // dQ from the stored dS: dQ^T += K^T dS^T over the key blocks at or before
@@ -805,12 +802,9 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
     }
 
     if (!row_ok) return;
-    float* dqrow = p.dq + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
 #pragma unroll
-    for (int db = 0; db < NDB; db++) {
-        dqt[db] *= p.scale;  // dS was stored without the softmax scale
-        add_row_block(dqrow, dqt[db], db * 32, hh, DP, true);
-    }
+    for (int db = 0; db < NDB; db++) dqt[db] *= p.scale;  // dS was stored without the softmax scale
+    write_grad_row<NDB>(p.dq + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP, dqt, hh, tq, p);
 }
 
 // dK/dV with two specialised waves per 32-key slice: eight waves, 128 keys per
@@ -1201,10 +1195,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
         if (!wave_active || kw >= p.seq) return;
         float* row = (PW ? p.dv : p.dk) + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
+        if constexpr (PW) {
 #pragma unroll
-        for (int db = 0; db < NDB; db++) {
-            if constexpr (!PW) acc[db] *= p.scale;  // dS was accumulated without the softmax scale
-            add_row_block(row, acc[db], db * 32, hh, DP, true);
+            for (int db = 0; db < NDB; db++) add_row_block(row, acc[db], db * 32, hh, DP, true);
+        } else {
+#pragma unroll
+            for (int db = 0; db < NDB; db++) acc[db] *= p.scale;  // dS was accumulated without the softmax scale
+            write_grad_row<NDB>(row, acc, hh, kw, p);
         }
     };
 
@@ -1258,10 +1255,28 @@ size_t attn_bwd_ds_bytes(Dtype dt, const Dims& d) {
     return (size_t)d.batch * d.nh * (nqb * (nqb + 1) / 2) * kDsBlock * sizeof(bf16_bits);
 }
 
+// The fast bf16 kernels' condition (launch_attn_bwd below).
+static bool fast_bf16_applies(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
+                              const float* dq, const float* dk, const float* dv, const Tuning& tu) {
+    const uintptr_t al = 16;
+    const bool vec_ok = d.hd % 8 == 0 && (uintptr_t)q % al == 0 && (uintptr_t)k % al == 0 &&
+                        (uintptr_t)v % al == 0 && (uintptr_t)d_o % al == 0;
+    const bool g_vec_ok = d.hd % 4 == 0 && (uintptr_t)dq % al == 0 && (uintptr_t)dk % al == 0 &&
+                          (uintptr_t)dv % al == 0;
+    return dt == kBF16 && vec_ok && g_vec_ok && (d.hd == 64 || d.hd == 128) && tu.bwd_kv_waves == 0;
+}
+
+bool attn_bwd_epilogue_applies(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k,
+                               const void* v, const float* dq, const float* dk, const float* dv, const Tuning& tu) {
+    return fast_bf16_applies(dt, d, d_o, q, k, v, dq, dk, dv, tu);
+}
+
 hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
                            const float* o, const float* lse, float* delta, float* dq, float* dk, float* dv,
-                           hipStream_t st, const Tuning& tu, void* ds, size_t ds_bytes) {
+                           hipStream_t st, const Tuning& tu, void* ds, size_t ds_bytes, const BwdEpilogue* epi) {
     if (d.batch == 0 || d.seq == 0 || d.nh == 0) return hipSuccess;
+    const bool fast = fast_bf16_applies(dt, d, d_o, q, k, v, dq, dk, dv, tu);
+    if (epi && epi->mode != kEpiAdd && (!fast || !epi->cos || !epi->sin)) return hipErrorInvalidValue;
     BwdParams p{};
     p.d_o = d_o;
     p.q = q;
@@ -1301,7 +1316,13 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
                ((uintptr_t)v % al == 0) && ((uintptr_t)d_o % al == 0);
     p.g_vec_ok = (d.hd % 4 == 0) && ((uintptr_t)dq % al == 0) && ((uintptr_t)dk % al == 0) && ((uintptr_t)dv % al == 0);
     p.xcd = tu.xcd_remap;
-    if (dt == kBF16 && p.vec_ok && p.g_vec_ok && (d.hd == 64 || d.hd == 128) && tu.bwd_kv_waves == 0) {
+    if (epi) {
+        p.epi = epi->mode;
+        p.rope_cos = epi->cos;
+        p.rope_sin = epi->sin;
+        p.rope_pos0 = epi->pos0;
+    }
+    if (fast) {
         // Fast paths: the dQ kernel runs kDqWaves waves per workgroup, dK/dV eight.
         p.hpw = p.group % 4 == 0 ? 4 : p.group % 2 == 0 ? 2 : 1;
         p.tpw = kDqWaves / p.hpw;

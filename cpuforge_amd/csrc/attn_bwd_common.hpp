@@ -2,6 +2,7 @@
 // attn_dkdv.hip): gradient row accumulation and the stored-dS block layout.
 #pragma once
 #include "cfattn_common.hpp"
+#include "attn_params.hpp"
 
 namespace cfattn {
 
@@ -24,6 +25,59 @@ __device__ __forceinline__ void add_row_block(float* row, const f32x16& acc, int
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 if (d0 + i < hd) row[d0 + i] += acc[rq * 4 + i];
+        }
+    }
+}
+
+// One lane's part of a gradient row held as NDB transposed accumulator blocks
+// (block db: head dims db*32 + 8*rq + 4*hh + [0, 4) in acc[db][4*rq + i]),
+// written per the epilogue mode (p.epi, EpilogueMode): added, or unrotated
+// (inverse rotate-half RoPE with the cos/sin row of position
+// p.rope_pos0 + t) and then added or stored.  Rotate-half pairs head dims j
+// and j + DP/2, which sit in blocks db and db + NDB/2 of the same lane, so the
+// rotation is lane-local.  The unrotation repeats the prologue backward's
+// expressions (s = -sin; lo' = lo c - hi s, hi' = hi c + lo s), uncontracted,
+// so both paths give the same bits.
+template <int NDB>
+__device__ __forceinline__ void write_grad_row(float* row, const f32x16 (&acc)[NDB], int hh, int t,
+                                               const BwdParams& p) {
+#pragma clang fp contract(off)
+    constexpr int DP = NDB * 32, HALF = DP / 2;
+    if (p.epi == kEpiAdd) {
+#pragma unroll
+        for (int db = 0; db < NDB; db++) add_row_block(row, acc[db], db * 32, hh, DP, true);
+        return;
+    }
+    const float* cs = p.rope_cos + (long)(p.rope_pos0 + t) * HALF;
+    const float* sn = p.rope_sin + (long)(p.rope_pos0 + t) * HALF;
+#pragma unroll
+    for (int db = 0; db < NDB / 2; db++) {
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            const int d0 = db * 32 + rq * 8 + hh * 4;
+            const float4 c4 = *reinterpret_cast<const float4*>(cs + d0);
+            const float4 s4 = *reinterpret_cast<const float4*>(sn + d0);
+            const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+            float lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float g1 = acc[db][rq * 4 + i], g2 = acc[db + NDB / 2][rq * 4 + i];
+                const float s = -1.0f * sv[i];
+                lo[i] = g1 * c[i] - g2 * s;
+                hi[i] = g2 * c[i] + g1 * s;
+            }
+            float4* r1 = reinterpret_cast<float4*>(row + d0);
+            float4* r2 = reinterpret_cast<float4*>(row + d0 + HALF);
+            if (p.epi == kEpiUnrotAdd) {
+                float4 a = *r1, b = *r2;
+                a.x += lo[0], a.y += lo[1], a.z += lo[2], a.w += lo[3];
+                b.x += hi[0], b.y += hi[1], b.z += hi[2], b.w += hi[3];
+                *r1 = a;
+                *r2 = b;
+            } else {
+                *r1 = make_float4(lo[0], lo[1], lo[2], lo[3]);
+                *r2 = make_float4(hi[0], hi[1], hi[2], hi[3]);
+            }
         }
     }
 }

@@ -308,17 +308,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                      : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[1][0]), "+a"(acc[1][1]), "+a"(acc[2][0]),
                        "+a"(acc[2][1]), "+a"(acc[3][0]), "+a"(acc[3][1]));
     };
-    auto store_rows = [&](float* dst, f32x16 (&acc)[NDB][NKB], bool scale) {
+    // dV rows are added; dK rows (scaled: dS was accumulated without the
+    // softmax scale) go through the epilogue mode.
+    auto store_rows = [&](float* dst, f32x16 (&acc)[NDB][NKB], bool dk_rows) {
         if (!pair_live) return;
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
             const int kw = key0 + kb * 32 + l32;
             if (kw >= p.seq) continue;
             float* row = dst + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
+            if (dk_rows) {
+                f32x16 r[NDB];
 #pragma unroll
-            for (int db = 0; db < NDB; db++) {
-                if (scale) acc[db][kb] *= p.scale;  // dS was accumulated without the softmax scale
-                add_row_block(row, acc[db][kb], db * 32, hh, DP, true);
+                for (int db = 0; db < NDB; db++) r[db] = acc[db][kb] * p.scale;
+                write_grad_row<NDB>(row, r, hh, kw, p);
+            } else {
+#pragma unroll
+                for (int db = 0; db < NDB; db++) add_row_block(row, acc[db][kb], db * 32, hh, DP, true);
             }
         }
     };

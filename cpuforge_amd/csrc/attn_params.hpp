@@ -60,6 +60,11 @@ struct BwdParams {
     int ksplit, units_q;
     long part_rows;
     float* qpart;
+    // Epilogue of the fast bf16 kernels' dQ and dK rows (BwdEpilogue).
+    int epi;
+    const float* rope_cos;
+    const float* rope_sin;
+    int rope_pos0;
 };
 
 // fp32 fast path (attn_f32.hip): head_dim 64 or 128, 16-byte aligned rows.

@@ -360,7 +360,8 @@ int cfattn_fwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const voi
 }
 
 static int cfattn_bwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const void* d_o, const void* q, const void* k,
-               const void* v, const float* o, const float* lse, float* dq, float* dk, float* dv, void* stream) {
+               const void* v, const float* o, const float* lse, float* dq, float* dk, float* dv, void* stream,
+               const cfattn::BwdEpilogue* epi = nullptr) {
     CF_TRY(check_dtype(c, dtype));
     if (batch == 0 || s.seq == 0) return CFATTN_OK;
     CF_TRY(check_shape(c, s));
@@ -374,7 +375,7 @@ static int cfattn_bwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dt
     size_t ds_bytes = 0;
     void* ds = ds_scratch(c, (Dtype)dtype, dims_of(s, batch), &ds_bytes);
     CF_HIP(c, cfattn::launch_attn_bwd((Dtype)dtype, dims_of(s, batch), d_o, q, k, v, o, lse, delta, dq, dk, dv,
-                                      pick_stream(c, stream), c->tuning(), ds, ds_bytes),
+                                      pick_stream(c, stream), c->tuning(), ds, ds_bytes, epi),
            "attention backward launch");
     return CFATTN_OK;
 }
@@ -449,7 +450,7 @@ int cfattn_prologue_fwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, 
 static int cfattn_prologue_bwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, const cfattn_prologue* pr, const float* dq,
                         const float* dk, const float* q_pre, const float* k_pre, const float* q_rstd,
                         const float* k_rstd, float* dq_pre, float* dk_pre, float* dq_norm, float* dk_norm,
-                        void* stream) {
+                        void* stream, bool unrotated = false) {
     if (batch == 0 || s.seq == 0) return CFATTN_OK;
     CF_TRY(check_shape(c, s));
     CF_TRY(check_prologue(c, s, pr));
@@ -465,7 +466,7 @@ static int cfattn_prologue_bwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batc
         if (!partial) return rc;
     }
     CF_HIP(c, cfattn::launch_prologue_bwd(d, to_prologue(pr), dq, dk, q_pre, k_pre, q_rstd, k_rstd, dq_pre, dk_pre,
-                                          dq_norm, dk_norm, partial, pick_stream(c, stream), c->timer),
+                                          dq_norm, dk_norm, partial, pick_stream(c, stream), c->timer, unrotated),
            "prologue backward launch");
     return CFATTN_OK;
 }
@@ -504,6 +505,31 @@ int cfattn_fused_bwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, con
     DeviceGuard dg(c->device);
     int rc = CFATTN_OK;
     const size_t nq = batch * s.seq * s.n_heads * s.head_dim, nk = batch * s.seq * s.n_kv * s.head_dim;
+    if (!d_o || !q || !k || !v || !dq_pre || !dk_pre || !dv) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (cfattn::attn_bwd_epilogue_applies((Dtype)dtype, dims_of(s, batch), d_o, q, k, v, dq_pre, dk_pre, dv,
+                                          c->tuning())) {
+        // The fast kernels unrotate their dQ and dK rows themselves
+        // (layer.rs:191-192): without the norm they add them into
+        // dq_pre/dk_pre directly; with it they store the unrotated
+        // gradients once, and the norm backward alone follows.
+        const cfattn::Prologue P = to_prologue(pr);
+        cfattn::BwdEpilogue epi;
+        epi.cos = P.cos;
+        epi.sin = P.sin;
+        epi.pos0 = P.pos0;
+        if (!pr->q_norm) {
+            epi.mode = cfattn::kEpiUnrotAdd;
+            return cfattn_bwd_locked(c, s, batch, dtype, d_o, q, k, v, o, lse, dq_pre, dk_pre, dv, stream, &epi);
+        }
+        epi.mode = cfattn::kEpiUnrotStore;
+        float* dy_q = static_cast<float*>(slot(c, cfattn_ctx::DQROT, nq * 4, &rc));
+        if (!dy_q) return rc;
+        float* dy_k = static_cast<float*>(slot(c, cfattn_ctx::DKROT, nk * 4, &rc));
+        if (!dy_k) return rc;
+        CF_TRY(cfattn_bwd_locked(c, s, batch, dtype, d_o, q, k, v, o, lse, dy_q, dy_k, dv, stream, &epi));
+        return cfattn_prologue_bwd_locked(c, s, batch, pr, dy_q, dy_k, q_pre, k_pre, q_rstd, k_rstd, dq_pre, dk_pre,
+                                          dq_norm, dk_norm, stream, /*unrotated=*/true);
+    }
     float* dq_rot = static_cast<float*>(slot(c, cfattn_ctx::DQROT, nq * 4, &rc));
     if (!dq_rot) return rc;
     float* dk_rot = static_cast<float*>(slot(c, cfattn_ctx::DKROT, nk * 4, &rc));

@@ -85,12 +85,35 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
 // recomputes S and dP.  Both paths give the same result up to bf16
 // rounding of dS, which both apply.
 size_t attn_bwd_ds_bytes(Dtype dt, const Dims& d);
+// How the fast bf16 kernels write the dQ and dK rows (dV rows are always
+// added).  The inverse-RoPE modes fold the prologue backward's rotation
+// (RopeCache::apply with inverse = true, rope.rs:71-89) into the kernels:
+// row t of a sequence is unrotated with cos/sin row pos0 + t of the
+// [max_pos][head_dim/2] tables, elementwise as the prologue backward does.
+enum EpilogueMode {
+    kEpiAdd = 0,          // dq/dk += rows
+    kEpiUnrotAdd = 1,     // dq/dk += inverse-RoPE(rows)
+    kEpiUnrotStore = 2    // dq/dk  = inverse-RoPE(rows), every row written once
+};
+struct BwdEpilogue {
+    int mode = kEpiAdd;
+    const float* cos = nullptr;
+    const float* sin = nullptr;
+    int pos0 = 0;
+};
+// True when launch_attn_bwd takes the fast bf16 kernels for these operands,
+// the only ones that honour a BwdEpilogue other than kEpiAdd.
+bool attn_bwd_epilogue_applies(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k,
+                               const void* v, const float* dq, const float* dk, const float* dv, const Tuning& tu);
 // With f32 inputs the same scratch (when large enough) holds the per-head
 // dK/dV contributions of the fp32 fast path (attn_f32.hip), which
 // attn_bwd_ds_bytes reports for kF32.
+// A non-default `epi` needs attn_bwd_epilogue_applies (hipErrorInvalidValue
+// otherwise).
 hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
                            const float* o, const float* lse, float* delta, float* dq, float* dk, float* dv,
-                           hipStream_t st, const Tuning& tu, void* ds = nullptr, size_t ds_bytes = 0);
+                           hipStream_t st, const Tuning& tu, void* ds = nullptr, size_t ds_bytes = 0,
+                           const BwdEpilogue* epi = nullptr);
 
 // Attention prologue: optional per-head RMSNorm of q_pre/k_pre (when qw/kw
 // are non-null) followed by rotate-half RoPE at positions pos0+t, written in
@@ -112,10 +135,12 @@ hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, cons
 // backward.  dq_pre/dk_pre and dqw/dkw are accumulated.  `partial` is
 // scratch of prologue_bwd_scratch_floats(d) floats (unused without norm).
 size_t prologue_bwd_scratch_floats(const Dims& d);
+// With `unrotated`, dq/dk already hold the inverse-RoPE'd gradients (a
+// kEpiUnrotStore backward) and only the norm backward runs (pr.qw/kw set).
 hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* dq, const float* dk,
                                const float* q_pre, const float* k_pre, const float* q_rstd, const float* k_rstd,
                                float* dq_pre, float* dk_pre, float* dqw, float* dkw, float* partial, hipStream_t st,
-                               KernelTimer* timer = nullptr);
+                               KernelTimer* timer = nullptr, bool unrotated = false);
 
 // Elementwise helpers.
 hipError_t launch_f32_to_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t st);

@@ -180,6 +180,7 @@ struct ProBwdParams {
     long rows_q, rows_k;
     int chunk_rows, n_chunks_q, n_chunks_k;
     int srows;  // rows per block of the staged kernel
+    int unrot;  // 0: dq/dk are already unrotated (the backward's kEpiUnrotStore epilogue)
 };
 
 // Inverse rotation of element i of a gradient row (sine negated, as
@@ -208,17 +209,18 @@ __global__ __launch_bounds__(256) void prologue_bwd_rows_kernel(const ProBwdPara
     const float* w = isq ? p.qw : p.kw;
     const float* cs = p.cos + (long)(p.pos0 + t) * p.half;
     const float* sn = p.sin + (long)(p.pos0 + t) * p.half;
+    auto dyv = [&](int i) { return p.unrot ? unrotate(g, cs, sn, i, p.half) : g[i]; };
     if (!w) {
-        for (int i = 0; i < p.hd; i++) dx[i] += unrotate(g, cs, sn, i, p.half);
+        for (int i = 0; i < p.hd; i++) dx[i] += dyv(i);
         return;
     }
     const float* x = (isq ? p.q_pre : p.k_pre) + r * p.hd;
     const float inv = (isq ? p.q_rstd : p.k_rstd)[r];
     float dot = 0.0f;
-    for (int i = 0; i < p.hd; i++) dot += unrotate(g, cs, sn, i, p.half) * w[i] * x[i] * inv;
+    for (int i = 0; i < p.hd; i++) dot += dyv(i) * w[i] * x[i] * inv;
     const float mean = dot / (float)p.hd;
     for (int i = 0; i < p.hd; i++) {
-        const float dy = unrotate(g, cs, sn, i, p.half);
+        const float dy = dyv(i);
         const float xhat = x[i] * inv;
         dx[i] += inv * (dy * w[i] - xhat * mean);
     }
@@ -257,8 +259,13 @@ __global__ __launch_bounds__(256) void prologue_bwd_rows_staged_kernel(const Pro
         const float* cs = p.cos + (long)(p.pos0 + t) * half;
         const float* sn = p.sin + (long)(p.pos0 + t) * half;
         const float* gr = g + (long)row * D;
-        dy1 = unrotate(gr, cs, sn, i, half);
-        dy2 = unrotate(gr, cs, sn, i + half, half);
+        if (p.unrot) {
+            dy1 = unrotate(gr, cs, sn, i, half);
+            dy2 = unrotate(gr, cs, sn, i + half, half);
+        } else {
+            dy1 = gr[i];
+            dy2 = gr[i + half];
+        }
     };
     if (!w) {
         for (int j = tid; j < nr * half; j += 256) {
@@ -327,7 +334,7 @@ __global__ __launch_bounds__(256) void prologue_bwd_dw_partial_kernel(const ProB
         const int t = (int)((r / heads) % p.seq);
         const float* cs = p.cos + (long)(p.pos0 + t) * p.half;
         const float* sn = p.sin + (long)(p.pos0 + t) * p.half;
-        const float dy = unrotate(gbase + r * p.hd, cs, sn, i, p.half);
+        const float dy = p.unrot ? unrotate(gbase + r * p.hd, cs, sn, i, p.half) : gbase[r * p.hd + i];
         const float xhat = xbase[r * p.hd + i] * rstd[r];
         acc += dy * xhat;
     }
@@ -436,8 +443,9 @@ size_t prologue_bwd_scratch_floats(const Dims& d) {
 hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* dq, const float* dk,
                                const float* q_pre, const float* k_pre, const float* q_rstd, const float* k_rstd,
                                float* dq_pre, float* dk_pre, float* dqw, float* dkw, float* partial, hipStream_t st,
-                               KernelTimer* timer) {
+                               KernelTimer* timer, bool unrotated) {
     ProBwdParams p{};
+    p.unrot = unrotated ? 0 : 1;
     p.dq = dq;
     p.dk = dk;
     p.q_pre = q_pre;

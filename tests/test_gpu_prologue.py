@@ -214,6 +214,56 @@ def test_fused_config_bf16(env, cfg_name):
         assert e <= BF16_TOL, f"{cfg_name} {nm}: {e}"
 
 
+# Shapes of the fast bf16 kernels (head_dim 64 and 128; stored-dS dQ at 128),
+# with and without the Qwen3 norm, and a ragged tail.
+EPILOGUE_SHAPES = {
+    "plain": PROLOGUES["plain"],
+    "llama3": PROLOGUES["llama3"],
+    "qknorm": PROLOGUES["qknorm"],
+    "rope128": (2, 97, 8, 2, 128, 5e5, None, False, 5),
+    "qknorm64": (1, 70, 4, 4, 64, 1e6, None, True, 2),
+}
+
+
+@pytest.mark.parametrize("name", sorted(EPILOGUE_SHAPES))
+def test_fused_bwd_epilogue_matches_separate_passes(env, name):
+    """In bf16 mode cfattn_fused_bwd folds the inverse RoPE into the dQ and
+    dK kernels' epilogues (adding into dq_pre/dk_pre, or with the norm storing
+    the unrotated rows for the norm-only pass).  It must give the same bits
+    as the attention backward into zeroed dq/dk followed by the separate
+    prologue backward, also on top of nonzero dq_pre/dk_pre."""
+    torch, cf, D, ctx = env
+    B, S, Hq, Hk, Dh, theta, sc, qkn, pos0 = EPILOGUE_SHAPES[name]
+    max_pos = S + pos0
+    rope = cf.RopeCache(Dh, max_pos, theta, cf.Llama3Scaling(*sc) if sc else None)
+    qw = kw = None
+    if qkn:
+        qw = torch.from_numpy((1.0 + O.rand(Dh, 950, 0.02)).astype(np.float32)).cuda()
+        kw = torch.from_numpy((1.0 + O.rand(Dh, 951, 0.02)).astype(np.float32)).cuda()
+    pr = D.DeviceRope(rope, "cuda", pos0, qw, kw, 1e-6)
+    torch.manual_seed(31)
+    q_pre = torch.randn(B, S, Hq, Dh, device="cuda")
+    k_pre = torch.randn(B, S, Hk, Dh, device="cuda")
+    vd = torch.randn(B, S, Hk, Dh, device="cuda").to(torch.bfloat16)
+    gd = torch.randn(B, S, Hq, Dh, device="cuda").to(torch.bfloat16)
+    init_q = torch.randn(B, S, Hq, Dh, device="cuda")
+    init_k = torch.randn(B, S, Hk, Dh, device="cuda")
+    o, lse, q, k, qr, kr = D.fused_fwd(q_pre, k_pre, vd, pr, ctx=ctx)
+    fz = D.fused_bwd(gd, q_pre, k_pre, q, k, vd, o, lse, qr, kr, pr, dq_pre=init_q.clone(), dk_pre=init_k.clone(),
+                     ctx=ctx)
+    dq, dk, dv = D.bwd(gd, q, k, vd, o, lse, ctx=ctx)
+    sp = D.prologue_bwd(dq, dk, q_pre, k_pre, qr, kr, pr, dq_pre=init_q.clone(), dk_pre=init_k.clone(), ctx=ctx)
+    torch.cuda.synchronize()
+    got = {"dq_pre": fz[0], "dk_pre": fz[1], "dv": fz[2]}
+    want = {"dq_pre": sp[0], "dk_pre": sp[1], "dv": dv}
+    if qkn:
+        got.update(dq_norm=fz[3], dk_norm=fz[4])
+        want.update(dq_norm=sp[2], dk_norm=sp[3])
+    for nm in got:
+        a, r = got[nm].cpu().numpy(), want[nm].cpu().numpy()
+        assert np.array_equal(a, r), f"{name} {nm}: max diff {np.abs(a - r).max():.3e}"
+
+
 def test_forward_and_backward_are_bitwise_repeatable(env):
     """Checkpoint mode recomputes the forward and expects the identical loss
     (crates/model/src/tests.rs:147-163): the kernels use no atomics, so two
