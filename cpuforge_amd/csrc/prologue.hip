@@ -36,6 +36,7 @@ struct ProParams {
     int seq, nh, nkv, hd;
     long rows_q, rows_k;
     int srows;  // rows per block of the staged kernel
+    int vec4;   // 4-column accesses: D % 8 == 0, D/8 divides 256, 16-byte aligned rows and tables
 };
 
 template <typename T>
@@ -141,6 +142,49 @@ __global__ __launch_bounds__(256) void prologue_fwd_staged_kernel(const ProParam
         __syncthreads();
     }
     T* y = static_cast<T*>(isq ? p.q_out : p.k_out) + r0 * D;
+    if (p.vec4) {
+        // Four consecutive columns per thread: half/4 threads per row, the
+        // position (one division) per row; same expressions per element.
+        const int cpr = half / 4, rpi = 256 / cpr;
+        const int i = (tid % cpr) * 4;
+        for (int row = tid / cpr; row < nr; row += rpi) {
+            const int t = (int)(((r0 + row) / heads) % p.seq);
+            const float4 c4 = *reinterpret_cast<const float4*>(p.cos + (long)(p.pos0 + t) * half + i);
+            const float4 s4 = *reinterpret_cast<const float4*>(p.sin + (long)(p.pos0 + t) * half + i);
+            float a[4], b[4];
+            if (w) {
+                const float inv = srstd[row];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    a[u] = stage[row * LD + i + u] * inv * w[i + u];
+                    b[u] = stage[row * LD + i + half + u] * inv * w[i + half + u];
+                }
+            } else {
+                const float4 a4 = *reinterpret_cast<const float4*>(x + (long)row * D + i);
+                const float4 b4 = *reinterpret_cast<const float4*>(x + (long)row * D + i + half);
+                a[0] = a4.x, a[1] = a4.y, a[2] = a4.z, a[3] = a4.w;
+                b[0] = b4.x, b[1] = b4.y, b[2] = b4.z, b[3] = b4.w;
+            }
+            const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+            T lo[4], hi[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                lo[u] = from_f32<T>(a[u] * c[u] - b[u] * sv[u]);
+                hi[u] = from_f32<T>(b[u] * c[u] + a[u] * sv[u]);
+            }
+            T* yr = y + (long)row * D + i;
+            if constexpr (sizeof(T) == 2) {
+                *reinterpret_cast<uint2*>(yr) = make_uint2((uint32_t)lo[0] | ((uint32_t)lo[1] << 16),
+                                                           (uint32_t)lo[2] | ((uint32_t)lo[3] << 16));
+                *reinterpret_cast<uint2*>(yr + half) = make_uint2((uint32_t)hi[0] | ((uint32_t)hi[1] << 16),
+                                                                  (uint32_t)hi[2] | ((uint32_t)hi[3] << 16));
+            } else {
+                *reinterpret_cast<float4*>(yr) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+                *reinterpret_cast<float4*>(yr + half) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+            }
+        }
+        return;
+    }
     for (int j = tid; j < nr * half; j += 256) {
         const int row = j / half, i = j % half;
         const int t = (int)(((r0 + row) / heads) % p.seq);
@@ -407,6 +451,10 @@ hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, cons
     p.rows_k = (long)d.batch * d.seq * d.nkv;
     const long rows = p.rows_q + p.rows_k;
     if (rows == 0) return hipSuccess;
+    const uintptr_t al = 16;
+    p.vec4 = d.hd % 8 == 0 && 256 % (d.hd / 8) == 0 && (uintptr_t)q_pre % al == 0 && (uintptr_t)k_pre % al == 0 &&
+             (uintptr_t)q_out % al == 0 && (uintptr_t)k_out % al == 0 && (uintptr_t)pr.cos % al == 0 &&
+             (uintptr_t)pr.sin % al == 0;
     TimedLaunch tl(timer, kKernProFwd, st);
     if (d.hd <= kStageMaxD) {
         p.srows = stage_rows(d.hd + 1, 1);  // the rstd column counted as one more float per row
