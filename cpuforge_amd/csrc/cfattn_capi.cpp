@@ -102,15 +102,11 @@ hipStream_t pick_stream(cfattn_ctx*, void* st) { return static_cast<hipStream_t>
 const void* upload(cfattn_ctx* c, int s32, int s16, const float* host, size_t n, bool bf16, int* rc) {
     float* d = static_cast<float*>(slot(c, s32, n * 4, rc));
     if (!d) return nullptr;
-    hipError_t e = hipMemcpyAsync(d, host, n * 4, hipMemcpyHostToDevice, c->stream);
-    if (e != hipSuccess) {
-        *rc = hip_fail(c, e, "hipMemcpyAsync H2D");
-        return nullptr;
-    }
+    if ((*rc = stage_upload(c, d, host, n * 4)) != CFATTN_OK) return nullptr;
     if (!bf16) return d;
     uint16_t* b = static_cast<uint16_t*>(slot(c, s16, n * 2, rc));
     if (!b) return nullptr;
-    e = cfattn::launch_f32_to_bf16(d, b, n, c->stream);
+    const hipError_t e = cfattn::launch_f32_to_bf16(d, b, n, c->stream);
     if (e != hipSuccess) {
         *rc = hip_fail(c, e, "f32_to_bf16 launch");
         return nullptr;
@@ -136,6 +132,7 @@ int forward_host(cfattn_ctx* c, const float* q, size_t q_len, const float* k, si
     if (!q || !k || !v || !o || !lse) return fail(c, CFATTN_ERR_ARG, "null buffer");
     DeviceGuard dg(c->device);
     if (!dg.ok) return fail(c, CFATTN_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+    CF_TRY(order_after_device_calls(c));
     const bool bf = c->mode == CFATTN_BF16;
     int rc = CFATTN_OK;
     const void* dq = upload(c, cfattn_ctx::Q, cfattn_ctx::QB, q, q_len, bf, &rc);
@@ -153,8 +150,8 @@ int forward_host(cfattn_ctx* c, const float* q, size_t q_len, const float* k, si
     CF_HIP(c, cfattn::launch_attn_fwd(bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), dq, dk, dv, dout, dlse,
                                       c->stream, c->tuning(), fs, fs_bytes),
            "attention forward launch");
-    CF_HIP(c, hipMemcpyAsync(o, dout, o_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H o");
-    CF_HIP(c, hipMemcpyAsync(lse, dlse, lse_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H lse");
+    CF_TRY(stage_download(c, o, dout, o_len * 4));
+    CF_TRY(stage_download(c, lse, dlse, lse_len * 4));
     CF_HIP(c, hipStreamSynchronize(c->stream), "attention forward");
     return CFATTN_OK;
 }
@@ -183,6 +180,7 @@ int backward_host(cfattn_ctx* c, const float* d_o, size_t d_o_len, const float* 
     if (!d_o || !q || !k || !v || !o || !lse || !dq || !dk || !dv) return fail(c, CFATTN_ERR_ARG, "null buffer");
     DeviceGuard dg(c->device);
     if (!dg.ok) return fail(c, CFATTN_ERR_HIP, "hipSetDevice(%d) failed", c->device);
+    CF_TRY(order_after_device_calls(c));
     const bool bf = c->mode == CFATTN_BF16;
     int rc = CFATTN_OK;
     const void* ddo = upload(c, cfattn_ctx::DO_, cfattn_ctx::DOB, d_o, d_o_len, bf, &rc);
@@ -202,17 +200,19 @@ int backward_host(cfattn_ctx* c, const float* d_o, size_t d_o_len, const float* 
     float* g_v = g_k ? static_cast<float*>(slot(c, cfattn_ctx::DV, dv_len * 4, &rc)) : nullptr;
     float* delta = g_v ? static_cast<float*>(slot(c, cfattn_ctx::DELTA, s.n_heads * s.seq * 4, &rc)) : nullptr;
     if (!delta) return rc;
-    CF_HIP(c, hipMemcpyAsync(g_q, dq, dq_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dq");
-    CF_HIP(c, hipMemcpyAsync(g_k, dk, dk_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dk");
-    CF_HIP(c, hipMemcpyAsync(g_v, dv, dv_len * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D dv");
+    // The gradients accumulate (+=, attention.rs:145-154): their current
+    // values go up with the inputs.
+    CF_TRY(stage_upload(c, g_q, dq, dq_len * 4));
+    CF_TRY(stage_upload(c, g_k, dk, dk_len * 4));
+    CF_TRY(stage_upload(c, g_v, dv, dv_len * 4));
     size_t ds_bytes = 0;
     void* ds = ds_scratch(c, bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), &ds_bytes);
     CF_HIP(c, cfattn::launch_attn_bwd(bf ? cfattn::kBF16 : cfattn::kF32, dims_of(s, 1), ddo, dq_in, dk_in, dv_in,
                                       d_out, d_lse, delta, g_q, g_k, g_v, c->stream, c->tuning(), ds, ds_bytes),
            "attention backward launch");
-    CF_HIP(c, hipMemcpyAsync(dq, g_q, dq_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H dq");
-    CF_HIP(c, hipMemcpyAsync(dk, g_k, dk_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H dk");
-    CF_HIP(c, hipMemcpyAsync(dv, g_v, dv_len * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H dv");
+    CF_TRY(stage_download(c, dq, g_q, dq_len * 4));
+    CF_TRY(stage_download(c, dk, g_k, dk_len * 4));
+    CF_TRY(stage_download(c, dv, g_v, dv_len * 4));
     CF_HIP(c, hipStreamSynchronize(c->stream), "attention backward");
     return CFATTN_OK;
 }
@@ -257,6 +257,11 @@ int cfattn_create(int device, cfattn_ctx** out) {
         delete c;
         return CFATTN_ERR_HIP;
     }
+    if (hipEventCreateWithFlags(&c->dev_done, hipEventDisableTiming) != hipSuccess) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return CFATTN_ERR_HIP;
+    }
     // The fixed scratch of cfattn_bwd_noalloc on this device (looked up once
     // per device; a failure here is reported by that entry point, which
     // retries the lookup).
@@ -276,6 +281,8 @@ int cfattn_destroy(cfattn_ctx* c) {
         delete c->timer;
         c->timer = nullptr;
         if (c->io && c->io_release) c->io_release(c->io);  // waits for its staging copies
+        if (c->hs && c->hs_release) c->hs_release(c->hs);  // the same for the host-slice staging
+        if (c->dev_done) (void)hipEventDestroy(c->dev_done);
         for (int i = 0; i < cfattn_ctx::NSLOT; i++)
             if (c->buf[i]) (void)hipFree(c->buf[i]);
         if (c->blas && c->blas_release) c->blas_release(c->blas);
@@ -356,6 +363,7 @@ int cfattn_fwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const voi
     if (!c) return CFATTN_ERR_ARG;
     std::lock_guard<std::mutex> lk(c->mu);
     c->err.clear();
+    DeviceCallMark mark(c, pick_stream(c, stream));
     return cfattn_fwd_locked(c, s, batch, dtype, q, k, v, o, lse, stream);
 }
 
@@ -385,6 +393,7 @@ int cfattn_bwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, const voi
     if (!c) return CFATTN_ERR_ARG;
     std::lock_guard<std::mutex> lk(c->mu);
     c->err.clear();
+    DeviceCallMark mark(c, pick_stream(c, stream));
     return cfattn_bwd_locked(c, s, batch, dtype, d_o, q, k, v, o, lse, dq, dk, dv, stream);
 }
 
@@ -487,6 +496,7 @@ int cfattn_fused_fwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, con
     if (!c) return CFATTN_ERR_ARG;
     std::lock_guard<std::mutex> lk(c->mu);
     c->err.clear();
+    DeviceCallMark mark(c, pick_stream(c, stream));
     CF_TRY(cfattn_prologue_fwd_locked(c, s, batch, dtype, pr, q_pre, k_pre, q_out, k_out, q_rstd, k_rstd, stream));
     return cfattn_fwd_locked(c, s, batch, dtype, q_out, k_out, v, o, lse, stream);
 }
@@ -498,6 +508,7 @@ int cfattn_fused_bwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, con
     if (!c) return CFATTN_ERR_ARG;
     std::lock_guard<std::mutex> lk(c->mu);
     c->err.clear();
+    DeviceCallMark mark(c, pick_stream(c, stream));
     CF_TRY(check_dtype(c, dtype));
     if (batch == 0 || s.seq == 0) return CFATTN_OK;
     CF_TRY(check_shape(c, s));

@@ -124,6 +124,15 @@ struct cfattn_ctx {
     void* io = nullptr;
     void (*io_release)(void*) = nullptr;
     size_t io_chunk = (size_t)8 << 20;
+    // Pinned staging of the host-slice entry points (host_stage.cpp),
+    // created on first use; released by cfattn_destroy.
+    void* hs = nullptr;
+    void (*hs_release)(void*) = nullptr;
+    // Recorded on the caller's stream at the end of every device entry
+    // point that uses the pool's attention slots; host-slice calls order
+    // the context's stream after it before they reuse those slots.
+    hipEvent_t dev_done = nullptr;
+    bool dev_pending = false;
 
     cfattn::Tuning tuning() const {
         cfattn::Tuning t;
@@ -186,6 +195,32 @@ inline void* slot(cfattn_ctx* c, int s, size_t bytes, int* rc) {
     c->buf[s] = p;
     c->cap[s] = want;
     return p;
+}
+
+// Host-slice staging (host_stage.cpp): copies through two pinned chunks on
+// the context's stream.  stage_upload returns once every chunk is queued
+// (the caller's slice may then change); stage_download returns with the
+// data in the caller's slice.
+int stage_upload(cfattn_ctx* c, void* dev, const void* host, size_t bytes);
+int stage_download(cfattn_ctx* c, void* host, const void* dev, size_t bytes);
+
+// Marks the end of a device entry point's work on `st` (see dev_done).
+struct DeviceCallMark {
+    cfattn_ctx* c;
+    hipStream_t st;
+    DeviceCallMark(cfattn_ctx* c_, hipStream_t st_) : c(c_), st(st_) {}
+    ~DeviceCallMark() {
+        if (c->dev_done && hipEventRecord(c->dev_done, st) == hipSuccess) c->dev_pending = true;
+    }
+};
+
+// Orders the context's stream after the last device entry point's work.
+inline int order_after_device_calls(cfattn_ctx* c) {
+    if (!c->dev_pending) return CFATTN_OK;
+    const hipError_t e = hipStreamWaitEvent(c->stream, c->dev_done, 0);
+    if (e != hipSuccess) return hip_fail(c, e, "hipStreamWaitEvent");
+    c->dev_pending = false;
+    return CFATTN_OK;
 }
 
 }  // namespace cfcapi

@@ -231,3 +231,72 @@ def test_fast_backward_accumulates(env, shape, mode, ds):
                                                      g1.cpu().numpy().astype(np.float64))
         err = np.abs(a - want).max() / (1.0 + np.abs(want).max())
         assert err <= 1e-6, f"{shape} {mode} {ds} {name}: {err}"
+
+
+def test_host_slices_through_several_staging_chunks(env):
+    """The host-slice entry points copy through two 32 MiB pinned chunks;
+    q, dO, o and dq here span two chunks with a ragged tail.  In f32 mode
+    the host-slice path runs the same kernels as the device entry points on
+    the same values, so both give the same bits, also with nonzero dq/dk/dv
+    to accumulate into."""
+    torch, cf, D, ctx = env
+    seq, h, kv, hd = 4100, 16, 4, 128
+    rng = np.random.default_rng(77)
+    q, g = (rng.standard_normal(seq * h * hd, dtype=np.float32) for _ in range(2))
+    k, v = (rng.standard_normal(seq * kv * hd, dtype=np.float32) for _ in range(2))
+    dq0 = rng.standard_normal(seq * h * hd, dtype=np.float32)
+    dk0, dv0 = (rng.standard_normal(seq * kv * hd, dtype=np.float32) for _ in range(2))
+    s = cf.AttnShape(seq, h, kv, hd)
+    o = np.zeros(seq * h * hd, np.float32)
+    lse = np.zeros(h * seq, np.float32)
+    cf.attention_forward(q, k, v, o, lse, s, ctx)
+    dq, dk, dv = dq0.copy(), dk0.copy(), dv0.copy()
+    cf.attention_backward(g, q, k, v, o, lse, dq, dk, dv, s, ctx)
+    t = lambda x, H: torch.from_numpy(x).view(1, seq, H, hd).cuda()  # noqa: E731
+    od, ld = D.fwd(t(q, h), t(k, kv), t(v, kv), ctx=ctx)
+    dqd, dkd, dvd = D.bwd(t(g, h), t(q, h), t(k, kv), t(v, kv), od, ld, t(dq0, h).clone(), t(dk0, kv).clone(),
+                          t(dv0, kv).clone(), ctx=ctx)
+    torch.cuda.synchronize()
+    for n, a, r in (("o", o, od), ("lse", lse, ld), ("dq", dq, dqd), ("dk", dk, dkd), ("dv", dv, dvd)):
+        assert np.array_equal(a, r.cpu().numpy().reshape(-1)), n
+
+
+def test_host_slice_call_waits_for_device_calls(env):
+    """A host-slice call reuses the context's scratch slots (delta, stored
+    dS, the staged operands) that a device call queued on another stream may
+    still be reading; it must order its stream after that work.  A large
+    bf16 backward is queued on torch's stream and, without a host wait, a
+    host-slice backward of another shape follows at once; both results must
+    equal the same calls run alone."""
+    torch, cf, D, ctx = env
+    torch.manual_seed(5)
+    B, S, H, KV, Dh = 1, 4096, 16, 4, 128
+    q = torch.randn(B, S, H, Dh, device="cuda").to(torch.bfloat16)
+    k = torch.randn(B, S, KV, Dh, device="cuda").to(torch.bfloat16)
+    v = torch.randn(B, S, KV, Dh, device="cuda").to(torch.bfloat16)
+    g = torch.randn(B, S, H, Dh, device="cuda").to(torch.bfloat16)
+    o, lse = D.fwd(q, k, v, ctx=ctx)
+    torch.cuda.synchronize()
+    alone = [x.cpu().numpy() for x in D.bwd(g, q, k, v, o, lse, ctx=ctx)]
+    torch.cuda.synchronize()
+    seq, h, kv, hd = 300, 8, 2, 128
+    hq, hk, hv = case(seq, h, kv, hd, 81)
+    hg = O.rand(seq * h * hd, 84, 1.0)
+    s = cf.AttnShape(seq, h, kv, hd)
+
+    def host_bwd():
+        ho = np.zeros(seq * h * hd, np.float32)
+        hl = np.zeros(h * seq, np.float32)
+        cf.attention_forward(hq, hk, hv, ho, hl, s, ctx)
+        dq, dk, dv = np.zeros_like(hq), np.zeros_like(hk), np.zeros_like(hv)
+        cf.attention_backward(hg, hq, hk, hv, ho, hl, dq, dk, dv, s, ctx)
+        return [ho, hl, dq, dk, dv]
+
+    host_alone = host_bwd()
+    mixed_dev = D.bwd(g, q, k, v, o, lse, ctx=ctx)  # queued; no synchronisation before the host call
+    host_mixed = host_bwd()
+    torch.cuda.synchronize()
+    for n, a, r in zip(("dq", "dk", "dv"), [x.cpu().numpy() for x in mixed_dev], alone):
+        assert np.array_equal(a, r), f"device {n} changed by the host-slice call"
+    for n, a, r in zip(("o", "lse", "dq", "dk", "dv"), host_mixed, host_alone):
+        assert np.array_equal(a, r), f"host-slice {n}"
