@@ -298,15 +298,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const int wv = wave_uniform(wave);
     constexpr int NBL = L::NB;
     const int lane_off = NBL * (lane / CPR) * (int)kvrs + (lane % CPR) * 8;
+    // Full tiles: a scalar tile base plus the lane's byte offset within the
+    // tile (the saddr form: no 64-bit address arithmetic per lane and load).
+    const uint32_t lane_boff = (uint32_t)lane_off * 2u;
     auto dma = [&](int kt, bf16_bits* Kd, bf16_bits* Vd) {
         if ((kt + 1) * BN <= p.seq) {
             const long base = (long)kt * BN * kvrs;
 #pragma unroll
             for (int i = 0; i < CPW; i++) {
                 const int blk = wv * CPW + i;
-                const long off = base + (long)blk * kvrs + lane_off;
-                __builtin_amdgcn_global_load_lds(kg + off, Kd + blk * BSTRIDE, 16, 0, 0);
-                __builtin_amdgcn_global_load_lds(vg + off, Vd + blk * BSTRIDE, 16, 0, 0);
+                const uint32_t off = lane_boff + (uint32_t)(blk * kvrs) * 2u;
+                lds_load16_sv(kg + base, off, Kd + blk * BSTRIDE);
+                lds_load16_sv(vg + base, off, Vd + blk * BSTRIDE);
             }
         } else {
 #pragma unroll
@@ -381,9 +384,27 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 // All score blocks are issued first; each block's max is taken
                 // on its own, so block kb's softmax runs while the products of
                 // block kb+1 (scores) and of block kb-1 (O^T) are in flight.
+                // The K row operands are read kLA MFMAs ahead of their product
+                // (the order pinned: left to itself the compiler reads each
+                // right before its MFMA and waits for it).
                 f32x16 sc[NKB];
+                {
+                    constexpr int N = NKB * NKD, kLA = 4;
+                    auto rd = [&](int j) {
+                        return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                                              Ks + rrow + (j % NKB) * 2 * ROW16 + (j / NKB) * 8));
+                    };
+                    bf16x8 kr[N];
 #pragma unroll
-                for (int kb = 0; kb < NKB; kb++) sc[kb] = scores(kb);
+                    for (int j = 0; j < kLA; j++) kr[j] = rd(j);
+#pragma unroll
+                    for (int j = 0; j < N; j++) {
+                        if (j + kLA < N) kr[j + kLA] = rd(j + kLA);
+                        const int kb = j % NKB, kd = j / NKB;
+                        sc[kb] = mfma32(kr[j], qf[kd], kd == 0 ? zero16() : sc[kb]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
                 if (more) dma(kt + 1, Kn, Vn);
 #pragma unroll
                 for (int kb = 0; kb < NKB; kb++) {
