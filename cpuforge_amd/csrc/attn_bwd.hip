@@ -885,12 +885,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int qt_begin = wg_key0 / BM;
     const int nq = n_qt - qt_begin;
     const int n_steps = p.group * nq;
-    // Step s covers query tile qt_begin + s % nq of query head s / nq.
-    // (Walking every workgroup's tiles from the last one down, heads
-    // innermost, so that the workgroups on an XCD read the same Q/dO tiles
-    // together, measured 4% slower.)
-    auto step_q0 = [&](int s) { return (qt_begin + s % nq) * BM; };
-    auto step_h = [&](int s) { return g * p.group + s / nq; };
+    // Step s covers query head g * group + s % group of query tile
+    // n_qt - 1 - s / group (walking down) or qt_begin + s / group (walking
+    // up): the order of attn_bwd_dkdv_k64_kernel, whose sums this kernel
+    // reproduces bit for bit.
+    const bool down = dkdv_walks_down(blockIdx.x, p.xcd_cus);
+    auto step_q0 = [&](int s) { return (down ? n_qt - 1 - s / p.group : qt_begin + s / p.group) * BM; };
+    auto step_h = [&](int s) { return g * p.group + s % p.group; };
 
     float pl = 0.0f;
     // The dS waves (threads 256..511) load the tiles, lse and delta: they
@@ -1316,6 +1317,13 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
                ((uintptr_t)v % al == 0) && ((uintptr_t)d_o % al == 0);
     p.g_vec_ok = (d.hd % 4 == 0) && ((uintptr_t)dq % al == 0) && ((uintptr_t)dk % al == 0) && ((uintptr_t)dv % al == 0);
     p.xcd = tu.xcd_remap;
+    {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return hipErrorInvalidDevice;
+        p.xcd_cus = cus >= 8 ? cus / 8 : 1;
+    }
     if (epi) {
         p.epi = epi->mode;
         p.rope_cos = epi->cos;

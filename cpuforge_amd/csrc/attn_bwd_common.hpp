@@ -8,6 +8,22 @@ namespace cfattn {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// Direction in which a dK/dV workgroup (one per CU) walks its query tiles,
+// heads innermost.  The XCDs dispatch workgroups in rounds of xcd_cus, one
+// per CU; key tiles ascend within a round.  In even rounds every workgroup
+// starts at the last query tile and walks down: they all start together
+// and so read each Q/dO tile of a head within a step of each other.  The
+// next round's workgroups start as the previous round's end, the one with
+// the fewest query tiles (the highest key tile) first; walking up from
+// their own first tile, each reaches tile q when the others do (a
+// workgroup that starts d tiles later starts d tiles higher), so they too
+// share each tile in the XCD's L2.  Walking every workgroup up from its
+// diagonal instead leaves neighbours 2 tiles (8 steps, about 8 MB of an
+// XCD's reads at C5) apart, more than a 4 MB L2 holds.
+__device__ __forceinline__ bool dkdv_walks_down(unsigned hw_id, int xcd_cus) {
+    return ((hw_id / 8u / (unsigned)xcd_cus) & 1u) == 0u;
+}
+
 // Accumulate one lane's 4 x (4 consecutive head dims) of a transposed
 // accumulator block into a global row: dst[d0 + 8*rq + 4*hh + i] += acc[4*rq + i].
 __device__ __forceinline__ void add_row_block(float* row, const f32x16& acc, int dbase, int hh, int hd, bool vec_ok) {

@@ -146,17 +146,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int qt_begin = wg_key0 / BM;
     const int n_steps = p.group * (n_qt - qt_begin);
     // A step: query tile [q0, q0 + BM) of query head h.  Steps run over the
-    // query tiles qt_begin.. of each head of the group in turn, and each
-    // wave walks them with a cursor (no divisions in the loop).
+    // heads of the group for one query tile, then the next tile, walking the
+    // tiles qt_begin..n_qt-1 down or up (dkdv_walks_down), and each wave
+    // walks them with a cursor (no divisions in the loop).
     struct Pos {
         int q0, h;
     };
-    const Pos first{qt_begin * BM, g * p.group};
+    const bool down = dkdv_walks_down(blockIdx.x, p.xcd_cus);
+    const int h0 = g * p.group, h_end = h0 + p.group, q_step = down ? -BM : BM;
+    const Pos first{(down ? n_qt - 1 : qt_begin) * BM, h0};
     auto next_pos = [&](Pos x) {
-        x.q0 += BM;
-        if (x.q0 >= n_qt * BM) {
-            x.q0 = qt_begin * BM;
-            x.h++;
+        if (++x.h == h_end) {
+            x.h = h0;
+            x.q0 += q_step;
         }
         return x;
     };

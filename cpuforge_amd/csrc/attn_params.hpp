@@ -43,8 +43,9 @@ struct BwdParams {
     float* dk;
     float* dv;
     int batch, seq, nh, nkv, hd, group;
-    // dK/dV grid
-    int kv_tile, n_kvtiles, n_wg_kv;
+    // dK/dV grid; xcd_cus: compute units per XCD, that is the workgroups of
+    // one XCD's dispatch round for the one-workgroup-per-CU dK/dV kernels
+    int kv_tile, n_kvtiles, n_wg_kv, xcd_cus;
     // dQ grid
     int hpw, tpw, n_sub, n_ttiles, n_wg_q;
     float scale, sl2;
