@@ -42,6 +42,11 @@
 // (stores early in the interval: the barrier's wait covers them).
 // P of step t is in LDS at barrier t; the dS wave uses it in interval t + 1.
 // Diagonal and ragged steps (a few per head) take a plain, unpipelined path.
+// The full steps of a wave's walk are one run; each role loops over the
+// masked steps before it, the run (branch-free, two steps per iteration)
+// and the masked steps after it.  The per-step bookkeeping (cursors,
+// buffers, the next step's buffer resources) is scalar and runs in the MFMA
+// shadow of the last region.
 //
 // Buffers: Q (and lse) of step t are read in intervals t - 1, t and t + 1
 // and loaded in interval t - 2: four buffers.  dO (and delta) of step t are
@@ -111,9 +116,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     __shared__ uint4 sP[2][2][2][NKB][2][64];
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int pair = wave & 1;
-    const bool pwave = wave < 2;
+    const int lane = tid & 63;
+    // Wave index and everything derived from it, uniform (scalar registers).
+    const int wv = wave_uniform(tid >> 6);
+    const int pair = (tid >> 6) & 1;
+    const bool pwave = wv < 2;
     const int l32 = lane & 31, hh = lane >> 5;
 
     const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
@@ -147,19 +154,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int n_steps = p.group * (n_qt - qt_begin);
     // A step: query tile [q0, q0 + BM) of query head h.  Steps run over the
     // heads of the group for one query tile, then the next tile, walking the
-    // tiles qt_begin..n_qt-1 down or up (dkdv_walks_down), and each wave
-    // walks them with a cursor (no divisions in the loop).
+    // tiles qt_begin..n_qt-1 down or up (dkdv_walks_down).  Each wave walks
+    // them with cursors that also carry the step's byte offsets: qo of its
+    // Q / dO rows (row q0, head h) and lo of its lse / delta rows, both
+    // within the sequence (32-bit: a sequence's Q has fewer than 2^31
+    // elements, checked by the launcher's shape limits).  Past the last step
+    // a cursor starts over at the first, so the loads a wave issues for
+    // steps beyond its last stay inside the sequence (they fill buffers that
+    // are never read).
     struct Pos {
         int q0, h;
+        uint32_t qo, lo;
     };
     const bool down = dkdv_walks_down(blockIdx.x, p.xcd_cus);
     const int h0 = g * p.group, h_end = h0 + p.group, q_step = down ? -BM : BM;
-    const Pos first{(down ? n_qt - 1 : qt_begin) * BM, h0};
+    const int q_first = (down ? n_qt - 1 : qt_begin) * BM, q_past = (down ? qt_begin - 1 : n_qt) * BM;
+    const uint32_t qo_row = (uint32_t)qrs * 2u;  // bytes per query row
+    const uint32_t qo_head = DP * 2, lo_head = (uint32_t)p.seq * 4u;
+    const uint32_t qo_wrap = (uint32_t)q_step * qo_row - (uint32_t)(p.group - 1) * qo_head;
+    const uint32_t lo_wrap = (uint32_t)q_step * 4u - (uint32_t)(p.group - 1) * lo_head;
+    const uint32_t qo_again = (uint32_t)(q_first - q_past) * qo_row, lo_again = (uint32_t)(q_first - q_past) * 4u;
+    const Pos first{q_first, h0, (uint32_t)q_first * qo_row + (uint32_t)h0 * qo_head,
+                    (uint32_t)h0 * lo_head + (uint32_t)q_first * 4u};
+    // (Selects, not branches: it runs in MFMA shadows.)
     auto next_pos = [&](Pos x) {
-        if (++x.h == h_end) {
-            x.h = h0;
-            x.q0 += q_step;
-        }
+        const bool wrap = x.h + 1 == h_end;
+        x.h = wrap ? h0 : x.h + 1;
+        x.q0 += wrap ? q_step : 0;
+        x.qo += wrap ? qo_wrap : qo_head;
+        x.lo += wrap ? lo_wrap : lo_head;
+        const bool again = x.q0 == q_past;
+        x.q0 = again ? q_first : x.q0;
+        x.qo += again ? qo_again : 0u;
+        x.lo += again ? lo_again : 0u;
         return x;
     };
     // The wave's keys meet at least one query of the step.
@@ -167,57 +194,64 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // Every query of the step is past every key of the wave and inside the
     // sequence: no mask, and every block is on or below the diagonal.
     auto pos_full = [&](Pos x) { return x.q0 >= key0 + 63 && x.q0 + BM <= p.seq; };
+    // The full steps of the wave's walk are one run, steps [s_full0,
+    // s_full1): query tiles t with 64 t >= key0 + 63 (past the diagonal) and
+    // 64 (t + 1) <= seq (not cut by the end), met in walk order.  The loops
+    // below run the steps before and after the run through the masked path
+    // and the run itself through the pipelined one, with no per-step branch.
+    int s_full0 = 0, s_full1 = 0;
+    {
+        const int k0 = wg_key0 + (wv & 1) * 64;  // key0, as a scalar
+        const int t_lo = max((k0 + 63 + BM - 1) / BM, qt_begin), t_hi = p.seq / BM - 1;
+        if (k0 < p.seq && t_lo <= t_hi) {
+            s_full0 = (down ? n_qt - 1 - t_hi : t_lo - qt_begin) * p.group;
+            s_full1 = (down ? n_qt - t_lo : t_hi + 1 - qt_begin) * p.group;
+        }
+    }
 
-    const int wv = wave_uniform(wave);
     // Tile loads: wave w loads blocks w*BPW.. of a Q and a dO tile, lane l of
-    // block bk reading chunk l % CPR of tile row bk + NB*(l / CPR); rows past
-    // the end read the last row (finite values, masked below).  Wave 0 also
-    // loads lse and wave 1 delta, one value per MFMA row (MFMA row `lane`:
-    // tile row (lane & 32) + qperm(lane & 31)).  Each load is a scalar base
-    // (the tile) plus a per-lane byte offset, set once per interval.
+    // block bk reading chunk l % CPR of tile row bk + NB*(l / CPR).  Wave 0
+    // also loads lse and wave 1 delta, one value per MFMA row (MFMA row
+    // `lane`: tile row (lane & 32) + qperm(lane & 31)).  The loads are
+    // bounds-checked buffer loads whose buffer starts at the step's rows and
+    // ends with the sequence: rows past the end read zeros (masked below),
+    // and the per-lane byte offsets are the same for every step.
     const int lane_row = NBL * (lane / CPR), lane_col = (lane % CPR) * 8;
     const int lrow = (lane & 32) + qperm(lane & 31);
     constexpr int kLoadsP = 2 * BPW + 1, kLoadsDs = 2 * BPW;
+    uint32_t tile_off[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; i++) tile_off[i] = (uint32_t)(((lane_row + wv * BPW + i) * (int)qrs + lane_col) * 2);
+    const uint32_t row_off = (uint32_t)lrow * 4u;
     struct Loads {
-        const bf16_bits* q;  // the Q tile
-        const bf16_bits* o;  // the dO tile
-        const float* ld;     // lse row of the Q step (wave 0) or delta row of the dO step (wave 1)
-        uint32_t qoff[BPW], ooff[BPW], lvoff;
-        int qbuf, obuf, lbuf;
+        BufRsrc q, o, l;            // the Q tile, the dO tile, the lse (wave 0) or delta (wave 1) rows
+        uint32_t qlds, olds, llds;  // LDS byte addresses of this wave's first block / of the row values
     };
-    // Byte offsets of this wave's blocks in a whole tile; a tile cut by the
-    // end of the sequence clamps them to the last row: min over rows of
-    // row*stride + column is min(offset, last row*stride + column).
-    uint32_t full_off[BPW];
-#pragma unroll
-    for (int i = 0; i < BPW; i++) full_off[i] = (uint32_t)(((lane_row + wv * BPW + i) * (int)qrs + lane_col) * 2);
-    auto tile_offsets = [&](int q0, uint32_t (&off)[BPW]) {
-        const uint32_t cap = ((uint32_t)(p.seq - 1 - q0) * (uint32_t)qrs + (uint32_t)lane_col) * 2u;
-#pragma unroll
-        for (int i = 0; i < BPW; i++) off[i] = min(full_off[i], cap);
-    };
+    const char* qgb = reinterpret_cast<const char*>(qg);
+    const char* ogb = reinterpret_cast<const char*>(og);
+    const char* lgb = reinterpret_cast<const char*>((wv == 0 ? p.lse : p.delta) + lrow_base);
+    const uint32_t sq0 = lds_offset(sQ) + (uint32_t)(wv * BPW * BSTRIDE * 2);
+    const uint32_t so0 = lds_offset(sO) + (uint32_t)(wv * BPW * BSTRIDE * 2);
+    const uint32_t sl0 = lds_offset(wv == 0 ? &sL[0][0] : &sD[0][0]);
     auto set_loads = [&](Pos xq, int qbuf, Pos xo, int obuf, int dbuf) {
         Loads l;
-        l.q = qg + (long)xq.q0 * qrs + (long)xq.h * DP;
-        l.o = og + (long)xo.q0 * qrs + (long)xo.h * DP;
-        tile_offsets(xq.q0, l.qoff);
-        tile_offsets(xo.q0, l.ooff);
+        l.q = buf_rsrc(qgb + xq.qo, (uint32_t)(p.seq - xq.q0) * qo_row);
+        l.o = buf_rsrc(ogb + xo.qo, (uint32_t)(p.seq - xo.q0) * qo_row);
         const Pos xl = wv == 0 ? xq : xo;
-        l.ld = (wv == 0 ? p.lse : p.delta) + lrow_base + (long)xl.h * p.seq;
-        l.lvoff = (uint32_t)(min(xl.q0 + lrow, p.seq - 1) * 4);
-        l.qbuf = qbuf;
-        l.obuf = obuf;
-        l.lbuf = wv == 0 ? qbuf : dbuf;
+        l.l = buf_rsrc(lgb + xl.lo, (uint32_t)(p.seq - xl.q0) * 4u);
+        l.qlds = sq0 + (uint32_t)(qbuf * TSZ * 2);
+        l.olds = so0 + (uint32_t)(obuf * TSZ * 2);
+        l.llds = sl0 + (uint32_t)((wv == 0 ? qbuf : dbuf) * BM * 4);
         return l;
     };
     // Load i of this wave's share: Q blocks, dO blocks, then lse / delta.
     auto issue_load = [&](int i, const Loads& l) {
         if (i < BPW) {
-            lds_load16_sv(l.q, l.qoff[i], sQ + l.qbuf * TSZ + (wv * BPW + i) * BSTRIDE);
+            lds_buf_load16(l.q, tile_off[i], l.qlds + (uint32_t)(i * BSTRIDE * 2));
         } else if (i < 2 * BPW) {
-            lds_load16_sv(l.o, l.ooff[i - BPW], sO + l.obuf * TSZ + (wv * BPW + i - BPW) * BSTRIDE);
+            lds_buf_load16(l.o, tile_off[i - BPW], l.olds + (uint32_t)((i - BPW) * BSTRIDE * 2));
         } else {
-            lds_load4_sv(l.ld, l.lvoff, wv == 0 ? sL[l.lbuf] : sD[l.lbuf]);
+            lds_buf_load4(l.l, row_off, l.llds);
         }
     };
     auto issue_all = [&](const Loads& l, auto n) {
@@ -307,6 +341,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // them.
     auto acc_drain = [&](f32x16 (&acc)[NDB][NKB]) {
         asm volatile("s_waitcnt vmcnt(0)\n\ts_nop 15\n\ts_nop 15\n\ts_nop 3"
+                     : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[1][0]), "+a"(acc[1][1]), "+a"(acc[2][0]),
+                       "+a"(acc[2][1]), "+a"(acc[3][0]), "+a"(acc[3][1]));
+    };
+    // The same 34 wait states without the load wait, at the end of every
+    // iteration of the loops over a wave's steps (masked steps, the full
+    // run, masked steps): the compiler may keep the accumulators in other
+    // registers in each loop and copy them across on leaving it, and it
+    // cannot see that the MFMAs right before such a copy (inline assembly)
+    // are still writing them.  Copies for a loop's exit come after the
+    // iteration's last instruction.
+    auto acc_settle = [&](f32x16 (&acc)[NDB][NKB]) {
+        asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 3"
                      : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[1][0]), "+a"(acc[1][1]), "+a"(acc[2][0]),
                        "+a"(acc[2][1]), "+a"(acc[3][0]), "+a"(acc[3][1]));
     };
@@ -430,7 +476,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // block issue until the pipe frees).  EARLY: step t + 1 is full too,
         // and its S of block 0 and first softmax quarter are formed here.
         auto full_step = [&](auto early_tag, int qbuf, int obuf, int pbuf, int nqbuf, const Loads& ld,
-                             const PState& in, PState& out) {
+                             const PState& in, PState& out, auto&& adv) {
             constexpr bool EARLY = decltype(early_tag)::value;
             const bf16_bits* Qs = sQ + qbuf * TSZ;
             const bf16_bits* Qn = sQ + nqbuf * TSZ;  // Q of step t + 1
@@ -510,43 +556,73 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 if (kb == 0 && o + LA < 2 * NDB) tr[o + LA] = rd_tr(Os, 1, o + LA);
                 mfma_acc(acc[o >> 1][kb], tr[o], kb == 0 ? p10[o & 1] : p11[o & 1]);
                 if (EARLY) sm(k, sn0, out.lv0, out.p00, 0, 0, false);
+                adv(k);
                 CF_FENCE();
             }
         };
 
         Pos cur = first, n1 = next_pos(first), n2 = next_pos(n1);
         int qbuf = 0, obuf = 0, dbuf = 0;  // buffers of the current step
-        if (pos_full(cur)) prime(qbuf, st0);
-        // Step s with state `in` (formed by the previous step), forming `out`.
-        auto step = [&](int s, const PState& in, PState& out) {
-            const int pbuf = s & 1;
-            const int nqbuf = (qbuf + 1) & 3, lqbuf = (qbuf + 2) & 3;
-            const int nobuf = obuf ^ 1, ndbuf = dbuf == 2 ? 0 : dbuf + 1;
-            // Loads of interval s: Q of step s + 2, dO of step s + 1 (a step
-            // past the last reloads step s, unused).
-            const Loads ld = set_loads(s + 2 < n_steps ? n2 : cur, lqbuf, s + 1 < n_steps ? n1 : cur, nobuf, ndbuf);
-            const bool full = pos_full(cur);
-            const bool next_full = s + 1 < n_steps && pos_full(n1);
-            if (full && next_full) {
-                full_step(std::true_type{}, qbuf, obuf, pbuf, nqbuf, ld, in, out);
-            } else if (full) {
-                full_step(std::false_type{}, qbuf, obuf, pbuf, nqbuf, ld, in, out);
-            } else {
-                issue_all(ld, std::integral_constant<int, kLoadsP>{});
-                if (pos_act(cur)) masked_step(cur, qbuf, obuf, pbuf);
-                if (next_full) prime(nqbuf, out);
+        // The current step's loads: Q of the step two ahead, dO of the next
+        // one (past the last step, the cursors' restarted walk: loaded,
+        // unused).
+        Loads ld = set_loads(n2, 2, n1, 1, 1);
+        // Part k of moving the bookkeeping above on to the next step; a full
+        // step spreads the parts over the slots of its last region (whose
+        // MFMAs leave issue slots free), after its own loads are issued.
+        auto adv = [&](int k) {
+            if (k == 1) {
+                cur = n1;
+                n1 = n2;
             }
-            step_barrier();
-            cur = n1;
-            n1 = n2;
-            n2 = next_pos(n2);
-            qbuf = nqbuf;
-            obuf = nobuf;
-            dbuf = ndbuf;
+            if (k == 3) n2 = next_pos(n2);
+            if (k == 5) {
+                qbuf = (qbuf + 1) & 3;
+                obuf ^= 1;
+                dbuf = dbuf == 2 ? 0 : dbuf + 1;
+            }
+            if (k == 7) ld = set_loads(n2, (qbuf + 2) & 3, n1, obuf ^ 1, dbuf == 2 ? 0 : dbuf + 1);
         };
-        for (int s = 0; s < n_steps; s += 2) {
-            step(s, st0, st1);
-            if (s + 1 < n_steps) step(s + 1, st1, st0);
+        // Step s outside the full run; the one right before it forms the
+        // run's first state (in st0).
+        auto masked = [&](int s) {
+            issue_all(ld, std::integral_constant<int, kLoadsP>{});
+            if (pos_act(cur)) masked_step(cur, qbuf, obuf, s & 1);
+            if (s + 1 == s_full0) prime((qbuf + 1) & 3, st0);
+#pragma unroll
+            for (int k = 0; k < 2 * NKD; k++) adv(k);
+            step_barrier();
+        };
+        // Step s of the full run with state `in`, forming `out` if the next
+        // step is in the run too (EARLY).
+        auto full = [&](auto early, int s, const PState& in, PState& out) {
+            full_step(early, qbuf, obuf, s & 1, (qbuf + 1) & 3, ld, in, out, adv);
+            step_barrier();
+        };
+        if (s_full0 == 0 && s_full1 > 0) prime(qbuf, st0);
+        int s = 0;
+        for (; s < s_full0; s++) {
+            masked(s);
+            acc_settle(acc);
+        }
+        for (; s + 2 < s_full1; s += 2) {
+            full(std::true_type{}, s, st0, st1);
+            full(std::true_type{}, s + 1, st1, st0);
+            acc_settle(acc);
+        }
+        if (s + 1 < s_full1) {
+            full(std::true_type{}, s, st0, st1);
+            full(std::false_type{}, s + 1, st1, st0);
+            acc_settle(acc);
+            s += 2;
+        } else if (s < s_full1) {
+            full(std::false_type{}, s, st0, st1);
+            acc_settle(acc);
+            s++;
+        }
+        for (; s < n_steps; s++) {
+            masked(s);
+            acc_settle(acc);
         }
         acc_drain(acc);
         store_rows(p.dv, acc, false);
@@ -642,7 +718,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // step t + 1, in regions R1-R4 (see the file header).  Step t is
         // unmasked and step t + 1 active.
         auto full_iter = [&](Pos x, int qbuf, int pbuf, int nobuf, int ndbuf, const Loads& ld, const DState& in,
-                             DState& out) {
+                             DState& out, auto&& adv) {
             const bf16_bits* Qs = sQ + qbuf * TSZ;
             const bf16_bits* On = sO + nobuf * TSZ;  // dO of step t + 1
             bf16x8 orow[NKD], tr[2 * NDB];
@@ -721,6 +797,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 if constexpr (WDS) {
                     if (k == 0) store_piece(7);
                 }
+                adv(k);
                 CF_FENCE();
             }
         };
@@ -728,37 +805,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // Interval 0: dP - delta of step 0 and this wave's loads of interval
         // 0 (Q of step 2, dO of step 1).
         Pos cur = first, n1 = next_pos(first), n2 = next_pos(n1), n3 = next_pos(n2);
-        issue_all(set_loads(n_steps > 2 ? n2 : first, 2, n_steps > 1 ? n1 : first, 1, 1),
+        issue_all(set_loads(n2, 2, n1, 1, 1),
                   std::integral_constant<int, kLoadsDs>{});
         if (pos_act(cur)) dp_of(0, 0, st0);
         // Iteration s runs in interval s + 1, whose loads are Q of step s + 3
-        // and dO of step s + 2.
+        // and dO of step s + 2 (past the last step, the cursors' restarted
+        // walk: loaded, unused).
         int qbuf = 0, dbuf = 0;  // buffers of step s
-        auto iter = [&](int s, const DState& in, DState& out) {
-            step_barrier();
-            const int pbuf = s & 1;
-            const int nobuf = (s + 1) & 1, ndbuf = dbuf == 2 ? 0 : dbuf + 1;
-            const int lqbuf = (qbuf + 3) & 3, lobuf = s & 1, ldbuf = ndbuf == 2 ? 0 : ndbuf + 1;
-            const Loads ld = set_loads(s + 3 < n_steps ? n3 : cur, lqbuf, s + 2 < n_steps ? n2 : cur, lobuf, ldbuf);
-            const bool act = pos_act(cur);
-            const bool act_n = s + 1 < n_steps && pos_act(n1);
-            if (act && act_n && pos_full(cur)) {
-                full_iter(cur, qbuf, pbuf, nobuf, ndbuf, ld, in, out);
-            } else {
-                issue_all(ld, std::integral_constant<int, kLoadsDs>{});
-                if (act) ds_dk(cur, qbuf, pbuf, !pos_full(cur), in);
-                if (act_n) dp_of(nobuf, ndbuf, out);
+        Loads ld = set_loads(n3, 3, n2, 0, 2);
+        // Part k of moving the bookkeeping above on to the next iteration
+        // (spread over the last region's slots in a full iteration).
+        auto adv = [&](int s, int k) {
+            if (k == 1) {
+                cur = n1;
+                n1 = n2;
+                n2 = n3;
             }
-            cur = n1;
-            n1 = n2;
-            n2 = n3;
-            n3 = next_pos(n3);
-            qbuf = (qbuf + 1) & 3;
-            dbuf = ndbuf;
+            if (k == 3) n3 = next_pos(n3);
+            if (k == 5) {
+                qbuf = (qbuf + 1) & 3;
+                dbuf = dbuf == 2 ? 0 : dbuf + 1;
+            }
+            if (k == 7) ld = set_loads(n3, (qbuf + 3) & 3, n2, (s + 1) & 1, dbuf == 2 ? 1 : dbuf == 1 ? 0 : 2);
         };
-        for (int s = 0; s < n_steps; s += 2) {
-            iter(s, st0, st1);
-            if (s + 1 < n_steps) iter(s + 1, st1, st0);
+        // Iterations of the pipelined path: step s is full and step s + 1
+        // active, that is s in [s_full0, s_ds1).  Past the run the next step
+        // is masked (active: it is the diagonal tile or the cut last tile)
+        // unless the run ends the walk.
+        const int s_ds1 = s_full1 < n_steps ? s_full1 : s_full1 - 1;
+        // Iteration s outside that range: dS of step s from the state in
+        // st0, the state of step s + 1 formed in st1 and moved to st0.
+        auto masked = [&](int s) {
+            step_barrier();
+            const int ndbuf = dbuf == 2 ? 0 : dbuf + 1;
+            issue_all(ld, std::integral_constant<int, kLoadsDs>{});
+            if (pos_act(cur)) ds_dk(cur, qbuf, s & 1, !pos_full(cur), st0);
+            if (s + 1 < n_steps && pos_act(n1)) {
+                dp_of((s + 1) & 1, ndbuf, st1);
+                st0 = st1;
+            }
+#pragma unroll
+            for (int k = 0; k < 2 * NKD; k++) adv(s, k);
+        };
+        auto full = [&](int s, const DState& in, DState& out) {
+            step_barrier();
+            const int ndbuf = dbuf == 2 ? 0 : dbuf + 1;
+            full_iter(cur, qbuf, s & 1, (s + 1) & 1, ndbuf, ld, in, out, [&](int k) { adv(s, k); });
+        };
+        int s = 0;
+        for (; s < s_full0; s++) {
+            masked(s);
+            acc_settle(acc);
+        }
+        for (; s + 1 < s_ds1; s += 2) {
+            full(s, st0, st1);
+            full(s + 1, st1, st0);
+            acc_settle(acc);
+        }
+        if (s < s_ds1) {
+            full(s, st0, st1);
+            acc_settle(acc);
+            st0 = st1;
+            s++;
+        }
+        for (; s < n_steps; s++) {
+            masked(s);
+            acc_settle(acc);
         }
         acc_drain(acc);
         store_rows(p.dk, acc, true);
@@ -771,7 +883,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             issue_all(l0, std::integral_constant<int, kLoadsP>{});
         else
             issue_all(l0, std::integral_constant<int, kLoadsDs>{});
-        const Loads l1 = set_loads(n_steps > 1 ? next_pos(first) : first, 1, first, 0, 0);
+        const Loads l1 = set_loads(next_pos(first), 1, first, 0, 0);
 #pragma unroll
         for (int i = 0; i < BPW; i++) issue_load(i, l1);
         if (wv == 0) issue_load(2 * BPW, l1);

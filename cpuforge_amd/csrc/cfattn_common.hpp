@@ -295,6 +295,38 @@ __device__ __forceinline__ void lds_load4_sv(const void* sbase, uint32_t voff, c
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));
     asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
+// The same with the LDS destination given as a byte address (M0).
+__device__ __forceinline__ void lds_load16_so(const void* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+                 "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+__device__ __forceinline__ void lds_load4_so(const void* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase),
+                 "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+// A raw buffer resource (gfx9 layout: 48-bit base, stride 0, num_records,
+// 32-bit untyped data format): loads at byte offsets at or past num_records
+// return zeros and access no memory.
+typedef int32_t BufRsrc __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ BufRsrc buf_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    BufRsrc r;
+    r[0] = (int32_t)(uint32_t)a;
+    r[1] = (int32_t)(uint32_t)(a >> 32);
+    r[2] = (int32_t)bytes;
+    r[3] = 0x00020000;
+    return r;
+}
+// 64 lanes x 16 bytes from a buffer (lane byte offset voff) to 1 KiB of LDS
+// at byte address lds (M0), and the same for 4 bytes per lane.
+__device__ __forceinline__ void lds_buf_load16(const BufRsrc& r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r),
+                 "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+__device__ __forceinline__ void lds_buf_load4(const BufRsrc& r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r),
+                 "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
 // 64 lanes x 4 bytes to 256 consecutive bytes of LDS (one float per lane).
 __device__ __forceinline__ void lds_load4_asm(const void* g, const void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_offset(lds));

@@ -325,6 +325,30 @@ def test_f32_fast_path_is_bitwise_repeatable(cf):
         assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("ds", ["stored", "recompute"])
+@pytest.mark.parametrize("shape", [(1, 1000, 8, 2, 128), (1, 1024, 8, 2, 128), (2, 300, 4, 4, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_bf16_backward_is_bitwise_repeatable(cf, shape, ds):
+    """The bf16 backward (one-wave-per-SIMD dK/dV, stored or recomputed dQ)
+    four times on the same inputs gives the same bits: every sum has a fixed
+    order, and the dK/dV accumulators are never read while an MFMA is still
+    writing them (small grids, where one workgroup runs alone on its CU and
+    the P waves pass each barrier last, are the timing that showed such a
+    read)."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    print(f"bf16 backward repeat, shape {shape}, dS {ds}", flush=True)
+    _, (q, k, v, g) = _fast_inputs(shape, seed=2100)
+    o, lse = D.fwd(q, k, v, ctx=ctx)
+    with _DsLimit(ctx, ctx.ds_limit if ds == "stored" else 0):
+        runs = [[x.cpu().numpy() for x in D.bwd(g, q, k, v, o, lse, ctx=ctx)] for _ in range(4)]
+    torch.cuda.synchronize()
+    for r in runs[1:]:
+        for name, a, b in zip(("dq", "dk", "dv"), runs[0], r):
+            assert np.array_equal(a, b), f"{shape} {ds} {name}: max diff {np.abs(a - b).max()}"
+
+
 @pytest.mark.parametrize("shape", [(8, 512, 9, 3, 64), (1, 2048, 4, 1, 128), (1, 1000, 8, 8, 64)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_f32_key_split_matches_oracle_and_unsplit(cf, shape):
