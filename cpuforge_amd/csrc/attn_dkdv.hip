@@ -130,6 +130,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int b = rest / p.nkv;
     const int wg_key0 = kvt * p.kv_tile;
     const int key0 = wg_key0 + pair * 64;
+    // key0 as a scalar, for addresses (the branch conditions keep the
+    // per-lane form, with which the compiler allocates registers better).
+    const int key0s = wg_key0 + (wv & 1) * 64;
     const bool pair_live = key0 < p.seq;
 
     const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
@@ -201,9 +204,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // and the run itself through the pipelined one, with no per-step branch.
     int s_full0 = 0, s_full1 = 0;
     {
-        const int k0 = wg_key0 + (wv & 1) * 64;  // key0, as a scalar
-        const int t_lo = max((k0 + 63 + BM - 1) / BM, qt_begin), t_hi = p.seq / BM - 1;
-        if (k0 < p.seq && t_lo <= t_hi) {
+        const int t_lo = max((key0s + 63 + BM - 1) / BM, qt_begin), t_hi = p.seq / BM - 1;
+        if (key0s < p.seq && t_lo <= t_hi) {
             s_full0 = (down ? n_qt - 1 - t_hi : t_lo - qt_begin) * p.group;
             s_full1 = (down ? n_qt - t_lo : t_hi + 1 - qt_begin) * p.group;
         }
@@ -675,6 +677,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v),
                                         reinterpret_cast<u32x4*>(const_cast<char*>(base) + (h ? ds_off1 : ds_off0)));
         };
+        // The same for a full step, from the step's block (query block 0,
+        // key block 0) address: key block kb is the next block, query block
+        // 1 starts qi + 1 blocks on (its row of the triangle is one longer).
+        constexpr uint32_t kDsBytes = kDsBlock * sizeof(bf16_bits);
+        auto ds_row_base = [&](Pos x) {
+            const uint32_t qi = (uint32_t)x.q0 >> 5, ki = (uint32_t)key0s >> 5;
+            const uint32_t blk = ((uint32_t)b * (uint32_t)p.nh + (uint32_t)x.h) * (uint32_t)p.ds_ntri +
+                                 qi * (qi + 1) / 2 + ki;
+            return reinterpret_cast<const char*>(p.ds) + (size_t)blk * kDsBytes;
+        };
+        auto ds_store_at = [&](const char* base, int kb, int h, const bf16x8& v) {
+            __builtin_nontemporal_store(
+                __builtin_bit_cast(u32x4, v),
+                reinterpret_cast<u32x4*>(const_cast<char*>(base) + kb * kDsBytes + (h ? ds_off1 : ds_off0)));
+        };
 
         // delta - dP of the step whose dS comes next, by query block and key
         // block: the products with the negated V^T operands accumulated onto
@@ -717,8 +734,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // Iteration t (interval t + 1): dS and dK of step t, dP - delta of
         // step t + 1, in regions R1-R4 (see the file header).  Step t is
         // unmasked and step t + 1 active.
-        auto full_iter = [&](Pos x, int qbuf, int pbuf, int nobuf, int ndbuf, const Loads& ld, const DState& in,
-                             DState& out, auto&& adv) {
+        auto full_iter = [&](Pos x, const char* dsb, int qbuf, int pbuf, int nobuf, int ndbuf, const Loads& ld,
+                             const DState& in, DState& out, auto&& adv) {
             const bf16_bits* Qs = sQ + qbuf * TSZ;
             const bf16_bits* On = sO + nobuf * TSZ;  // dO of step t + 1
             bf16x8 orow[NKD], tr[2 * NDB];
@@ -731,9 +748,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 if ((e & 7) == 7) dd[kb][e >> 3] = cvt_bf16x8(&ds[kb][e & 8]);
             };
             // Piece i of the step's stored dS: (qb, kb, half) = (i / 4, (i / 2) % 2, i % 2).
+            const char* dsq1 = dsb + ((uint32_t)(x.q0 >> 5) + 1u) * kDsBytes;  // query block 1
             auto store_piece = [&](int i) {
                 const int sq = i >> 2, skb = (i >> 1) & 1, sh = i & 1;
-                ds_store(x, sq, skb, sh, sq ? d1[skb][sh] : d0[skb][sh], false);
+                ds_store_at(sq ? dsq1 : dsb, skb, sh, sq ? d1[skb][sh] : d0[skb][sh]);
             };
             f32x16 dl = delta16(ndbuf, 0);
 #pragma unroll
@@ -813,6 +831,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // walk: loaded, unused).
         int qbuf = 0, dbuf = 0;  // buffers of step s
         Loads ld = set_loads(n3, 3, n2, 0, 2);
+        const char* dsb = WDS ? ds_row_base(cur) : nullptr;  // stored-dS address of step s (full steps)
         // Part k of moving the bookkeeping above on to the next iteration
         // (spread over the last region's slots in a full iteration).
         auto adv = [&](int s, int k) {
@@ -827,6 +846,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 dbuf = dbuf == 2 ? 0 : dbuf + 1;
             }
             if (k == 7) ld = set_loads(n3, (qbuf + 3) & 3, n2, (s + 1) & 1, dbuf == 2 ? 1 : dbuf == 1 ? 0 : 2);
+            if (WDS && k == 9) dsb = ds_row_base(cur);
         };
         // Iterations of the pipelined path: step s is full and step s + 1
         // active, that is s in [s_full0, s_ds1).  Past the run the next step
@@ -850,7 +870,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         auto full = [&](int s, const DState& in, DState& out) {
             step_barrier();
             const int ndbuf = dbuf == 2 ? 0 : dbuf + 1;
-            full_iter(cur, qbuf, s & 1, (s + 1) & 1, ndbuf, ld, in, out, [&](int k) { adv(s, k); });
+            full_iter(cur, dsb, qbuf, s & 1, (s + 1) & 1, ndbuf, ld, in, out, [&](int k) { adv(s, k); });
         };
         int s = 0;
         for (; s < s_full0; s++) {
