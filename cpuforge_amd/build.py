@@ -19,7 +19,7 @@ INCLUDE = os.path.join(ROOT, "include")
 OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcfattn.so")
 
-HIP_SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "attn_dkdv.hip", "attn_f32.hip", "prologue.hip", "layer_ops.hip", "lora.hip",
+HIP_SOURCES = ["attn_fwd.hip", "attn_fwd_q64.hip", "attn_bwd.hip", "attn_dkdv.hip", "attn_f32.hip", "prologue.hip", "layer_ops.hip", "lora.hip",
                "io_kernels.hip", "noalloc.hip", "cfattn_capi.cpp", "cfops_capi.cpp", "cfio_capi.cpp", "host_stage.cpp"]
 ARCH = "gfx950"
 COMMON = ["-std=c++17", "-fPIC", "-O3", f"--offload-arch={ARCH}", f"-I{INCLUDE}", f"-I{CSRC}",
@@ -30,7 +30,8 @@ COMMON = ["-std=c++17", "-fPIC", "-O3", f"--offload-arch={ARCH}", f"-I{INCLUDE}"
 # accumulators are kept in AGPRs by inline assembly).  Left to choose, the
 # compiler puts every MFMA of that one-wave-per-SIMD kernel in the AGPR form
 # and copies the scores and accumulators between the two files each step.
-EXTRA = {"attn_dkdv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+EXTRA = {"attn_dkdv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+         "attn_fwd_q64.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc() -> str:

@@ -58,40 +58,11 @@
 #include "cfattn_common.hpp"
 #include "attn_params.hpp"
 #include "attn_bwd_common.hpp"
+#include "mfma_asm.hpp"
 
 #include <type_traits>
 
 namespace cfattn {
-
-namespace {
-
-// No instruction is scheduled across this point.
-#define CF_FENCE() __builtin_amdgcn_sched_barrier(0)
-// A fence with two wait states in it: the operand registers a VALU
-// instruction wrote just before must not be read by an MFMA issued from
-// inline assembly (which the compiler's hazard checks do not see) in the
-// next two cycles.
-#define CF_HAZARD_FENCE()                  \
-    do {                                   \
-        __builtin_amdgcn_sched_barrier(0); \
-        asm volatile("s_nop 1");           \
-        __builtin_amdgcn_sched_barrier(0); \
-    } while (0)
-
-// acc += a * b with acc held in AGPRs for the whole kernel.  Inline assembly
-// because the compiler gives every MFMA of a function one register form,
-// and this kernel needs its score products (read by VALU code) in VGPRs and
-// its long-lived accumulators (read only at the end) in AGPRs.  Back-to-back
-// MFMAs accumulating into the same registers need no wait states; the
-// operands' hazards are covered by CF_HAZARD_FENCE and the final read by
-// acc_drain.
-__device__ __forceinline__ void mfma_acc(f32x16& acc, const bf16x8& a, const bf16x8& b) {
-    asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-}
-// Keeps a value in AGPRs from here on (ties its registers to an empty asm).
-__device__ __forceinline__ void agpr_pin(f32x16& acc) { asm volatile("" : "+a"(acc)); }
-
-}  // namespace
 
 template <bool WDS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_bwd_dkdv_k64_kernel(
@@ -354,9 +325,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // are still writing them.  Copies for a loop's exit come after the
     // iteration's last instruction.
     auto acc_settle = [&](f32x16 (&acc)[NDB][NKB]) {
-        asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 3"
-                     : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[1][0]), "+a"(acc[1][1]), "+a"(acc[2][0]),
-                       "+a"(acc[2][1]), "+a"(acc[3][0]), "+a"(acc[3][1]));
+        acc_wait8(acc[0][0], acc[0][1], acc[1][0], acc[1][1], acc[2][0], acc[2][1], acc[3][0], acc[3][1]);
     };
     // dV rows are added; dK rows (scaled: dS was accumulated without the
     // softmax scale) go through the epilogue mode.
@@ -526,7 +495,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 const int o = k >> 1, kb = k & 1;
                 if (kb == 0 && o + LA < 2 * NDB) tr[o + LA] = rd_tr(Os, 0, o + LA);
                 if (EARLY && (k & 3) == 1 && (k >> 2) < LA) qr[k >> 2] = rd_row(Qn, 0, k >> 2);
-                mfma_acc(acc[o >> 1][kb], tr[o], kb == 0 ? in.p00[o & 1] : p01[o & 1]);
+                // The step's first MFMA into each accumulator waits for a
+                // copy the compiler may place right before it.
+                if ((o & 1) == 0)
+                    mfma_acc_lead(acc[o >> 1][kb], tr[o], kb == 0 ? in.p00[o & 1] : p01[o & 1]);
+                else
+                    mfma_acc(acc[o >> 1][kb], tr[o], kb == 0 ? in.p00[o & 1] : p01[o & 1]);
                 sm(k, s1[0], lv1, p10, 1, 0, true);
                 if (k == 0) issue_load(NKD, ld);
                 CF_FENCE();
@@ -916,9 +890,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     else
         run_ds();
 }
-
-#undef CF_FENCE
-#undef CF_HAZARD_FENCE
 
 void launch_attn_bwd_dkdv_k64(const BwdParams& p, bool wds, hipStream_t st) {
     if (wds)

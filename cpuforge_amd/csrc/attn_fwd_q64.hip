@@ -1,0 +1,442 @@
+// Causal GQA attention forward on gfx950: bf16 inputs at head_dim 128, fp32
+// accumulation, one wave per SIMD.
+//
+// Reference semantics (crates/core/src/ops/attention.rs:46-122): per query
+// head h and token t,
+//   O[t,h]   = sum_{j<=t} softmax_j(q_t . k_j / sqrt(D)) v_j   (overwritten)
+//   lse[h,t] = max_j s_tj + ln sum_j exp(s_tj - max)            (overwritten)
+// with KV head g = h / group serving `group` consecutive query heads.
+//
+// A workgroup is four waves, one per SIMD; each wave owns 64 queries (two
+// 32-query blocks, A and B) of one head, and the workgroup hpw heads x
+// 4 / hpw such query tiles of one GQA group.  K and V tiles of 64 keys are
+// loaded once into LDS for the four waves.  Holding 64 queries, a wave
+// uses every K or V operand it reads from LDS for two MFMAs (one per query
+// block) -- half the LDS bytes per product of the two-waves-per-SIMD kernel
+// (attn_fwd_bf16_kernel), whose register budget holds 32 queries per wave.
+// Per key tile, per wave:
+//   S^T = K Q^T   (32 MFMAs, Q^T of both blocks held in registers),
+//   online softmax in the exp2 domain (running max m per query, moved
+//   lazily: only when a tile's max exceeds it by more than kLazyRescaleQ,
+//   which keeps every P below 2^8), P^T rounded to bf16,
+//   O^T += V^T P^T (32 MFMAs, O^T in AGPRs, V^T read transposed).
+//
+// Interval t (between barriers t - 1 and t) runs two regions of 32 MFMAs:
+//   X  S of tile t (both blocks)        | P of tile t - 1: block B, and
+//                                         block A's second key block
+//   Y  O += V^T P^T of tile t - 1       | row max of tile t, then P of its
+//                                         block A, first key block
+// so that the softmax of one tile issues in the shadow of the products of
+// the next (one wave hides only about five other instructions per
+// 32x32x16 MFMA).  Tile t's K is read in X(t), its V in Y(t + 1): loads of
+// K(t + 1) and V(t) are issued in X(t) into the buffer pair the interval
+// before last read.  The key tile on the wave's diagonal is the last one
+// it computes (its scores masked where the key follows the query); tiles
+// past it are only loaded, for the workgroup's other waves.
+#include "cfattn_common.hpp"
+#include "attn_params.hpp"
+#include "cfattn_kernels.hpp"
+#include "mfma_asm.hpp"
+
+namespace cfattn {
+
+// The running max moves only when a tile's max exceeds it by more than this
+// (log2 units): P <= 2^8, exact in fp32 sums, and O^T (in AGPRs) is
+// rescaled a few times per query row instead of every tile.
+constexpr float kLazyRescaleQ = 8.0f;
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_fwd_q64_kernel(
+    const FwdParams p) {
+    constexpr int DP = 128, BN = 64, BQ = 64;
+    constexpr int CPR = DP / 8;  // 16-byte chunks per row
+    using L = BlkTile<DP, BN>;
+    constexpr int NBL = L::NB;  // 1 KiB load blocks per tile
+    constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16, TSZ = L::SIZE;
+    constexpr int BPW = NBL / 4;  // blocks of each tile one wave loads
+    constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32;
+    // K row / V^T operands are read this many operands ahead of their MFMAs.
+    constexpr int LA = 3;
+    __shared__ __attribute__((aligned(16))) bf16_bits sK[2 * TSZ];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV[2 * TSZ];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = wave_uniform(tid >> 6);
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    const int id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
+    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;  // longest tiles first
+    int rest = id / p.n_ttiles;
+    const int sub = rest % p.n_sub;
+    rest /= p.n_sub;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+    const int head = g * p.group + sub * p.hpw + wv % p.hpw;
+    const int TT = BQ * p.tpw;
+    const int t0 = tile * TT + (wv / p.hpw) * BQ;  // the wave's first query
+    const int wg_end = min(p.seq, tile * TT + TT);
+    const int n_kt = (wg_end + BN - 1) / BN;  // key tiles the workgroup loads
+    const bool active = t0 < p.seq;
+    const int dt = t0 / BN;  // the wave's diagonal tile; tiles before it are full
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const char* kgb = reinterpret_cast<const char*>(static_cast<const bf16_bits*>(p.k) + (long)b * p.kv_bs + (long)g * DP);
+    const char* vgb = reinterpret_cast<const char*>(static_cast<const bf16_bits*>(p.v) + (long)b * p.kv_bs + (long)g * DP);
+
+    // Q^T operands: query t0 + 32*qb + l32, head dims hh*HALF + kd*8 + [0, 8);
+    // queries past the end are zero (their results are not stored).
+    bf16x8 qf[2][NKD];
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+        const int tq = t0 + qb * 32 + l32;
+        const bf16_bits* qrow =
+            static_cast<const bf16_bits*>(p.q) + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP + hh * HALF;
+#pragma unroll
+        for (int kd = 0; kd < NKD; kd++) {
+            const uint4 u = tq < p.seq ? *reinterpret_cast<const uint4*>(qrow + kd * 8) : make_uint4(0, 0, 0, 0);
+            qf[qb][kd] = __builtin_bit_cast(bf16x8, u);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+
+    // Tile loads: wave w fills blocks w*BPW.. of a K and a V tile, lane l of
+    // block bk reading chunk l % CPR of tile row bk + NB*(l / CPR), through a
+    // bounds-checked buffer that starts at the tile and ends with the
+    // sequence (keys past the end read zeros; the mask removes them).
+    uint32_t tile_off[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; i++)
+        tile_off[i] = (uint32_t)(((NBL * (lane / CPR) + wv * BPW + i) * (int)kvrs + (lane % CPR) * 8) * 2);
+    const uint32_t kv_row = (uint32_t)kvrs * 2u;  // bytes per key row
+    const uint32_t sk0 = lds_offset(sK) + (uint32_t)(wv * BPW * BSTRIDE * 2);
+    const uint32_t sv0 = lds_offset(sV) + (uint32_t)(wv * BPW * BSTRIDE * 2);
+    auto tile_rsrc = [&](const char* base, int kt) {
+        return buf_rsrc(base + (uint32_t)(kt * BN) * kv_row, (uint32_t)(p.seq - kt * BN) * kv_row);
+    };
+    // Load i (< 2 * BPW) of interval t: K(t + 1) blocks, then V(t) blocks.
+    auto issue_load = [&](int i, const BufRsrc& rk, const BufRsrc& rv, int t) {
+        if (i < BPW)
+            lds_buf_load16(rk, tile_off[i], sk0 + (uint32_t)(((t + 1) & 1) * TSZ * 2 + i * BSTRIDE * 2));
+        else
+            lds_buf_load16(rv, tile_off[i - BPW], sv0 + (uint32_t)((t & 1) * TSZ * 2 + (i - BPW) * BSTRIDE * 2));
+    };
+    // Interval t's loads, all at once (intervals outside the pipelined run).
+    auto issue_all = [&](int t) {
+        if (t + 1 < n_kt) {
+            const BufRsrc rk = tile_rsrc(kgb, t + 1);
+#pragma unroll
+            for (int i = 0; i < BPW; i++) issue_load(i, rk, rk, t);
+        }
+        if (t < n_kt) {
+            const BufRsrc rv = tile_rsrc(vgb, t);
+#pragma unroll
+            for (int i = BPW; i < 2 * BPW; i++) issue_load(i, rv, rv, t);
+        }
+    };
+    auto barrier = [&]() {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    // Row reads (K): lane (l32, hh) reads MFMA row l32 (key qperm(l32)),
+    // chunks hh*NKD + kd.  Transposed reads (V^T): in each 16-lane group G,
+    // lane 4k + m supplies head dims 16*(G%2) + 4m + [0, 4) of MFMA row
+    // 4*hh + k (+8, +16, +24), that is tile row 4k + hh (+2, +16, +18).
+    const int rrow = L::row(qperm(l32)) + hh * HALF;
+    const int G = lane >> 4, jj = lane & 15;
+    const int trow = L::row(4 * (jj >> 2) + hh) + 16 * (G & 1) + 4 * (jj & 3);
+    // K operand o (kd = o / 2, key block kb = o % 2) of the K tile at Ks.
+    auto rd_k = [&](const bf16_bits* Ks, int o) {
+        return __builtin_bit_cast(bf16x8,
+                                  *reinterpret_cast<const uint4*>(Ks + rrow + (o & 1) * 2 * ROW16 + (o >> 1) * 8));
+    };
+    // V^T operand o (key block kb = o / 8, 16-key half h = (o / 4) % 2,
+    // head-dim block db = o % 4) of the V tile at Vs: each P^T operand
+    // (kb, h) is used by four consecutive operands, so it is free as soon
+    // as the next tile's replaces it.
+    auto rd_v = [&](const bf16_bits* Vs, int o) {
+        const bf16_bits* t = Vs + trow + (o >> 3) * 2 * ROW16 + (o & 3) * 32 + ((o >> 2) & 1) * ROW16;
+        return join_bf16x4(ds_read_tr16(t), ds_read_tr16(t + 2 * BSTRIDE));
+    };
+
+    f32x16 oacc[2][NDB];  // O^T of blocks A and B, in AGPRs
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+        for (int db = 0; db < NDB; db++) {
+            oacc[qb][db] = zero16();
+            agpr_pin(oacc[qb][db]);
+        }
+    auto acc_ready = [&]() {
+        acc_ready8(oacc[0][0], oacc[0][1], oacc[0][2], oacc[0][3], oacc[1][0], oacc[1][1], oacc[1][2], oacc[1][3]);
+    };
+    auto acc_wait = [&]() {
+        acc_wait8(oacc[0][0], oacc[0][1], oacc[0][2], oacc[0][3], oacc[1][0], oacc[1][1], oacc[1][2], oacc[1][3]);
+    };
+    float m2[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.0f, 0.0f};
+    bool resc[2] = {false, false};  // block's O^T waits for a rescale by alpha
+    float alpha[2] = {1.0f, 1.0f};
+
+    // Scores of a tile kt, [qb][kb]: keys kt*BN + kb*32 + qperm(MFMA row) x
+    // the block's 32 queries (lanes); two sets, for even and odd tiles (X
+    // forms one while block B of the other is still turned into P).  The
+    // diagonal tile masks keys after the query (element r: MFMA row
+    // (r/4)*8 + hh*4 + r%4).
+    f32x16 s0[2][2], s1[2][2];
+    bf16x8 pA[2][2], pB[2][2];  // P^T operands [kb][half] of the previous tile
+    auto mask_diag = [&](f32x16 (&sc)[2][2]) {
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int key = kb * 32 + qperm((r >> 2) * 8 + hh * 4 + (r & 3));
+                    if (key > qb * 32 + l32) sc[qb][kb][r] = -INFINITY;
+                }
+    };
+    // Row max of the tile's scores: partial maxima over eight elements at a
+    // time (part j of 8: block j / 4, key block (j / 2) % 2, half j % 2),
+    // then per block the max over the lane halves and the lazy move of m.
+    float mxp[2];
+    auto max_part = [&](const f32x16 (&sc)[2][2], int j) {
+        const int qb = j >> 2, kb = (j >> 1) & 1, r0 = (j & 1) * 8;
+        float mx = (j & 3) == 0 ? -INFINITY : mxp[qb];
+#pragma unroll
+        for (int r = 0; r < 8; r++) mx = fmaxf(mx, sc[qb][kb][r0 + r]);
+        mxp[qb] = mx;
+    };
+    auto max_final = [&](int qb) {
+        const float mx = max_halves(mxp[qb]) * p.sl2;
+        const float mnew = mx > m2[qb] + kLazyRescaleQ ? mx : m2[qb];
+        const float a = __builtin_amdgcn_exp2f(m2[qb] - mnew);
+        lsum[qb] *= a;
+        resc[qb] = __any(mnew != m2[qb]);
+        alpha[qb] = a;
+        m2[qb] = mnew;
+    };
+    // P of element r of a 16-element score block s (block qb); after every
+    // eighth element its bf16 operand and their sum into the row sum (pr:
+    // the block's staging, one per block so that the two blocks' elements
+    // interleave).  The row sum adds the bf16 values the products use, two
+    // per instruction (v_dot2 with (1, 1)): O is normalised by the sum of
+    // exactly the weights in its numerator.
+    float prA[8], prB[8];
+    const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
+    auto p_elem = [&](const f32x16& s, int r, int qb, bf16x8 (&pq)[2]) {
+        float* pr = qb == 0 ? prA : prB;
+        pr[r & 7] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], p.sl2, -m2[qb]));
+        if ((r & 7) == 7) {
+            const bf16x8 v = cvt_bf16x8(pr);
+            pq[r >> 3] = v;
+            float l = lsum[qb];
+#pragma unroll
+            for (int i = 0; i < 4; i++) l = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[2 * i], v[2 * i + 1]}, ones2, l, false);
+            lsum[qb] = l;
+        }
+    };
+    // O^T of the blocks waiting for a rescale (after their last products).
+    auto rescale = [&]() {
+        if (resc[0] || resc[1]) {
+            acc_wait();
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++)
+                if (resc[qb]) {
+#pragma unroll
+                    for (int db = 0; db < NDB; db++) {
+                        oacc[qb][db] *= alpha[qb];
+                        agpr_pin(oacc[qb][db]);
+                    }
+                }
+            resc[0] = resc[1] = false;
+        }
+    };
+
+    // X(t): S of tile t into sc in 32 slots (K operand o = j / 2 for blocks
+    // A, B), P of block B of tile t - 1 (scores sp) one element per slot,
+    // interval t's loads in the odd slots of the first half.
+    auto region_x = [&](auto prev_tag, const bf16_bits* Ks, int t, const BufRsrc& rk, const BufRsrc& rv,
+                        f32x16 (&sc)[2][2], const f32x16 (&sp)[2][2]) {
+        constexpr bool PREV = decltype(prev_tag)::value;
+        bf16x8 kr[NKD * 2];
+#pragma unroll
+        for (int o = 0; o < LA; o++) kr[o] = rd_k(Ks, o);
+        CF_FENCE();
+#pragma unroll
+        for (int j = 0; j < 4 * NKD; j++) {
+            const int o = j >> 1, qb = j & 1, kd = o >> 1, kb = o & 1;
+            // The MFMA first, then the slot's other work in its shadow.
+            sc[qb][kb] = mfma32(kr[o], qf[qb][kd], kd == 0 ? zero16() : sc[qb][kb]);
+            CF_FENCE();
+            if (qb == 0 && o + LA < 2 * NKD) kr[o + LA] = rd_k(Ks, o + LA);
+            if (PREV) {
+                p_elem(sp[1][j >> 4], j & 15, 1, pB[j >> 4]);
+                if ((j & 1) == 0) p_elem(sp[0][1], j >> 1, 0, pA[1]);
+            }
+            if ((j & 1) && j < 2 * 2 * BPW) issue_load(j >> 1, rk, rv, t);
+            CF_FENCE();
+        }
+        // Used here: the P above is first used in Y, past the diagonal
+        // tile's mask branch, and would otherwise be moved there.
+        if (PREV) {
+            const float l0 = lsum[0], l1 = lsum[1];
+            asm volatile("" ::"v"(pA[1][0]), "v"(pA[1][1]), "v"(pB[0][0]), "v"(pB[0][1]), "v"(pB[1][0]),
+                         "v"(pB[1][1]), "v"(l0), "v"(l1));
+        }
+    };
+    // Y(t): O^T += V^T P^T of tile t - 1 (V operand o = j / 2 for blocks
+    // A, B); the row max of tile t (scores sc) and P of its block A.
+    auto region_y = [&](auto prev_tag, auto next_tag, const bf16_bits* Vs, const f32x16 (&sc)[2][2]) {
+        constexpr bool PREV = decltype(prev_tag)::value, NEXT = decltype(next_tag)::value;
+        bf16x8 vt[4 * NDB];
+        if (PREV) {
+#pragma unroll
+            for (int o = 0; o < LA; o++) vt[o] = rd_v(Vs, o);
+            acc_ready();
+        }
+        CF_HAZARD_FENCE();
+#pragma unroll
+        for (int j = 0; j < 8 * NDB; j++) {
+            const int o = j >> 1, qb = j & 1, kb = o >> 3, h = (o >> 2) & 1, db = o & 3;
+            if (PREV) {
+                mfma_acc(oacc[qb][db], vt[o], qb == 0 ? pA[kb][h] : pB[kb][h]);
+                CF_FENCE();
+                if (qb == 0 && o + LA < 4 * NDB) vt[o + LA] = rd_v(Vs, o + LA);
+            }
+            if (NEXT) {
+                if (j < 8) max_part(sc, j);
+                if (j == 8) max_final(0);
+                if (j == 9) max_final(1);
+                if (j >= 10 && j < 26) p_elem(sc[0][0], j - 10, 0, pA[0]);
+            }
+            CF_FENCE();
+        }
+        // Used here, so that block A's P stays in the slots above: its first
+        // use is in the next interval, past the rescale branch, and the
+        // compiler would otherwise move it there, out of the MFMAs' shadow.
+        if (NEXT) {
+            const float l0 = lsum[0];
+            asm volatile("" ::"v"(pA[0][0]), "v"(pA[0][1]), "v"(l0));
+        }
+    };
+    // Interval t (1 <= t <= dt): S(t) into sc with P of block B of tile
+    // t - 1 (scores sp), then the products of tile t - 1 with the max and
+    // block A's P of tile t.
+    auto interval = [&](int t, f32x16 (&sc)[2][2], const f32x16 (&sp)[2][2]) {
+        const bf16_bits* Ks = sK + (t & 1) * TSZ;
+        const bf16_bits* Vs = sV + ((t - 1) & 1) * TSZ;
+        // Past the last tile the K loads reload tile t into the free buffer.
+        const BufRsrc rk = tile_rsrc(kgb, t + 1 < n_kt ? t + 1 : t), rv = tile_rsrc(vgb, t);
+        region_x(std::true_type{}, Ks, t, rk, rv, sc, sp);
+        if (t == dt) mask_diag(sc);
+        region_y(std::true_type{}, std::true_type{}, Vs, sc);
+        rescale();
+        barrier();
+    };
+
+    // ---------------------------------------------------------------- walk
+    // Interval 0 needs K(0).
+    {
+        const BufRsrc rk = tile_rsrc(kgb, 0);
+#pragma unroll
+        for (int i = 0; i < BPW; i++) lds_buf_load16(rk, tile_off[i], sk0 + (uint32_t)(i * BSTRIDE * 2));
+    }
+    barrier();
+    // The wave computes tiles 0..dt in intervals 0..dt + 1; the workgroup
+    // runs n_kt + 1 intervals (its last wave's).
+    const int n_int = n_kt + 1;
+    int t = 0;
+    if (active) {
+        // Interval 0: S(0) (into s0), its max and block A's P.
+        {
+            const BufRsrc rk = tile_rsrc(kgb, 1 < n_kt ? 1 : 0), rv = tile_rsrc(vgb, 0);
+            region_x(std::false_type{}, sK, 0, rk, rv, s0, s1);
+            if (dt == 0) mask_diag(s0);
+            region_y(std::false_type{}, std::true_type{}, sV, s0);
+            resc[0] = resc[1] = false;  // O^T is still zero
+            barrier();
+            t = 1;
+        }
+        // Intervals 1..dt, two per iteration (odd t forms s1, even t s0).
+        for (; t + 1 <= dt; t += 2) {
+            interval(t, s1, s0);
+            interval(t + 1, s0, s1);
+            acc_wait();
+        }
+        if (t <= dt) {
+            // One interval left (t odd): tile dt's scores to s1, then moved
+            // to s0 for the last interval.
+            interval(t, s1, s0);
+            acc_wait();
+#pragma unroll
+            for (int qb = 0; qb < 2; qb++)
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++) s0[qb][kb] = s1[qb][kb];
+            t++;
+        }
+        // Interval dt + 1: P of block B and the products of the diagonal tile
+        // (its scores in sl).
+        auto last = [&](const f32x16 (&sl)[2][2]) {
+            const bf16_bits* Vs = sV + ((t - 1) & 1) * TSZ;
+#pragma unroll
+            for (int j = 0; j < 32; j++) {
+                p_elem(sl[1][j >> 4], j & 15, 1, pB[j >> 4]);
+                if ((j & 1) == 0) p_elem(sl[0][1], j >> 1, 0, pA[1]);
+            }
+            issue_all(t);
+            region_y(std::true_type{}, std::false_type{}, Vs, sl);
+            acc_wait();
+            barrier();
+        };
+        last(s0);
+        t++;
+    }
+    for (; t < n_int; t++) {
+        issue_all(t);
+        barrier();
+    }
+    if (!active) return;
+
+    // O = O^T / l per query, lse = (m + log2 l) ln 2.
+    acc_wait();
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+        const int tq = t0 + qb * 32 + l32;
+        const float ltot = sum_halves(lsum[qb]);
+        if (tq >= p.seq) continue;
+        const float inv = 1.0f / ltot;
+        float* orow = p.o + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
+#pragma unroll
+        for (int db = 0; db < NDB; db++) {
+#pragma unroll
+            for (int rq = 0; rq < 4; rq++) {
+                const int d0 = db * 32 + rq * 8 + hh * 4;
+                *reinterpret_cast<float4*>(orow + d0) =
+                    make_float4(oacc[qb][db][rq * 4 + 0] * inv, oacc[qb][db][rq * 4 + 1] * inv,
+                                oacc[qb][db][rq * 4 + 2] * inv, oacc[qb][db][rq * 4 + 3] * inv);
+            }
+        }
+        if (hh == 0) p.lse[((long)b * p.nh + head) * p.seq + tq] = (m2[qb] + __log2f(ltot)) * kLn2;
+    }
+}
+
+// The kernel's grid for dims d: hpw heads x 4 / hpw 64-query tiles per
+// workgroup.
+bool attn_fwd_q64_applies(const Dims& d, bool vec_ok, bool o_vec_ok) {
+    return d.hd == 128 && vec_ok && o_vec_ok;
+}
+
+hipError_t launch_attn_fwd_q64(const Dims& d, FwdParams p, hipStream_t st, KernelTimer* tm) {
+    p.hpw = p.group % 4 == 0 ? 4 : p.group % 2 == 0 ? 2 : 1;
+    p.tpw = 4 / p.hpw;
+    p.n_sub = p.group / p.hpw;
+    p.n_ttiles = (d.seq + 64 * p.tpw - 1) / (64 * p.tpw);
+    const long n_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+    if (n_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    p.n_wg = (int)n_wg;
+    TimedLaunch tl(tm, kKernFwd, st);
+    hipLaunchKernelGGL(attn_fwd_q64_kernel, dim3(p.n_wg), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
+}  // namespace cfattn

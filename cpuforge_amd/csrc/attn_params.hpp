@@ -81,5 +81,10 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStr
 // bf16 dK/dV at head_dim 128, one wave per SIMD (attn_dkdv.hip); with
 // `wds` it also stores dS for the stored-dS dQ kernel.  p.kv_tile is 128.
 void launch_attn_bwd_dkdv_k64(const BwdParams& p, bool wds, hipStream_t st);
+// bf16 forward at head_dim 128, one wave per SIMD (attn_fwd_q64.hip): 16-byte
+// aligned rows.  Sets the grid fields of p (heads and query tiles per
+// workgroup) itself.
+bool attn_fwd_q64_applies(const Dims& d, bool vec_ok, bool o_vec_ok);
+hipError_t launch_attn_fwd_q64(const Dims& d, FwdParams p, hipStream_t st, KernelTimer* tm);
 
 }  // namespace cfattn

@@ -17,6 +17,7 @@
 namespace cfattn {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint16_t bf16_bits;  // bf16 values live in memory as raw 16-bit patterns
 

@@ -141,6 +141,10 @@ struct cfattn_ctx {
         // (bitwise equal results; kept for comparison and measurement).
         const char* v = std::getenv("CFATTN_DKDV_KERNEL");
         if (v && std::strcmp(v, "ws") == 0) t.dkdv_variant = cfattn::kDkdvWaveSpecialised;
+        // CFATTN_FWD_KERNEL=two selects the two-waves-per-SIMD bf16 forward
+        // at head_dim 128 (kept for comparison and measurement).
+        const char* f = std::getenv("CFATTN_FWD_KERNEL");
+        if (f && std::strcmp(f, "two") == 0) t.fwd_variant = cfattn::kFwdTwoPerSimd;
         return t;
     }
 };

@@ -42,6 +42,12 @@ enum DkdvVariant {
     kDkdvWaveSpecialised = 1    // two waves per SIMD, 32 keys per wave (same results, bit for bit)
 };
 
+// Forward kernel of the bf16 fast path at head_dim 128.
+enum FwdVariant {
+    kFwdAuto = 0,        // one wave per SIMD, 64 queries per wave
+    kFwdTwoPerSimd = 1   // two waves per SIMD, 32 queries per wave
+};
+
 // Tuning knobs of one launch; defaults are chosen by the launchers.
 struct Tuning {
     int xcd_remap = 1;  // XCD-aware workgroup ordering
@@ -49,6 +55,7 @@ struct Tuning {
     int fwd_tblocks_per_wg = 0;
     int bwd_kv_waves = 0;
     int dkdv_variant = kDkdvAuto;
+    int fwd_variant = kFwdAuto;
     KernelTimer* timer = nullptr;
 };
 
