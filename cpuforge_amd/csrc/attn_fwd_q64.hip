@@ -45,8 +45,47 @@ namespace cfattn {
 // rescaled a few times per query row instead of every tile.
 constexpr float kLazyRescaleQ = 8.0f;
 
+__device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_bits* sK, bf16_bits* sV);
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_fwd_q64_kernel(
     const FwdParams p) {
+    constexpr int TSZ = BlkTile<128, 64>::SIZE;
+    __shared__ __attribute__((aligned(16))) bf16_bits sK[2 * TSZ];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV[2 * TSZ];
+
+    // Items (query tiles) of this workgroup.  Persistent grid: the XCD of
+    // workgroup w (w % 8; the dispatcher deals workgroups round robin)
+    // takes a contiguous run of the items, so that its L2 holds few KV
+    // heads, and its xcd_wgs workgroups walk the run zig-zag (positions l,
+    // 2W - 1 - l, 2W + l, ...): with the items of a run longest first this
+    // gives every workgroup nearly the same number of key tiles.
+    const int xq = blockIdx.x % 8, xl = blockIdx.x / 8;
+    int run0 = 0, run_n = 1;
+    if (p.xcd_wgs > 0) {
+        const int q = p.n_items / 8, r = p.n_items % 8;
+        run0 = xq < r ? xq * (q + 1) : r * (q + 1) + (xq - r) * q;
+        run_n = q + (xq < r ? 1 : 0);
+    }
+    for (int it = 0;; it++) {
+        int id;
+        if (p.xcd_wgs > 0) {
+            const int W = p.xcd_wgs;
+            const int pos = (it >> 1) * 2 * W + ((it & 1) ? 2 * W - 1 - xl : xl);
+            if (pos >= run_n) break;
+            id = run0 + pos;
+        } else {
+            if (it > 0) break;
+            id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
+        }
+        q64_item(p, id, sK, sV);
+    }
+}
+
+// One item: a query tile of hpw heads x 4 / hpw 64-query blocks of one GQA
+// group.  Every wave of the workgroup passes the same number of barriers;
+// after the last one no wave reads the K/V tiles, so the next item may
+// load into them.
+__device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_bits* sK, bf16_bits* sV) {
     constexpr int DP = 128, BN = 64, BQ = 64;
     constexpr int CPR = DP / 8;  // 16-byte chunks per row
     using L = BlkTile<DP, BN>;
@@ -56,14 +95,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32;
     // K row / V^T operands are read this many operands ahead of their MFMAs.
     constexpr int LA = 3;
-    __shared__ __attribute__((aligned(16))) bf16_bits sK[2 * TSZ];
-    __shared__ __attribute__((aligned(16))) bf16_bits sV[2 * TSZ];
-
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = wave_uniform(tid >> 6);
     const int l32 = lane & 31, hh = lane >> 5;
 
-    const int id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
     const int tile = p.n_ttiles - 1 - id % p.n_ttiles;  // longest tiles first
     int rest = id / p.n_ttiles;
     const int sub = rest % p.n_sub;
@@ -96,7 +131,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             qf[qb][kd] = __builtin_bit_cast(bf16x8, u);
         }
     }
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    // (The first barrier waits for these loads and K(0)'s together.)
 
     // Tile loads: wave w fills blocks w*BPW.. of a K and a V tile, lane l of
     // block bk reading chunk l % CPR of tile row bk + NB*(l / CPR), through a
@@ -431,9 +466,23 @@ hipError_t launch_attn_fwd_q64(const Dims& d, FwdParams p, hipStream_t st, Kerne
     p.tpw = 4 / p.hpw;
     p.n_sub = p.group / p.hpw;
     p.n_ttiles = (d.seq + 64 * p.tpw - 1) / (64 * p.tpw);
-    const long n_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
-    if (n_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
-    p.n_wg = (int)n_wg;
+    const long n_items = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
+    if (n_items > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    p.n_items = (int)n_items;
+    // One workgroup per CU (the kernel's registers allow no second) when
+    // the items fill every CU at least once, in whole XCDs; else one
+    // workgroup per item.
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return hipErrorInvalidDevice;
+    if (p.xcd && cus >= 8 && cus % 8 == 0 && n_items >= cus) {
+        p.xcd_wgs = cus / 8;
+        p.n_wg = cus;
+    } else {
+        p.xcd_wgs = 0;
+        p.n_wg = p.n_items;
+    }
     TimedLaunch tl(tm, kKernFwd, st);
     hipLaunchKernelGGL(attn_fwd_q64_kernel, dim3(p.n_wg), dim3(256), 0, st, p);
     return hipGetLastError();

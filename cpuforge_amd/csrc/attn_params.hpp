@@ -20,6 +20,9 @@ struct FwdParams {
     float sl2;  // softmax scale * log2(e)
     long q_bs, kv_bs;
     int vec_ok, o_vec_ok, xcd;
+    // Persistent grid of the bf16 head_dim 128 kernel: n_items query tiles,
+    // xcd_wgs workgroups per XCD (0: one item per workgroup).
+    int n_items, xcd_wgs;
     // Key split of the fp32 kernel (0: none): a query tile's key tiles are
     // cut into runs of `ksplit`, one workgroup each; `units` workgroups per
     // (sequence, KV head, head subset).  Split s of a row writes its
