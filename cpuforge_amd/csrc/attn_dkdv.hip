@@ -426,6 +426,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             f32x16 s01;
             float lv0[16];
             bf16x8 p00[2];
+            bf16x8 q1[LA];  // the first row operands of (t, block 1), read before barrier t - 1
         };
         PState st0, st1;
         // Forms the state of full step x (unscheduled: after a masked step).
@@ -440,6 +441,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             o.p00[0] = cvt_bf16x8(&pr[0]);
             o.p00[1] = cvt_bf16x8(&pr[8]);
             o.s01 = sc[1];
+#pragma unroll
+            for (int i = 0; i < LA; i++) o.q1[i] = rd_row(sQ + qbuf * TSZ, 1, i);
         };
 
         // Full step t in regions R1-R4, fenced in slots of one MFMA and the
@@ -469,8 +472,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             // R1: S of (t, 1) | softmax (t, 0, 1); P (t, 0, 0) published;
             // lse of block 1 (read here, scaled one element per slot); this
             // interval's loads.
+            // The first row operands came with the state (read in the
+            // previous step's last region); lse is scaled from slot 4 on, so
+            // that the first MFMAs wait for no LDS read.
 #pragma unroll
-            for (int i = 0; i < LA; i++) qr[i] = rd_row(Qs, 1, i);
+            for (int i = 0; i < LA; i++) qr[i] = in.q1[i];
             lse_raw(sL[qbuf], 1, lv1);
             publish(pbuf, 0, 0, in.p00);
             CF_FENCE();
@@ -478,7 +484,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int k = 0; k < 2 * NKD; k++) {
                 const int kd = k >> 1, kb = k & 1;
                 if (kb == 0 && kd + LA < NKD) qr[kd + LA] = rd_row(Qs, 1, kd + LA);
-                lv1[k] *= kLog2e;
+                if (k >= 4) lv1[k - 4] *= kLog2e;
                 if (k >= 2 * NKD - LA) tr[k - (2 * NKD - LA)] = rd_tr(Os, 0, k - (2 * NKD - LA));
                 s1[kb] = mfma32(qr[kd], xf[kb][kd], kd == 0 ? zero16() : s1[kb]);
                 sm(k, in.s01, in.lv0, p01, 0, 1, true);
@@ -501,6 +507,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     mfma_acc_lead(acc[o >> 1][kb], tr[o], kb == 0 ? in.p00[o & 1] : p01[o & 1]);
                 else
                     mfma_acc(acc[o >> 1][kb], tr[o], kb == 0 ? in.p00[o & 1] : p01[o & 1]);
+                if (k < 4) lv1[12 + k] *= kLog2e;
                 sm(k, s1[0], lv1, p10, 1, 0, true);
                 if (k == 0) issue_load(NKD, ld);
                 CF_FENCE();
@@ -532,6 +539,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 if (kb == 0 && o + LA < 2 * NDB) tr[o + LA] = rd_tr(Os, 1, o + LA);
                 mfma_acc(acc[o >> 1][kb], tr[o], kb == 0 ? p10[o & 1] : p11[o & 1]);
                 if (EARLY) sm(k, sn0, out.lv0, out.p00, 0, 0, false);
+                // The next step's first row operands: Q(t + 1) is complete
+                // since barrier t - 1.
+                if (EARLY && k >= 2 * NKD - 2 * LA && (k & 1)) out.q1[(k - (2 * NKD - 2 * LA)) >> 1] = rd_row(Qn, 1, (k - (2 * NKD - 2 * LA)) >> 1);
                 adv(k);
                 CF_FENCE();
             }
