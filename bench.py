@@ -263,13 +263,23 @@ def fused_timing(cfg, mode, steps, warmup):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    # Per-kernel times over `steps` untimed steps; the timed steps bracket
+    # the dK/dV kernel only, as the attention step's timing does.
+    ctx.profile_select(None)
+    ctx.profile_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    kernels = {n: round(ms / max(1, c), 4) for n, (ms, c) in ctx.profile_read().items() if c}
+    ctx.profile_enable(False)
+    ctx.profile_select(["attn_bwd_dkdv"])
     ctx.profile_enable(True)
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     per = (time.perf_counter() - t0) / steps
-    kernels = {n: round(ms / max(1, c), 4) for n, (ms, c) in ctx.profile_read().items() if c}
+    ctx.profile_enable(False)
     ctx.close()
     del q_pre, k_pre, v, d_o, dq_pre, dk_pre, dv, pr
     torch.cuda.empty_cache()
@@ -580,6 +590,19 @@ def attn_timing(cfg, mode, steps, warmup, ctx, traffic_file, copy_probe):
     torch.cuda.synchronize()
     print(f"bench: {cfg} {mode} warmup done ({warmup} steps)", file=sys.stderr, flush=True)
 
+    # Per-kernel times: every launch bracketed by the library's hipEvents,
+    # over `steps` steps before the timed ones.  The brackets add queue time
+    # between the kernels, so the timed steps bracket only the kernel that
+    # takes the most time (the roofline's), whose duration comes from them.
+    ctx.profile_select(None)
+    ctx.profile_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    every = {n: (t / c if c else 0.0, c) for n, (t, c) in ctx.profile_read().items() if c}
+    ctx.profile_enable(False)
+    dom = max((n for n in every if n in ALGO_UNITS), key=lambda n: every[n][0] * every[n][1])
+    ctx.profile_select([dom])
     ctx.profile_enable(True)
     stream = torch.cuda.current_stream()
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -594,14 +617,15 @@ def attn_timing(cfg, mode, steps, warmup, ctx, traffic_file, copy_probe):
     wall = time.perf_counter() - w0
     prof = ctx.profile_read()
     ctx.profile_enable(False)
+    ctx.profile_select(None)
     gpu_ms = ev0.elapsed_time(ev1)
     ms_per_step = max(gpu_ms, wall * 1e3) / steps
     flops = 7.0 * B * Hq * D * S * (S + 1)
     tflops = flops / (ms_per_step * 1e-3) / 1e12
     print(f"bench: {cfg} {mode} timed {steps} steps, {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
 
-    kernels = {n: (t / c if c else 0.0, c) for n, (t, c) in prof.items() if c}
-    dom = max((n for n in kernels if n in ALGO_UNITS), key=lambda n: kernels[n][0] * kernels[n][1])
+    kernels = dict(every)
+    kernels[dom] = (prof[dom][0] / prof[dom][1], prof[dom][1])  # from the timed steps
     dom_ms = kernels[dom][0]
     dom_flops = ALGO_UNITS[dom] * B * Hq * D * S * (S + 1)
     achieved = dom_flops / (dom_ms * 1e-3) / 1e12

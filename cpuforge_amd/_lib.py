@@ -64,6 +64,7 @@ SIGNATURES = {
     "cfattn_set_ds_limit": (C.c_int, [_vp, _sz]),
     "cfattn_get_ds_limit": (_sz, [_vp]),
     "cfattn_profile_enable": (C.c_int, [_vp, C.c_int]),
+    "cfattn_profile_select": (C.c_int, [_vp, C.c_uint]),
     "cfattn_profile_read": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]),
     "cfattn_kernel_name": (C.c_char_p, [C.c_int]),
     "cfattn_kernel_count": (C.c_int, []),

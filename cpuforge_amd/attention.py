@@ -94,6 +94,20 @@ class Context:
         stream (enabling again resets the totals)."""
         _lib.check(self._lib.cfattn_profile_enable(self.handle, int(bool(on))), self.handle)
 
+    def profile_select(self, names=None) -> None:
+        """Bracket only the named kernels ("attn_bwd_dkdv", ...) while
+        profiling; None selects every kernel."""
+        if names is None:
+            mask = 0xFFFFFFFF
+        else:
+            ids = {self._lib.cfattn_kernel_name(k).decode(): k for k in range(self._lib.cfattn_kernel_count())}
+            mask = 0
+            for n in names:
+                if n not in ids:
+                    raise ValueError(f"unknown kernel {n!r}")
+                mask |= 1 << ids[n]
+        _lib.check(self._lib.cfattn_profile_select(self.handle, mask), self.handle)
+
     def profile_read(self) -> dict:
         """{kernel name: (total ms, launches)} since profiling was enabled."""
         out = {}

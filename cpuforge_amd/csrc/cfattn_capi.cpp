@@ -620,10 +620,20 @@ int cfattn_profile_enable(cfattn_ctx* c, int on) {
         if (!c->timer) c->timer = new EventTimer();
         (void)c->timer->collect();
         c->timer->reset();
+        c->timer->mask = c->prof_mask;
     } else if (c->timer) {
         delete c->timer;
         c->timer = nullptr;
     }
+    return CFATTN_OK;
+}
+
+int cfattn_profile_select(cfattn_ctx* c, unsigned kernel_mask) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    c->prof_mask = kernel_mask;
+    if (c->timer) c->timer->mask = kernel_mask;
     return CFATTN_OK;
 }
 

@@ -31,6 +31,7 @@ struct EventTimer final : cfattn::KernelTimer {
     double total_ms[cfattn::kNumKernels] = {};
     long long launches[cfattn::kNumKernels] = {};
     hipError_t err = hipSuccess;
+    unsigned mask = ~0u;  // kernel ids bracketed (bit k: kernel k)
 
     hipEvent_t take() {
         if (!pool.empty()) {
@@ -44,6 +45,11 @@ struct EventTimer final : cfattn::KernelTimer {
         return r == hipSuccess ? e : nullptr;
     }
     void begin(int kernel, hipStream_t st) override {
+        if (!((mask >> kernel) & 1u)) {
+            open_ev = nullptr;
+            open_kernel = -1;
+            return;
+        }
         open_ev = take();
         open_kernel = kernel;
         if (open_ev) {
@@ -112,6 +118,7 @@ struct cfattn_ctx {
     void* buf[NSLOT] = {};
     size_t cap[NSLOT] = {};
     EventTimer* timer = nullptr;  // non-null while profiling is on
+    unsigned prof_mask = ~0u;     // kernels profiling brackets (cfattn_profile_select)
     size_t ds_limit = (size_t)8 << 30;  // stored-dS scratch limit (cfattn_set_ds_limit)
     // GEMM library state of the layer ops (hipBLASLt handle and per-shape
     // plans), created on first use; released by cfattn_destroy through

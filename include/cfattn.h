@@ -213,6 +213,11 @@ size_t cfattn_get_ds_limit(const cfattn_ctx* ctx);
  * queues is bracketed by two hipEvents on the kernel's stream; enabling
  * again resets the totals.  Disable with on = 0. */
 int cfattn_profile_enable(cfattn_ctx* ctx, int on);
+/* Which kernels profiling brackets: bit k of kernel_mask for kernel id k
+ * (default: all).  Applies at once and to later profiling sessions; a
+ * kernel left out costs no events (each bracket adds a few microseconds of
+ * queue time to a step). */
+int cfattn_profile_select(cfattn_ctx* ctx, unsigned kernel_mask);
 /* Waits for the recorded launches and returns, for kernel id `kernel`
  * (0 .. cfattn_kernel_count()-1), the summed event time in milliseconds and
  * the number of launches since profiling was enabled. */
