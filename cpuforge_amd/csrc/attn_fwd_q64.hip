@@ -18,14 +18,15 @@
 //   S^T = K Q^T   (32 MFMAs, Q^T of both blocks held in registers),
 //   online softmax in the exp2 domain (running max m per query, moved
 //   lazily: only when a tile's max exceeds it by more than kLazyRescaleQ,
-//   which keeps every P below 2^8), P^T rounded to bf16,
+//   which keeps every P below 2^8; P is formed against m first and the
+//   tile's row sums tell whether its max could have moved), P^T rounded to
+//   bf16,
 //   O^T += V^T P^T (32 MFMAs, O^T in AGPRs, V^T read transposed).
 //
 // Interval t (between barriers t - 1 and t) runs two regions of 32 MFMAs:
-//   X  S of tile t (both blocks)        | P of tile t - 1: block B, and
-//                                         block A's second key block
-//   Y  O += V^T P^T of tile t - 1       | row max of tile t, then P of its
-//                                         block A, first key block
+//   X  S of tile t (both blocks)        | P of tile t - 1, block B; then
+//                                         tile t - 1's row-sum guard
+//   Y  O += V^T P^T of tile t - 1       | P of tile t, block A
 // so that the softmax of one tile issues in the shadow of the products of
 // the next (one wave hides only about five other instructions per
 // 32x32x16 MFMA).  Tile t's K is read in X(t), its V in Y(t + 1): loads of
@@ -209,8 +210,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
         acc_wait8(oacc[0][0], oacc[0][1], oacc[0][2], oacc[0][3], oacc[1][0], oacc[1][1], oacc[1][2], oacc[1][3]);
     };
     float m2[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.0f, 0.0f};
-    bool resc[2] = {false, false};  // block's O^T waits for a rescale by alpha
-    float alpha[2] = {1.0f, 1.0f};
+    float lpre[2];  // the row sums before the current tile's P was added
 
     // Scores of a tile kt, [qb][kb]: keys kt*BN + kb*32 + qperm(MFMA row) x
     // the block's 32 queries (lanes); two sets, for even and odd tiles (X
@@ -230,72 +230,90 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
                     if (key > qb * 32 + l32) sc[qb][kb][r] = -INFINITY;
                 }
     };
-    // Row max of the tile's scores: partial maxima over eight elements at a
-    // time (part j of 8: block j / 4, key block (j / 2) % 2, half j % 2),
-    // then per block the max over the lane halves and the lazy move of m.
-    float mxp[2];
-    auto max_part = [&](const f32x16 (&sc)[2][2], int j) {
-        const int qb = j >> 2, kb = (j >> 1) & 1, r0 = (j & 1) * 8;
-        float mx = (j & 3) == 0 ? -INFINITY : mxp[qb];
-#pragma unroll
-        for (int r = 0; r < 8; r++) mx = fmaxf(mx, sc[qb][kb][r0 + r]);
-        mxp[qb] = mx;
-    };
-    auto max_final = [&](int qb) {
-        const float mx = max_halves(mxp[qb]) * p.sl2;
-        const float mnew = mx > m2[qb] + kLazyRescaleQ ? mx : m2[qb];
-        const float a = __builtin_amdgcn_exp2f(m2[qb] - mnew);
-        lsum[qb] *= a;
-        resc[qb] = __any(mnew != m2[qb]);
-        alpha[qb] = a;
-        m2[qb] = mnew;
-    };
-    // P of element r of a 16-element score block s (block qb); after every
-    // eighth element its bf16 operand and their sum into the row sum (pr:
-    // the block's staging, one per block so that the two blocks' elements
-    // interleave).  The row sum adds the bf16 values the products use, two
-    // per instruction (v_dot2 with (1, 1)): O is normalised by the sum of
-    // exactly the weights in its numerator.
-    float prA[8], prB[8];
+    // P of a tile is formed against the running max m as it stands, with no
+    // row max first: the lazy rule moves m only when the tile's max exceeds
+    // it by more than kLazyRescaleQ, and while it does not, every P is at
+    // most 2^8 -- which the tile's row sum then shows.  Once the tile's P is
+    // summed, a lane whose share of it exceeds kGuard (or is not a number:
+    // the first tile, against m = -inf) sends the wave to `settle`, which
+    // takes the exact row max, applies the lazy rule and forms the tile's P
+    // again.  m moves exactly when the lazy rule says, so O, lse and every
+    // P are the same as with the max taken first.
+    constexpr float kGuard = 64.0f;
+    // P of element e of block qb's 32 (key block e / 16, element e % 16 of
+    // the score block) into the block's staging; the bf16 operands of the
+    // eight elements of group g and their sum into the row sum (two per
+    // v_dot2 with (1, 1), in element order: O is normalised by the sum of
+    // exactly the weights in its numerator) follow in `p_group`, a slot or
+    // more after the last of them.
+    float prA[16], prB[16];
     const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
-    auto p_elem = [&](const f32x16& s, int r, int qb, bf16x8 (&pq)[2]) {
+    auto p_elem = [&](const f32x16 (&sc)[2][2], int qb, int e) {
         float* pr = qb == 0 ? prA : prB;
-        pr[r & 7] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], p.sl2, -m2[qb]));
-        if ((r & 7) == 7) {
-            const bf16x8 v = cvt_bf16x8(pr);
-            pq[r >> 3] = v;
-            float l = lsum[qb];
+        pr[e & 15] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[qb][e >> 4][e & 15], p.sl2, -m2[qb]));
+    };
+    auto p_group = [&](int qb, int g, bf16x8 (&pq)[2][2]) {
+        const float* pr = qb == 0 ? prA : prB;
+        const bf16x8 v = cvt_bf16x8(&pr[(g & 1) * 8]);
+        pq[g >> 1][g & 1] = v;
+        float l = lsum[qb];
 #pragma unroll
-            for (int i = 0; i < 4; i++) l = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[2 * i], v[2 * i + 1]}, ones2, l, false);
-            lsum[qb] = l;
+        for (int i = 0; i < 4; i++) l = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[2 * i], v[2 * i + 1]}, ones2, l, false);
+        lsum[qb] = l;
+    };
+    // The slow path of the guard for tile scores sp (unscheduled; the first
+    // tile of every row takes it): per block, the exact row max, the lazy
+    // rule, the row sum restarted from lpre and, if m moved anywhere in the
+    // wave, O^T rescaled and the block's P formed again.
+    auto settle = [&](const f32x16 (&sp)[2][2]) {
+        acc_wait();
+#pragma unroll
+        for (int qb = 0; qb < 2; qb++) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) mx = fmaxf(mx, sp[qb][kb][r]);
+            mx = max_halves(mx) * p.sl2;
+            const float mnew = mx > m2[qb] + kLazyRescaleQ ? mx : m2[qb];
+            const float a = __builtin_amdgcn_exp2f(m2[qb] - mnew);
+            if (__any(mnew != m2[qb])) {
+                m2[qb] = mnew;
+                lsum[qb] = lpre[qb] * a;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) p_elem(sp, qb, g * 8 + e);
+                    if (qb == 0)
+                        p_group(0, g, pA);
+                    else
+                        p_group(1, g, pB);
+                }
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    oacc[qb][db] *= a;
+                    agpr_pin(oacc[qb][db]);
+                }
+            }
         }
     };
-    // O^T of the blocks waiting for a rescale (after their last products).
-    auto rescale = [&]() {
-        if (resc[0] || resc[1]) {
-            acc_wait();
-#pragma unroll
-            for (int qb = 0; qb < 2; qb++)
-                if (resc[qb]) {
-#pragma unroll
-                    for (int db = 0; db < NDB; db++) {
-                        oacc[qb][db] *= alpha[qb];
-                        agpr_pin(oacc[qb][db]);
-                    }
-                }
-            resc[0] = resc[1] = false;
-        }
+    // The guard, once the tile's P of both blocks is summed.
+    auto guard = [&](const f32x16 (&sp)[2][2]) {
+        const float da = lsum[0] - lpre[0], db = lsum[1] - lpre[1];
+        if (__any(!(da <= kGuard) || !(db <= kGuard))) settle(sp);
     };
 
     // X(t): S of tile t into sc in 32 slots (K operand o = j / 2 for blocks
-    // A, B), P of block B of tile t - 1 (scores sp) one element per slot,
-    // interval t's loads in the odd slots of the first half.
+    // A, B); P of block B of tile t - 1 (scores sp), one element per slot,
+    // each group's operand a slot after its last element; interval t's
+    // loads in the odd slots of the first half.
     auto region_x = [&](auto prev_tag, const bf16_bits* Ks, int t, const BufRsrc& rk, const BufRsrc& rv,
                         f32x16 (&sc)[2][2], const f32x16 (&sp)[2][2]) {
         constexpr bool PREV = decltype(prev_tag)::value;
         bf16x8 kr[NKD * 2];
 #pragma unroll
         for (int o = 0; o < LA; o++) kr[o] = rd_k(Ks, o);
+        if (PREV) lpre[1] = lsum[1];
         CF_FENCE();
 #pragma unroll
         for (int j = 0; j < 4 * NKD; j++) {
@@ -305,22 +323,20 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
             CF_FENCE();
             if (qb == 0 && o + LA < 2 * NKD) kr[o + LA] = rd_k(Ks, o + LA);
             if (PREV) {
-                p_elem(sp[1][j >> 4], j & 15, 1, pB[j >> 4]);
-                if ((j & 1) == 0) p_elem(sp[0][1], j >> 1, 0, pA[1]);
+                if (j > 0 && (j & 7) == 0) p_group(1, (j >> 3) - 1, pB);
+                p_elem(sp, 1, j);
             }
             if ((j & 1) && j < 2 * 2 * BPW) issue_load(j >> 1, rk, rv, t);
             CF_FENCE();
         }
-        // Used here: the P above is first used in Y, past the diagonal
-        // tile's mask branch, and would otherwise be moved there.
         if (PREV) {
-            const float l0 = lsum[0], l1 = lsum[1];
-            asm volatile("" ::"v"(pA[1][0]), "v"(pA[1][1]), "v"(pB[0][0]), "v"(pB[0][1]), "v"(pB[1][0]),
-                         "v"(pB[1][1]), "v"(l0), "v"(l1));
+            p_group(1, 3, pB);
+            guard(sp);
         }
     };
     // Y(t): O^T += V^T P^T of tile t - 1 (V operand o = j / 2 for blocks
-    // A, B); the row max of tile t (scores sc) and P of its block A.
+    // A, B); P of block A of tile t (scores sc), one element per slot, each
+    // group's operand once the products have read the previous tile's.
     auto region_y = [&](auto prev_tag, auto next_tag, const bf16_bits* Vs, const f32x16 (&sc)[2][2]) {
         constexpr bool PREV = decltype(prev_tag)::value, NEXT = decltype(next_tag)::value;
         bf16x8 vt[4 * NDB];
@@ -329,6 +345,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
             for (int o = 0; o < LA; o++) vt[o] = rd_v(Vs, o);
             acc_ready();
         }
+        if (NEXT) lpre[0] = lsum[0];
         CF_HAZARD_FENCE();
 #pragma unroll
         for (int j = 0; j < 8 * NDB; j++) {
@@ -339,24 +356,18 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
                 if (qb == 0 && o + LA < 4 * NDB) vt[o + LA] = rd_v(Vs, o + LA);
             }
             if (NEXT) {
-                if (j < 8) max_part(sc, j);
-                if (j == 8) max_final(0);
-                if (j == 9) max_final(1);
-                if (j >= 10 && j < 26) p_elem(sc[0][0], j - 10, 0, pA[0]);
+                // Group g of block A replaces operand pA[g / 2][g % 2], last
+                // read by the product in slot 8g + 6.
+                if (j > 0 && (j & 7) == 0) p_group(0, (j >> 3) - 1, pA);
+                p_elem(sc, 0, j);
             }
             CF_FENCE();
         }
-        // Used here, so that block A's P stays in the slots above: its first
-        // use is in the next interval, past the rescale branch, and the
-        // compiler would otherwise move it there, out of the MFMAs' shadow.
-        if (NEXT) {
-            const float l0 = lsum[0];
-            asm volatile("" ::"v"(pA[0][0]), "v"(pA[0][1]), "v"(l0));
-        }
+        if (NEXT) p_group(0, 3, pA);
     };
     // Interval t (1 <= t <= dt): S(t) into sc with P of block B of tile
-    // t - 1 (scores sp), then the products of tile t - 1 with the max and
-    // block A's P of tile t.
+    // t - 1 (scores sp) and the guard of tile t - 1, then the products of
+    // tile t - 1 with block A's P of tile t.
     auto interval = [&](int t, f32x16 (&sc)[2][2], const f32x16 (&sp)[2][2]) {
         const bf16_bits* Ks = sK + (t & 1) * TSZ;
         const bf16_bits* Vs = sV + ((t - 1) & 1) * TSZ;
@@ -365,7 +376,6 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
         region_x(std::true_type{}, Ks, t, rk, rv, sc, sp);
         if (t == dt) mask_diag(sc);
         region_y(std::true_type{}, std::true_type{}, Vs, sc);
-        rescale();
         barrier();
     };
 
@@ -382,13 +392,12 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
     const int n_int = n_kt + 1;
     int t = 0;
     if (active) {
-        // Interval 0: S(0) (into s0), its max and block A's P.
+        // Interval 0: S(0) (into s0) and block A's P.
         {
             const BufRsrc rk = tile_rsrc(kgb, 1 < n_kt ? 1 : 0), rv = tile_rsrc(vgb, 0);
             region_x(std::false_type{}, sK, 0, rk, rv, s0, s1);
             if (dt == 0) mask_diag(s0);
             region_y(std::false_type{}, std::true_type{}, sV, s0);
-            resc[0] = resc[1] = false;  // O^T is still zero
             barrier();
             t = 1;
         }
@@ -413,11 +422,14 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
         // (its scores in sl).
         auto last = [&](const f32x16 (&sl)[2][2]) {
             const bf16_bits* Vs = sV + ((t - 1) & 1) * TSZ;
+            lpre[1] = lsum[1];
 #pragma unroll
             for (int j = 0; j < 32; j++) {
-                p_elem(sl[1][j >> 4], j & 15, 1, pB[j >> 4]);
-                if ((j & 1) == 0) p_elem(sl[0][1], j >> 1, 0, pA[1]);
+                if (j > 0 && (j & 7) == 0) p_group(1, (j >> 3) - 1, pB);
+                p_elem(sl, 1, j);
             }
+            p_group(1, 3, pB);
+            guard(sl);
             issue_all(t);
             region_y(std::true_type{}, std::false_type{}, Vs, sl);
             acc_wait();
