@@ -297,11 +297,17 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
             }
         }
     };
-    // The guard, once the tile's P of both blocks is summed.
-    auto guard = [&](const f32x16 (&sp)[2][2]) {
+    // The guard, once the tile's P of both blocks is summed: whether this
+    // lane's share of either block's tile sum exceeds kGuard (or is not a
+    // number).
+    auto guard_test = [&]() {
         const float da = lsum[0] - lpre[0], db = lsum[1] - lpre[1];
-        if (__any(!(da <= kGuard) || !(db <= kGuard))) settle(sp);
+        return !(da <= kGuard) || !(db <= kGuard);
     };
+    auto guard = [&](const f32x16 (&sp)[2][2]) {
+        if (__any(guard_test())) settle(sp);
+    };
+    bool trip = false;
 
     // X(t): S of tile t into sc in 32 slots (K operand o = j / 2 for blocks
     // A, B); P of block B of tile t - 1 (scores sp), one element per slot,
@@ -323,16 +329,23 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
             CF_FENCE();
             if (qb == 0 && o + LA < 2 * NKD) kr[o + LA] = rd_k(Ks, o + LA);
             if (PREV) {
-                if (j > 0 && (j & 7) == 0) p_group(1, (j >> 3) - 1, pB);
-                p_elem(sp, 1, j);
+                // Elements 0-23 one per slot, 24-31 two per slot in 24-27;
+                // the last group's operand in slot 28 and the guard's test
+                // in slot 30, so that its branch waits for nothing.
+                if (j > 0 && (j & 7) == 0 && j <= 24) p_group(1, (j >> 3) - 1, pB);
+                if (j < 24) {
+                    p_elem(sp, 1, j);
+                } else if (j < 28) {
+                    p_elem(sp, 1, 24 + 2 * (j - 24));
+                    p_elem(sp, 1, 25 + 2 * (j - 24));
+                }
+                if (j == 28) p_group(1, 3, pB);
+                if (j == 30) trip = guard_test();
             }
             if ((j & 1) && j < 2 * 2 * BPW) issue_load(j >> 1, rk, rv, t);
             CF_FENCE();
         }
-        if (PREV) {
-            p_group(1, 3, pB);
-            guard(sp);
-        }
+        if (PREV && __any(trip)) settle(sp);
     };
     // Y(t): O^T += V^T P^T of tile t - 1 (V operand o = j / 2 for blocks
     // A, B); P of block A of tile t (scores sc), one element per slot, each
