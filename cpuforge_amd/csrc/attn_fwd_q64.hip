@@ -51,7 +51,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attn_fwd_q64_kernel(
     const FwdParams p) {
     constexpr int TSZ = BlkTile<128, 64>::SIZE;
-    __shared__ __attribute__((aligned(16))) bf16_bits sK[2 * TSZ];
+    __shared__ __attribute__((aligned(16))) bf16_bits sK[3 * TSZ];
     __shared__ __attribute__((aligned(16))) bf16_bits sV[2 * TSZ];
 
     // Items (query tiles) of this workgroup.  Persistent grid: the XCD of
@@ -132,7 +132,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
             qf[qb][kd] = __builtin_bit_cast(bf16x8, u);
         }
     }
-    // (The first barrier waits for these loads and K(0)'s together.)
+    // (The first barrier waits for these loads and K(0), K(1)'s together.)
 
     // Tile loads: wave w fills blocks w*BPW.. of a K and a V tile, lane l of
     // block bk reading chunk l % CPR of tile row bk + NB*(l / CPR), through a
@@ -148,24 +148,29 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
     auto tile_rsrc = [&](const char* base, int kt) {
         return buf_rsrc(base + (uint32_t)(kt * BN) * kv_row, (uint32_t)(p.seq - kt * BN) * kv_row);
     };
-    // Load i (< 2 * BPW) of interval t: K(t + 1) blocks, then V(t) blocks.
-    auto issue_load = [&](int i, const BufRsrc& rk, const BufRsrc& rv, int t) {
+    // K tile kt lives in buffer kt % 3 (loaded two intervals ahead, so that
+    // Y(t) can read X(t + 1)'s first operands), V tile kt in buffer kt % 2.
+    auto k_dst = [&](int kt) { return sk0 + (uint32_t)((kt % 3) * TSZ * 2); };
+    auto v_dst = [&](int kt) { return sv0 + (uint32_t)((kt & 1) * TSZ * 2); };
+    // Load i (< 2 * BPW) of interval t: K(t + 2) blocks to kdst, then V(t)
+    // blocks to vdst.
+    auto issue_load = [&](int i, const BufRsrc& rk, const BufRsrc& rv, uint32_t kdst, uint32_t vdst) {
         if (i < BPW)
-            lds_buf_load16(rk, tile_off[i], sk0 + (uint32_t)(((t + 1) & 1) * TSZ * 2 + i * BSTRIDE * 2));
+            lds_buf_load16(rk, tile_off[i], kdst + (uint32_t)(i * BSTRIDE * 2));
         else
-            lds_buf_load16(rv, tile_off[i - BPW], sv0 + (uint32_t)((t & 1) * TSZ * 2 + (i - BPW) * BSTRIDE * 2));
+            lds_buf_load16(rv, tile_off[i - BPW], vdst + (uint32_t)((i - BPW) * BSTRIDE * 2));
     };
     // Interval t's loads, all at once (intervals outside the pipelined run).
     auto issue_all = [&](int t) {
-        if (t + 1 < n_kt) {
-            const BufRsrc rk = tile_rsrc(kgb, t + 1);
+        if (t + 2 < n_kt) {
+            const BufRsrc rk = tile_rsrc(kgb, t + 2);
 #pragma unroll
-            for (int i = 0; i < BPW; i++) issue_load(i, rk, rk, t);
+            for (int i = 0; i < BPW; i++) issue_load(i, rk, rk, k_dst(t + 2), 0);
         }
         if (t < n_kt) {
             const BufRsrc rv = tile_rsrc(vgb, t);
 #pragma unroll
-            for (int i = BPW; i < 2 * BPW; i++) issue_load(i, rv, rv, t);
+            for (int i = BPW; i < 2 * BPW; i++) issue_load(i, rv, rv, 0, v_dst(t));
         }
     };
     auto barrier = [&]() {
@@ -313,12 +318,15 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
     // A, B); P of block B of tile t - 1 (scores sp), one element per slot,
     // each group's operand a slot after its last element; interval t's
     // loads in the odd slots of the first half.
-    auto region_x = [&](auto prev_tag, const bf16_bits* Ks, int t, const BufRsrc& rk, const BufRsrc& rv,
-                        f32x16 (&sc)[2][2], const f32x16 (&sp)[2][2]) {
+    bf16x8 kr[NKD * 2];  // K operands of the current X
+    auto region_x = [&](auto prev_tag, const bf16_bits* Ks, uint32_t kdst, uint32_t vdst, const BufRsrc& rk,
+                        const BufRsrc& rv, f32x16 (&sc)[2][2], const f32x16 (&sp)[2][2]) {
         constexpr bool PREV = decltype(prev_tag)::value;
-        bf16x8 kr[NKD * 2];
+        // After interval 0 the previous Y read the first operands.
+        if (!PREV) {
 #pragma unroll
-        for (int o = 0; o < LA; o++) kr[o] = rd_k(Ks, o);
+            for (int o = 0; o < LA; o++) kr[o] = rd_k(Ks, o);
+        }
         if (PREV) lpre[1] = lsum[1];
         CF_FENCE();
 #pragma unroll
@@ -342,7 +350,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
                 if (j == 28) p_group(1, 3, pB);
                 if (j == 30) trip = guard_test();
             }
-            if ((j & 1) && j < 2 * 2 * BPW) issue_load(j >> 1, rk, rv, t);
+            if ((j & 1) && j < 2 * 2 * BPW) issue_load(j >> 1, rk, rv, kdst, vdst);
             CF_FENCE();
         }
         if (PREV && __any(trip)) settle(sp);
@@ -350,7 +358,10 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
     // Y(t): O^T += V^T P^T of tile t - 1 (V operand o = j / 2 for blocks
     // A, B); P of block A of tile t (scores sc), one element per slot, each
     // group's operand once the products have read the previous tile's.
-    auto region_y = [&](auto prev_tag, auto next_tag, const bf16_bits* Vs, const f32x16 (&sc)[2][2]) {
+    // With tile t's P (NEXT) the last slots also read the first K operands
+    // of X(t + 1) from Kn (K(t + 1) is complete since barrier t - 1).
+    auto region_y = [&](auto prev_tag, auto next_tag, const bf16_bits* Vs, const bf16_bits* Kn,
+                        const f32x16 (&sc)[2][2]) {
         constexpr bool PREV = decltype(prev_tag)::value, NEXT = decltype(next_tag)::value;
         bf16x8 vt[4 * NDB];
         if (PREV) {
@@ -373,6 +384,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
                 // read by the product in slot 8g + 6.
                 if (j > 0 && (j & 7) == 0) p_group(0, (j >> 3) - 1, pA);
                 p_elem(sc, 0, j);
+                if (j >= 32 - 2 * LA && (j & 1) == 0) kr[(j - (32 - 2 * LA)) >> 1] = rd_k(Kn, (j - (32 - 2 * LA)) >> 1);
             }
             CF_FENCE();
         }
@@ -382,22 +394,24 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
     // t - 1 (scores sp) and the guard of tile t - 1, then the products of
     // tile t - 1 with block A's P of tile t.
     auto interval = [&](int t, f32x16 (&sc)[2][2], const f32x16 (&sp)[2][2]) {
-        const bf16_bits* Ks = sK + (t & 1) * TSZ;
+        const bf16_bits* Ks = sK + (t % 3) * TSZ;
         const bf16_bits* Vs = sV + ((t - 1) & 1) * TSZ;
-        // Past the last tile the K loads reload tile t into the free buffer.
-        const BufRsrc rk = tile_rsrc(kgb, t + 1 < n_kt ? t + 1 : t), rv = tile_rsrc(vgb, t);
-        region_x(std::true_type{}, Ks, t, rk, rv, sc, sp);
+        // Past the last tile the K loads reload tile n_kt - 1 into the free
+        // buffer (no X reads it).
+        const BufRsrc rk = tile_rsrc(kgb, t + 2 < n_kt ? t + 2 : n_kt - 1), rv = tile_rsrc(vgb, t);
+        region_x(std::true_type{}, Ks, k_dst(t + 2), v_dst(t), rk, rv, sc, sp);
         if (t == dt) mask_diag(sc);
-        region_y(std::true_type{}, std::true_type{}, Vs, sc);
+        region_y(std::true_type{}, std::true_type{}, Vs, sK + ((t + 1) % 3) * TSZ, sc);
         barrier();
     };
 
     // ---------------------------------------------------------------- walk
-    // Interval 0 needs K(0).
-    {
-        const BufRsrc rk = tile_rsrc(kgb, 0);
+    // Intervals 0 and 1 need K(0) and K(1).
 #pragma unroll
-        for (int i = 0; i < BPW; i++) lds_buf_load16(rk, tile_off[i], sk0 + (uint32_t)(i * BSTRIDE * 2));
+    for (int kt = 0; kt < 2; kt++) {
+        const BufRsrc rk = tile_rsrc(kgb, kt < n_kt ? kt : 0);
+#pragma unroll
+        for (int i = 0; i < BPW; i++) lds_buf_load16(rk, tile_off[i], k_dst(kt) + (uint32_t)(i * BSTRIDE * 2));
     }
     barrier();
     // The wave computes tiles 0..dt in intervals 0..dt + 1; the workgroup
@@ -407,10 +421,10 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
     if (active) {
         // Interval 0: S(0) (into s0) and block A's P.
         {
-            const BufRsrc rk = tile_rsrc(kgb, 1 < n_kt ? 1 : 0), rv = tile_rsrc(vgb, 0);
-            region_x(std::false_type{}, sK, 0, rk, rv, s0, s1);
+            const BufRsrc rk = tile_rsrc(kgb, 2 < n_kt ? 2 : n_kt - 1), rv = tile_rsrc(vgb, 0);
+            region_x(std::false_type{}, sK, k_dst(2), v_dst(0), rk, rv, s0, s1);
             if (dt == 0) mask_diag(s0);
-            region_y(std::false_type{}, std::true_type{}, sV, s0);
+            region_y(std::false_type{}, std::true_type{}, sV, sK + TSZ, s0);
             barrier();
             t = 1;
         }
@@ -444,7 +458,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
             p_group(1, 3, pB);
             guard(sl);
             issue_all(t);
-            region_y(std::true_type{}, std::false_type{}, Vs, sl);
+            region_y(std::true_type{}, std::false_type{}, Vs, sK, sl);
             acc_wait();
             barrier();
         };
