@@ -29,9 +29,10 @@
 //   Y  O += V^T P^T of tile t - 1       | P of tile t, block A
 // so that the softmax of one tile issues in the shadow of the products of
 // the next (one wave hides only about five other instructions per
-// 32x32x16 MFMA).  Tile t's K is read in X(t), its V in Y(t + 1): loads of
-// K(t + 1) and V(t) are issued in X(t) into the buffer pair the interval
-// before last read.  The key tile on the wave's diagonal is the last one
+// 32x32x16 MFMA).  Tile t's K is read in X(t) (its first operands at the
+// end of Y(t - 1)), its V in Y(t + 1): X(t) issues the loads of K(t + 2)
+// (three K buffers) and V(t) (two V buffers) into buffers whose last
+// readers passed barrier t - 1.  The key tile on the wave's diagonal is the last one
 // it computes (its scores masked where the key follows the query); tiles
 // past it are only loaded, for the workgroup's other waves.
 #include "cfattn_common.hpp"
