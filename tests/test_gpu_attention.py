@@ -325,6 +325,37 @@ def test_bf16_running_max_moves(cf, shape):
             assert e <= BF16_TOL, f"{shape} seq {b} {name}: {e}"
 
 
+def test_bf16_guard_trips_with_and_without_a_max_move(cf):
+    """Every query row is one vector u and key j is a multiple of u, so that
+    all rows see the same scores, tile by tile (log2 units against the max so
+    far): 0, then 2 (P = 4 per key: the tile's P sum trips the forward's
+    guard but the max stays within the lazy bound, so m must not move), then
+    12 (m moves), then 14 (trips again without a move), then a ramp.  O and
+    lse must match the oracle."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    S, Hq, Hk, Dh = 320, 4, 1, 128
+    rng = np.random.default_rng(77)
+    u = O.round_bf16(rng.standard_normal(Dh).astype(np.float32))
+    target = np.concatenate([np.zeros(64), np.full(64, 2.0), np.full(64, 12.0), np.full(64, 14.0),
+                             np.linspace(14.0, 30.0, 64)]).astype(np.float64)
+    dots = target * np.sqrt(Dh) / np.log2(np.e)
+    k = (dots[:, None] / float(np.dot(u, u))) * u[None, :]
+    q = np.tile(u, (S, Hq, 1)).astype(np.float32).reshape(-1)
+    k = O.round_bf16(k.astype(np.float32).reshape(-1))
+    v = O.round_bf16(rng.standard_normal(S * Hk * Dh).astype(np.float32))
+    qd, kd, vd = (torch.from_numpy(x).view(1, S, h, Dh).to("cuda").to(torch.bfloat16)
+                  for x, h in ((q, Hq), (k, Hk), (v, Hk)))
+    o, lse = D.fwd(qd, kd, vd, ctx=ctx)
+    torch.cuda.synchronize()
+    ro = np.zeros(S * Hq * Dh, np.float32)
+    rl = np.zeros(Hq * S, np.float32)
+    O.attention_forward_blocked(q, k, v, ro, rl, S, Hq, Hk, Dh, 128)
+    assert rel_err(o.cpu().numpy().reshape(-1), ro) <= BF16_TOL
+    assert rel_err(lse.cpu().numpy().reshape(-1), rl) <= BF16_TOL
+
+
 @pytest.mark.parametrize("scratch", ["slots", "generic"])
 @pytest.mark.parametrize("shape", FAST_SHAPES + [(3, 64, 9, 3, 64), (1, 96, 16, 2, 64)],
                          ids=lambda s: "x".join(map(str, s)))
