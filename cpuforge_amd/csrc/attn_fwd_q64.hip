@@ -31,8 +31,8 @@
 // the next (one wave hides only about five other instructions per
 // 32x32x16 MFMA).  Tile t's K is read in X(t) (its first operands at the
 // end of Y(t - 1)), its V in Y(t + 1): X(t) issues the loads of K(t + 2)
-// (three K buffers) and V(t) (two V buffers) into buffers whose last
-// readers passed barrier t - 1.  The key tile on the wave's diagonal is the last one
+// (three K buffers) and Y(t), in its first slots, those of V(t) (two V
+// buffers), into buffers whose last readers passed barrier t - 1.  The key tile on the wave's diagonal is the last one
 // it computes (its scores masked where the key follows the query); tiles
 // past it are only loaded, for the workgroup's other waves.
 #include "cfattn_common.hpp"
@@ -351,7 +351,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
                 if (j == 28) p_group(1, 3, pB);
                 if (j == 30) trip = guard_test();
             }
-            if ((j & 1) && j < 2 * 2 * BPW) issue_load(j >> 1, rk, rv, kdst, vdst);
+            if ((j & 1) && j < 2 * BPW) issue_load(j >> 1, rk, rv, kdst, vdst);
             CF_FENCE();
         }
         if (PREV && __any(trip)) settle(sp);
@@ -361,9 +361,12 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
     // group's operand once the products have read the previous tile's.
     // With tile t's P (NEXT) the last slots also read the first K operands
     // of X(t + 1) from Kn (K(t + 1) is complete since barrier t - 1).
-    auto region_y = [&](auto prev_tag, auto next_tag, const bf16_bits* Vs, const bf16_bits* Kn,
+    auto region_y = [&](auto prev_tag, auto next_tag, const bf16_bits* Vs, const bf16_bits* Kn, int tv,
                         const f32x16 (&sc)[2][2]) {
         constexpr bool PREV = decltype(prev_tag)::value, NEXT = decltype(next_tag)::value;
+        // The interval's V loads (V(tv)), early in Y: they land before the
+        // barrier like X's K loads.
+        const BufRsrc rvy = tile_rsrc(vgb, tv);
         bf16x8 vt[4 * NDB];
         if (PREV) {
 #pragma unroll
@@ -386,6 +389,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
                 if (j > 0 && (j & 7) == 0) p_group(0, (j >> 3) - 1, pA);
                 p_elem(sc, 0, j);
                 if (j >= 32 - 2 * LA && (j & 1) == 0) kr[(j - (32 - 2 * LA)) >> 1] = rd_k(Kn, (j - (32 - 2 * LA)) >> 1);
+                if ((j & 1) && j < 2 * BPW) issue_load(BPW + (j >> 1), rvy, rvy, 0, v_dst(tv));
             }
             CF_FENCE();
         }
@@ -402,7 +406,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
         const BufRsrc rk = tile_rsrc(kgb, t + 2 < n_kt ? t + 2 : n_kt - 1), rv = tile_rsrc(vgb, t);
         region_x(std::true_type{}, Ks, k_dst(t + 2), v_dst(t), rk, rv, sc, sp);
         if (t == dt) mask_diag(sc);
-        region_y(std::true_type{}, std::true_type{}, Vs, sK + ((t + 1) % 3) * TSZ, sc);
+        region_y(std::true_type{}, std::true_type{}, Vs, sK + ((t + 1) % 3) * TSZ, t, sc);
         barrier();
     };
 
@@ -425,7 +429,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
             const BufRsrc rk = tile_rsrc(kgb, 2 < n_kt ? 2 : n_kt - 1), rv = tile_rsrc(vgb, 0);
             region_x(std::false_type{}, sK, k_dst(2), v_dst(0), rk, rv, s0, s1);
             if (dt == 0) mask_diag(s0);
-            region_y(std::false_type{}, std::true_type{}, sV, sK + TSZ, s0);
+            region_y(std::false_type{}, std::true_type{}, sV, sK + TSZ, 0, s0);
             barrier();
             t = 1;
         }
@@ -459,7 +463,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
             p_group(1, 3, pB);
             guard(sl);
             issue_all(t);
-            region_y(std::true_type{}, std::false_type{}, Vs, sK, sl);
+            region_y(std::true_type{}, std::false_type{}, Vs, sK, 0, sl);
             acc_wait();
             barrier();
         };
