@@ -317,11 +317,11 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
 
     // X(t): S of tile t into sc in 32 slots (K operand o = j / 2 for blocks
     // A, B); P of block B of tile t - 1 (scores sp), one element per slot,
-    // each group's operand a slot after its last element; interval t's
-    // loads in the odd slots of the first half.
+    // each group's operand a slot after its last element; interval t's K
+    // loads (K(t + 2) to kdst) in the odd slots of the first quarter.
     bf16x8 kr[NKD * 2];  // K operands of the current X
-    auto region_x = [&](auto prev_tag, const bf16_bits* Ks, uint32_t kdst, uint32_t vdst, const BufRsrc& rk,
-                        const BufRsrc& rv, f32x16 (&sc)[2][2], const f32x16 (&sp)[2][2]) {
+    auto region_x = [&](auto prev_tag, const bf16_bits* Ks, uint32_t kdst, const BufRsrc& rk, f32x16 (&sc)[2][2],
+                        const f32x16 (&sp)[2][2]) {
         constexpr bool PREV = decltype(prev_tag)::value;
         // After interval 0 the previous Y read the first operands.
         if (!PREV) {
@@ -351,7 +351,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
                 if (j == 28) p_group(1, 3, pB);
                 if (j == 30) trip = guard_test();
             }
-            if ((j & 1) && j < 2 * BPW) issue_load(j >> 1, rk, rv, kdst, vdst);
+            if ((j & 1) && j < 2 * BPW) issue_load(j >> 1, rk, rk, kdst, 0);
             CF_FENCE();
         }
         if (PREV && __any(trip)) settle(sp);
@@ -403,8 +403,8 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
         const bf16_bits* Vs = sV + ((t - 1) & 1) * TSZ;
         // Past the last tile the K loads reload tile n_kt - 1 into the free
         // buffer (no X reads it).
-        const BufRsrc rk = tile_rsrc(kgb, t + 2 < n_kt ? t + 2 : n_kt - 1), rv = tile_rsrc(vgb, t);
-        region_x(std::true_type{}, Ks, k_dst(t + 2), v_dst(t), rk, rv, sc, sp);
+        const BufRsrc rk = tile_rsrc(kgb, t + 2 < n_kt ? t + 2 : n_kt - 1);
+        region_x(std::true_type{}, Ks, k_dst(t + 2), rk, sc, sp);
         if (t == dt) mask_diag(sc);
         region_y(std::true_type{}, std::true_type{}, Vs, sK + ((t + 1) % 3) * TSZ, t, sc);
         barrier();
@@ -426,8 +426,8 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
     if (active) {
         // Interval 0: S(0) (into s0) and block A's P.
         {
-            const BufRsrc rk = tile_rsrc(kgb, 2 < n_kt ? 2 : n_kt - 1), rv = tile_rsrc(vgb, 0);
-            region_x(std::false_type{}, sK, k_dst(2), v_dst(0), rk, rv, s0, s1);
+            const BufRsrc rk = tile_rsrc(kgb, 2 < n_kt ? 2 : n_kt - 1);
+            region_x(std::false_type{}, sK, k_dst(2), rk, s0, s1);
             if (dt == 0) mask_diag(s0);
             region_y(std::false_type{}, std::true_type{}, sV, sK + TSZ, 0, s0);
             barrier();
