@@ -74,6 +74,7 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const BwdParams p) 
         const long t = (row / p.nh) % p.seq;
         const long h = row % p.nh;
         p.delta[(b * p.nh + h) * p.seq + t] = acc;
+        if (p.lse2) p.lse2[(b * p.nh + h) * p.seq + t] = p.lse[(b * p.nh + h) * p.seq + t] * kLog2e;
     }
 }
 
@@ -1340,6 +1341,9 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
         if (nq_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
         p.n_wg_q = (int)nq_wg;
         const long rows = (long)p.batch * p.seq * p.nh;
+        // The one-wave-per-SIMD dK/dV kernel reads lse * log2(e) rows, which
+        // the delta kernel writes after the delta rows.
+        if (d.hd == 128 && tu.dkdv_variant != kDkdvWaveSpecialised) p.lse2 = delta + rows;
         hipError_t e;
         {
             TimedLaunch tl(tu.timer, kKernBwdDelta, st);

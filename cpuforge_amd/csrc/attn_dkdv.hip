@@ -14,6 +14,7 @@
 // budget leaves room for only 32 keys per wave.
 //   waves 0, 1 (P waves; keys 0-63 / 64-127 of the tile) hold K^T and the
 //     dV^T accumulators: S = Q K^T, P = exp2(S*scale*log2e - lse*log2e)
+//     (lse*log2e per row from the delta kernel)
 //     (causally masked), P to LDS as bf16 MFMA operands, dV^T += dO^T P;
 //   waves 2, 3 (dS waves; the same keys) hold -V^T and the dK^T
 //     accumulators: the dO (-V^T) products accumulate onto delta, giving
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     static_assert(NBL % 4 == 0 && BM == 64, "tile must split evenly over the four waves");
     __shared__ __attribute__((aligned(16))) bf16_bits sQ[NQBUF * TSZ];
     __shared__ __attribute__((aligned(16))) bf16_bits sO[NOBUF * TSZ];  // dO rows
-    __shared__ __attribute__((aligned(16))) float sL[NQBUF][BM];        // lse, by MFMA row
+    __shared__ __attribute__((aligned(16))) float sL[NQBUF][BM];        // lse*log2e, by MFMA row
     __shared__ __attribute__((aligned(16))) float sD[NDBUF][BM];        // delta, by MFMA row
     // P as the P waves' bf16 MFMA operands: [buffer][pair][qb][kb][half][lane].
     __shared__ uint4 sP[2][2][2][NKB][2][64];
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     // Tile loads: wave w loads blocks w*BPW.. of a Q and a dO tile, lane l of
     // block bk reading chunk l % CPR of tile row bk + NB*(l / CPR).  Wave 0
-    // also loads lse and wave 1 delta, one value per MFMA row (MFMA row
+    // also loads lse*log2e (lse2) and wave 1 delta, one value per MFMA row (MFMA row
     // `lane`: tile row (lane & 32) + qperm(lane & 31)).  The loads are
     // bounds-checked buffer loads whose buffer starts at the step's rows and
     // ends with the sequence: rows past the end read zeros (masked below),
@@ -202,7 +203,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     };
     const char* qgb = reinterpret_cast<const char*>(qg);
     const char* ogb = reinterpret_cast<const char*>(og);
-    const char* lgb = reinterpret_cast<const char*>((wv == 0 ? p.lse : p.delta) + lrow_base);
+    const char* lgb = reinterpret_cast<const char*>((wv == 0 ? p.lse2 : p.delta) + lrow_base);
     const uint32_t sq0 = lds_offset(sQ) + (uint32_t)(wv * BPW * BSTRIDE * 2);
     const uint32_t so0 = lds_offset(sO) + (uint32_t)(wv * BPW * BSTRIDE * 2);
     const uint32_t sl0 = lds_offset(wv == 0 ? &sL[0][0] : &sD[0][0]);
@@ -360,9 +361,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         f32x16 acc[NDB][NKB];  // dV^T, in AGPRs
         zero_acc(acc);
 
-        // P of an element: exp2(S*scale*log2e - lse*log2e).
+        // P of an element: exp2(S*scale*log2e - lse*log2e), lv = lse*log2e
+        // (the delta kernel's lse2 rows: the same f32 product, formed once
+        // per row instead of once per row and key tile).
         auto p_elem = [&](float s, float lv) { return __builtin_amdgcn_exp2f(__builtin_fmaf(s, p.sl2, -lv)); };
-        // lse of the lane's 16 rows of query block qb, unscaled.
+        // lse*log2e of the lane's 16 rows of query block qb.
         auto lse_raw = [&](const float* Ls, int qb, float (&lv)[16]) {
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) {
@@ -372,10 +375,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         };
         auto lse_part = [&](const float* Ls, int qb, int g4, float (&lv)[16]) {
             const float4 l = row_vals4(Ls, qb, g4);
-            lv[g4 * 4 + 0] = l.x * kLog2e;
-            lv[g4 * 4 + 1] = l.y * kLog2e;
-            lv[g4 * 4 + 2] = l.z * kLog2e;
-            lv[g4 * 4 + 3] = l.w * kLog2e;
+            lv[g4 * 4 + 0] = l.x;
+            lv[g4 * 4 + 1] = l.y;
+            lv[g4 * 4 + 2] = l.z;
+            lv[g4 * 4 + 3] = l.w;
         };
         auto publish = [&](int pbuf, int qb, int kb, const bf16x8 (&pb)[2]) {
             sP[pbuf][pair][qb][kb][0][lane] = __builtin_bit_cast(uint4, pb[0]);
@@ -470,11 +473,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 }
             };
             // R1: S of (t, 1) | softmax (t, 0, 1); P (t, 0, 0) published;
-            // lse of block 1 (read here, scaled one element per slot); this
-            // interval's loads.
-            // The first row operands came with the state (read in the
-            // previous step's last region); lse is scaled from slot 4 on, so
-            // that the first MFMAs wait for no LDS read.
+            // lse*log2e of block 1 (read here, used from R2 on); this
+            // interval's loads.  The first row operands came with the state
+            // (read in the previous step's last region), so that the first
+            // MFMAs wait for no LDS read.
 #pragma unroll
             for (int i = 0; i < LA; i++) qr[i] = in.q1[i];
             lse_raw(sL[qbuf], 1, lv1);
@@ -484,14 +486,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int k = 0; k < 2 * NKD; k++) {
                 const int kd = k >> 1, kb = k & 1;
                 if (kb == 0 && kd + LA < NKD) qr[kd + LA] = rd_row(Qs, 1, kd + LA);
-                if (k >= 4) lv1[k - 4] *= kLog2e;
                 if (k >= 2 * NKD - LA) tr[k - (2 * NKD - LA)] = rd_tr(Os, 0, k - (2 * NKD - LA));
                 s1[kb] = mfma32(qr[kd], xf[kb][kd], kd == 0 ? zero16() : s1[kb]);
                 sm(k, in.s01, in.lv0, p01, 0, 1, true);
                 if (kb == 0) issue_load(kd, ld);
                 CF_FENCE();
             }
-            // lse of (t+1, 0), raw, for R3.
+            // lse*log2e of (t+1, 0), for R4.
             if (EARLY) lse_raw(sL[nqbuf], 0, out.lv0);
             CF_HAZARD_FENCE();
             // R2: dV of (t, 0) | softmax (t, 1, 0); the first Q rows of
@@ -507,19 +508,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     mfma_acc_lead(acc[o >> 1][kb], tr[o], kb == 0 ? in.p00[o & 1] : p01[o & 1]);
                 else
                     mfma_acc(acc[o >> 1][kb], tr[o], kb == 0 ? in.p00[o & 1] : p01[o & 1]);
-                if (k < 4) lv1[12 + k] *= kLog2e;
                 sm(k, s1[0], lv1, p10, 1, 0, true);
                 if (k == 0) issue_load(NKD, ld);
                 CF_FENCE();
             }
-            // R3: S of (t+1, 0) | softmax (t, 1, 1); lse of (t+1, 0).
+            // R3: S of (t+1, 0) | softmax (t, 1, 1).
 #pragma unroll
             for (int k = 0; k < 2 * NKD; k++) {
                 const int kd = k >> 1, kb = k & 1;
-                if (EARLY) {
-                    if (kb == 0 && kd + LA < NKD) qr[kd + LA] = rd_row(Qn, 0, kd + LA);
-                    out.lv0[k] *= kLog2e;
-                }
+                if (EARLY && kb == 0 && kd + LA < NKD) qr[kd + LA] = rd_row(Qn, 0, kd + LA);
                 if (k >= 2 * NKD - LA) tr[k - (2 * NKD - LA)] = rd_tr(Os, 1, k - (2 * NKD - LA));
                 if (EARLY) {
                     if (kb == 0)

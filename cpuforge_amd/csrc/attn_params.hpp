@@ -42,6 +42,9 @@ struct BwdParams {
     const float* o;
     const float* lse;
     float* delta;
+    // lse * log2(e) per row (the P recompute's exponent offset, in base 2),
+    // written by the delta kernel when set; same layout as delta.
+    float* lse2;
     float* dq;
     float* dk;
     float* dv;

@@ -198,7 +198,7 @@ int backward_host(cfattn_ctx* c, const float* d_o, size_t d_o_len, const float* 
     float* g_q = static_cast<float*>(slot(c, cfattn_ctx::DQ, dq_len * 4, &rc));
     float* g_k = g_q ? static_cast<float*>(slot(c, cfattn_ctx::DK, dk_len * 4, &rc)) : nullptr;
     float* g_v = g_k ? static_cast<float*>(slot(c, cfattn_ctx::DV, dv_len * 4, &rc)) : nullptr;
-    float* delta = g_v ? static_cast<float*>(slot(c, cfattn_ctx::DELTA, s.n_heads * s.seq * 4, &rc)) : nullptr;
+    float* delta = g_v ? static_cast<float*>(slot(c, cfattn_ctx::DELTA, s.n_heads * s.seq * 8, &rc)) : nullptr;
     if (!delta) return rc;
     // The gradients accumulate (+=, attention.rs:145-154): their current
     // values go up with the inputs.
@@ -378,7 +378,7 @@ static int cfattn_bwd_locked(cfattn_ctx* c, cfattn_shape s, size_t batch, int dt
     if (!d_o || !q || !k || !v || !o || !lse || !dq || !dk || !dv) return fail(c, CFATTN_ERR_ARG, "null buffer");
     DeviceGuard dg(c->device);
     int rc = CFATTN_OK;
-    float* delta = static_cast<float*>(slot(c, cfattn_ctx::DELTA, batch * s.n_heads * s.seq * 4, &rc));
+    float* delta = static_cast<float*>(slot(c, cfattn_ctx::DELTA, batch * s.n_heads * s.seq * 8, &rc));
     if (!delta) return rc;
     size_t ds_bytes = 0;
     void* ds = ds_scratch(c, (Dtype)dtype, dims_of(s, batch), &ds_bytes);
@@ -409,9 +409,9 @@ int cfattn_bwd_noalloc(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, c
     if (batch * s.seq * s.n_heads >= ((size_t)1 << 31))
         return fail(c, CFATTN_ERR_UNSUPPORTED, "batch*seq*n_heads too large");
     if (!d_o || !q || !k || !v || !o || !lse || !dq || !dk || !dv) return fail(c, CFATTN_ERR_ARG, "null buffer");
-    // The only scratch of this path is delta, one float per (sequence,
-    // query head, token).
-    const size_t need = batch * s.n_heads * s.seq * sizeof(float);
+    // The only scratch of this path: two floats per (sequence, query head,
+    // token), the delta row and the lse * log2(e) row.
+    const size_t need = 2 * batch * s.n_heads * s.seq * sizeof(float);
     if (need > cfattn::kNoAllocScratchBytes)
         return fail(c, CFATTN_ERR_UNSUPPORTED,
                     "cfattn_bwd_noalloc: batch*n_heads*seq = %zu needs %zu bytes of scratch, above its fixed %zu",

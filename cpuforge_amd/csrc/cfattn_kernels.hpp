@@ -116,7 +116,8 @@ bool attn_bwd_epilogue_applies(Dtype dt, const Dims& d, const void* d_o, const v
 // dK/dV contributions of the fp32 fast path (attn_f32.hip), which
 // attn_bwd_ds_bytes reports for kF32.
 // A non-default `epi` needs attn_bwd_epilogue_applies (hipErrorInvalidValue
-// otherwise).
+// otherwise).  `delta` is scratch of 2 * batch * n_heads * seq floats: the
+// delta rows, then (head_dim 128, bf16) the lse * log2(e) rows.
 hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
                            const float* o, const float* lse, float* delta, float* dq, float* dk, float* dv,
                            hipStream_t st, const Tuning& tu, void* ds = nullptr, size_t ds_bytes = 0,
@@ -159,7 +160,7 @@ constexpr int kMaxHeadDim = 256;
 // Fixed per-device scratch of the entry points that allocate nothing
 // (noalloc.hip).  8 MiB: the backward's delta rows, batch*n_heads*seq
 // floats, up to 2^21 rows.
-constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
 // Looks up the scratch array's address on `device`, which must be current;
 // idempotent per device.
 hipError_t noalloc_init_device(int device);

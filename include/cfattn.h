@@ -140,9 +140,10 @@ int cfattn_bwd(cfattn_ctx* ctx, cfattn_shape s, size_t batch, int dtype, const v
 /* No reference counterpart.  cfattn_bwd that allocates nothing, for callers
  * that cannot call hipMalloc (code under HIP graph capture, tight serving
  * loops, harnesses that forbid allocation).  The same arguments, results and
- * accumulation as cfattn_bwd; its only scratch (delta, batch*n_heads*seq
- * floats) is a fixed 8 MiB device array of the library, one per device, so
- * batch*n_heads*seq must not exceed 2^21 (CFATTN_ERR_UNSUPPORTED otherwise).
+ * accumulation as cfattn_bwd; its only scratch (the delta and lse*log2(e)
+ * rows, 2*batch*n_heads*seq floats) is a fixed 16 MiB device array of the
+ * library, one per device, so batch*n_heads*seq must not exceed 2^21
+ * (CFATTN_ERR_UNSUPPORTED otherwise).
  * It never stores dS: in bf16, dQ recomputes the softmax (equal to
  * cfattn_bwd with cfattn_set_ds_limit(ctx, 0)); in f32 it runs the generic
  * kernels.  Calls that overlap on one device race on the shared array. */
