@@ -218,9 +218,12 @@ class SmolLM:
 
 
 def train_tok_s(batch: int = 8, seq: int = 512, layers: int = 30, rank: int = 16, steps: int = 3,
-                dtype=torch.float32, attn_dtype=None, device="cuda", backend: str = "cfops") -> dict:
-    """Build the model, warm up one step, time `steps` forward+backward
-    passes; returns tok/s and the step time."""
+                dtype=torch.float32, attn_dtype=None, device="cuda", backend: str = "cfops",
+                warmup: int = 3) -> dict:
+    """Build the model, run `warmup` untimed steps (the first allocates the
+    library's scratch and plans; the clock settles over the next ones),
+    then time `steps` forward+backward passes; returns tok/s and the step
+    time."""
     model = SmolLM(layers, seq, rank, dtype, device, attn_dtype=attn_dtype, backend=backend)
     gen = torch.Generator(device=device)
     gen.manual_seed(7)
@@ -236,6 +239,8 @@ def train_tok_s(batch: int = 8, seq: int = 512, layers: int = 30, rank: int = 16
         return loss
 
     loss0 = step().item()
+    for _ in range(warmup - 1):
+        step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -244,5 +249,6 @@ def train_tok_s(batch: int = 8, seq: int = 512, layers: int = 30, rank: int = 16
     per = (time.perf_counter() - t0) / steps
     return {"value": batch * seq / per, "unit": "tok/s", "ms_per_step": per * 1e3, "batch": batch, "seq": seq,
             "layers": layers, "lora_rank": rank, "dtype": str(dtype).replace("torch.", ""),
-            "attn_dtype": str(attn_dtype or dtype).replace("torch.", ""), "steps": steps, "first_loss": loss0,
+            "attn_dtype": str(attn_dtype or dtype).replace("torch.", ""), "steps": steps, "warmup": warmup,
+            "first_loss": loss0,
             "backend": backend}
