@@ -745,18 +745,11 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
     f32x16 dqt[NDB];
 #pragma unroll
     for (int i = 0; i < NDB; i++) dqt[i] = zero16();
-    // With the plain += epilogue the lane's dq row part is read here, while
-    // the first tiles stream in, instead of as a dependent read at the end.
+    // With a += epilogue the lane's dq row part is read here, while the first
+    // tiles stream in, instead of as a dependent read at the end.
     float* const dq_row = p.dq + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
-    const bool pre = row_ok && p.epi == kEpiAdd;
     float4 dq_pre[NDB][4];
-    if (pre) {
-#pragma unroll
-        for (int db = 0; db < NDB; db++)
-#pragma unroll
-            for (int rq = 0; rq < 4; rq++)
-                dq_pre[db][rq] = *reinterpret_cast<const float4*>(dq_row + db * 32 + rq * 8 + hh * 4);
-    }
+    const bool pre = row_ok && grad_row_prefetch<NDB>(dq_pre, dq_row, hh, p);
 
     // Step kt reads buffer kt % 3 and fills buffer (kt + 2) % 3, which the
     // barrier closing step kt - 1 has freed.
@@ -817,21 +810,10 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
     if (!row_ok) return;
 #pragma unroll
     for (int db = 0; db < NDB; db++) dqt[db] *= p.scale;  // dS was stored without the softmax scale
-    if (pre) {
-#pragma unroll
-        for (int db = 0; db < NDB; db++)
-#pragma unroll
-            for (int rq = 0; rq < 4; rq++) {
-                float4 v = dq_pre[db][rq];
-                v.x += dqt[db][rq * 4 + 0];
-                v.y += dqt[db][rq * 4 + 1];
-                v.z += dqt[db][rq * 4 + 2];
-                v.w += dqt[db][rq * 4 + 3];
-                *reinterpret_cast<float4*>(dq_row + db * 32 + rq * 8 + hh * 4) = v;
-            }
-        return;
-    }
-    write_grad_row<NDB>(dq_row, dqt, hh, tq, p);
+    if (pre)
+        write_grad_row<NDB, true>(dq_row, dqt, hh, tq, p, dq_pre);
+    else
+        write_grad_row<NDB>(dq_row, dqt, hh, tq, p);
 }
 
 // dK/dV with two specialised waves per 32-key slice: eight waves, 128 keys per

@@ -54,12 +54,29 @@ __device__ __forceinline__ void add_row_block(float* row, const f32x16& acc, int
 // rotation is lane-local.  The unrotation repeats the prologue backward's
 // expressions (s = -sin; lo' = lo c - hi s, hi' = hi c + lo s), uncontracted,
 // so both paths give the same bits.
-template <int NDB>
+// With PRE (the += modes), the row's current values come from `pre` instead
+// of memory: grad_row_prefetch read them earlier, so that the read is not a
+// dependent round trip at the end of the kernel.
+template <int NDB, bool PRE = false>
 __device__ __forceinline__ void write_grad_row(float* row, const f32x16 (&acc)[NDB], int hh, int t,
-                                               const BwdParams& p) {
+                                               const BwdParams& p, const float4 (*pre)[4] = nullptr) {
 #pragma clang fp contract(off)
     constexpr int DP = NDB * 32, HALF = DP / 2;
     if (p.epi == kEpiAdd) {
+        if constexpr (PRE) {
+#pragma unroll
+            for (int db = 0; db < NDB; db++)
+#pragma unroll
+                for (int rq = 0; rq < 4; rq++) {
+                    float4 v = pre[db][rq];
+                    v.x += acc[db][rq * 4 + 0];
+                    v.y += acc[db][rq * 4 + 1];
+                    v.z += acc[db][rq * 4 + 2];
+                    v.w += acc[db][rq * 4 + 3];
+                    *reinterpret_cast<float4*>(row + db * 32 + rq * 8 + hh * 4) = v;
+                }
+            return;
+        }
 #pragma unroll
         for (int db = 0; db < NDB; db++) add_row_block(row, acc[db], db * 32, hh, DP, true);
         return;
@@ -85,7 +102,14 @@ __device__ __forceinline__ void write_grad_row(float* row, const f32x16 (&acc)[N
             float4* r1 = reinterpret_cast<float4*>(row + d0);
             float4* r2 = reinterpret_cast<float4*>(row + d0 + HALF);
             if (p.epi == kEpiUnrotAdd) {
-                float4 a = *r1, b = *r2;
+                float4 a, b;
+                if constexpr (PRE) {
+                    a = pre[db][rq];
+                    b = pre[db + NDB / 2][rq];
+                } else {
+                    a = *r1;
+                    b = *r2;
+                }
                 a.x += lo[0], a.y += lo[1], a.z += lo[2], a.w += lo[3];
                 b.x += hi[0], b.y += hi[1], b.z += hi[2], b.w += hi[3];
                 *r1 = a;
@@ -96,6 +120,19 @@ __device__ __forceinline__ void write_grad_row(float* row, const f32x16 (&acc)[N
             }
         }
     }
+}
+
+// The lane's part of a gradient row (the layout write_grad_row writes), read
+// ahead for the += epilogue modes; false (nothing read) for the others.
+template <int NDB>
+__device__ __forceinline__ bool grad_row_prefetch(float4 (&pre)[NDB][4], const float* row, int hh,
+                                                  const BwdParams& p) {
+    if (p.epi != kEpiAdd && p.epi != kEpiUnrotAdd) return false;
+#pragma unroll
+    for (int db = 0; db < NDB; db++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) pre[db][rq] = *reinterpret_cast<const float4*>(row + db * 32 + rq * 8 + hh * 4);
+    return true;
 }
 
 // Stored dS block: kDsBlock bf16 values (2 KiB) for query block qi and key
