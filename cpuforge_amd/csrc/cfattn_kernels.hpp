@@ -158,8 +158,8 @@ hipError_t launch_fill_zero(float* dst, size_t n, hipStream_t st);
 constexpr int kMaxHeadDim = 256;
 
 // Fixed per-device scratch of the entry points that allocate nothing
-// (noalloc.hip).  8 MiB: the backward's delta rows, batch*n_heads*seq
-// floats, up to 2^21 rows.
+// (noalloc.hip).  16 MiB: the backward's delta rows and lse * log2(e) rows,
+// 2*batch*n_heads*seq floats, up to 2^21 rows of each.
 constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
 // Looks up the scratch array's address on `device`, which must be current;
 // idempotent per device.
