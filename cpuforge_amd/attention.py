@@ -108,6 +108,26 @@ class Context:
                 mask |= 1 << ids[n]
         _lib.check(self._lib.cfattn_profile_select(self.handle, mask), self.handle)
 
+    def fwd_stats_enable(self, on: bool = True) -> None:
+        """Count the bf16 head_dim-128 forward's settled wave-tiles from now
+        on (enabling again restarts the count); off frees the counter."""
+        _lib.check(self._lib.cfattn_fwd_stats_enable(self.handle, int(bool(on))), self.handle)
+
+    def fwd_stats_read(self) -> int:
+        """Settled wave-tiles since cfattn_fwd_stats_enable."""
+        n = C.c_longlong()
+        _lib.check(self._lib.cfattn_fwd_stats_read(self.handle, C.byref(n)), self.handle)
+        return n.value
+
+    def probe_mfma_peak(self, zeros: bool = False, iters: int = 40000) -> float:
+        """TFLOP/s of a loop of bf16 32x32x16 MFMAs on every SIMD, on
+        pseudo-random operands (or zeros): the on-board ceiling of the bf16
+        roofline (cfattn_probe_mfma_peak)."""
+        out = C.c_double()
+        _lib.check(self._lib.cfattn_probe_mfma_peak(self.handle, int(bool(zeros)), int(iters), C.byref(out)),
+                   self.handle)
+        return out.value
+
     def profile_read(self) -> dict:
         """{kernel name: (total ms, launches)} since profiling was enabled."""
         out = {}

@@ -20,7 +20,7 @@ OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcfattn.so")
 
 HIP_SOURCES = ["attn_fwd.hip", "attn_fwd_q64.hip", "attn_bwd.hip", "attn_dkdv.hip", "attn_f32.hip", "prologue.hip", "layer_ops.hip", "lora.hip",
-               "io_kernels.hip", "noalloc.hip", "cfattn_capi.cpp", "cfops_capi.cpp", "cfio_capi.cpp", "host_stage.cpp"]
+               "io_kernels.hip", "noalloc.hip", "probe.hip", "cfattn_capi.cpp", "cfops_capi.cpp", "cfio_capi.cpp", "host_stage.cpp"]
 ARCH = "gfx950"
 COMMON = ["-std=c++17", "-fPIC", "-O3", f"--offload-arch={ARCH}", f"-I{INCLUDE}", f"-I{CSRC}",
           "-Wall", "-Wno-unused-result",

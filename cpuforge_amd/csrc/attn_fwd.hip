@@ -528,8 +528,10 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
     p.o_vec_ok = (d.hd % 4 == 0) && ((uintptr_t)o % al == 0);
     p.xcd = tu.xcd_remap;
     if (dt == kBF16 && tu.fwd_variant == kFwdAuto && attn_fwd_q64_applies(d, p.vec_ok, p.o_vec_ok) &&
-        tu.fwd_heads_per_wg == 0 && tu.fwd_tblocks_per_wg == 0)
+        tu.fwd_heads_per_wg == 0 && tu.fwd_tblocks_per_wg == 0) {
+        p.settles = tu.fwd_settles;
         return launch_attn_fwd_q64(d, p, st, tu.timer);
+    }
     if (dt == kBF16 && p.vec_ok && p.o_vec_ok && (d.hd == 64 || d.hd == 128) && tu.fwd_heads_per_wg == 0 &&
         tu.fwd_tblocks_per_wg == 0) {
         // Fast path: kFastWaves waves per workgroup, heads per workgroup in

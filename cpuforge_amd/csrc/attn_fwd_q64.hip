@@ -18,7 +18,7 @@
 //   S^T = K Q^T   (32 MFMAs, Q^T of both blocks held in registers),
 //   online softmax in the exp2 domain (running max m per query, moved
 //   lazily: only when a tile's max exceeds it by more than kLazyRescaleQ,
-//   which keeps every P below 2^8; P is formed against m first and the
+//   which keeps every P below 2^64; P is formed against m first and the
 //   tile's row sums tell whether its max could have moved), P^T rounded to
 //   bf16,
 //   O^T += V^T P^T (32 MFMAs, O^T in AGPRs, V^T read transposed).
@@ -43,9 +43,15 @@
 namespace cfattn {
 
 // The running max moves only when a tile's max exceeds it by more than this
-// (log2 units): P <= 2^8, exact in fp32 sums, and O^T (in AGPRs) is
-// rescaled a few times per query row instead of every tile.
-constexpr float kLazyRescaleQ = 8.0f;
+// (log2 units), so P <= 2^64.  The softmax is scale-invariant and bf16 P,
+// the fp32 row sums and the fp32 O^T accumulators (in AGPRs) have the fp32
+// exponent range: with |V| up to 2^13 and 2^13 keys the largest term is
+// 2^90, far below 2^128.  With this bound the first tile of a row sets m
+// and later tiles move it only when their scores grow by more than 64
+// log2 units; a smaller bound makes rows whose scores keep growing along
+// the sequence (late keys larger than early ones) move m, and trip the
+// row-sum guard below, on most of their tiles.
+constexpr float kLazyRescaleQ = 64.0f;
 
 __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_bits* sK, bf16_bits* sV);
 
@@ -239,13 +245,17 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
     // P of a tile is formed against the running max m as it stands, with no
     // row max first: the lazy rule moves m only when the tile's max exceeds
     // it by more than kLazyRescaleQ, and while it does not, every P is at
-    // most 2^8 -- which the tile's row sum then shows.  Once the tile's P is
-    // summed, a lane whose share of it exceeds kGuard (or is not a number:
-    // the first tile, against m = -inf) sends the wave to `settle`, which
-    // takes the exact row max, applies the lazy rule and forms the tile's P
-    // again.  m moves exactly when the lazy rule says, so O, lse and every
-    // P are the same as with the max taken first.
-    constexpr float kGuard = 64.0f;
+    // most 2^kLazyRescaleQ.  An element above that bound makes its lane's
+    // share of the tile's row sum (32 elements) exceed kGuard =
+    // 2^kLazyRescaleQ, so once the tile's P is summed, a lane whose share
+    // exceeds kGuard (or is not a number: the first tile, against m = -inf)
+    // sends the wave to `settle`, which takes the exact row max, applies the
+    // lazy rule and forms the tile's P again; a share above kGuard with no
+    // element above the bound settles to no change of m.  m moves exactly
+    // when the lazy rule says, so O, lse and every P are the same as with
+    // the max taken first.
+    constexpr float kGuard = 18446744073709551616.0f;  // 2^64 = 2^kLazyRescaleQ
+    static_assert(kLazyRescaleQ == 64.0f, "kGuard is 2^kLazyRescaleQ");
     // P of element e of block qb's 32 (key block e / 16, element e % 16 of
     // the score block) into the block's staging; the bf16 operands of the
     // eight elements of group g and their sum into the row sum (two per
@@ -272,6 +282,7 @@ __device__ __forceinline__ void q64_item(const FwdParams& p, const int id, bf16_
     // rule, the row sum restarted from lpre and, if m moved anywhere in the
     // wave, O^T rescaled and the block's P formed again.
     auto settle = [&](const f32x16 (&sp)[2][2]) {
+        if (p.settles != nullptr && lane == 0) atomicAdd(p.settles, 1u);
         acc_wait();
 #pragma unroll
         for (int qb = 0; qb < 2; qb++) {

@@ -32,6 +32,8 @@ struct FwdParams {
     long part_rows;  // batch * nh * seq
     float* part;
     float2* part_ml;
+    // Counter of settled wave-tiles (attn_fwd_q64_kernel), null when off.
+    unsigned* settles;
 };
 
 struct BwdParams {

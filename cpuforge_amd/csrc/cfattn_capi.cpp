@@ -283,6 +283,7 @@ int cfattn_destroy(cfattn_ctx* c) {
         if (c->io && c->io_release) c->io_release(c->io);  // waits for its staging copies
         if (c->hs && c->hs_release) c->hs_release(c->hs);  // the same for the host-slice staging
         if (c->dev_done) (void)hipEventDestroy(c->dev_done);
+        if (c->fwd_settles) (void)hipFree(c->fwd_settles);
         for (int i = 0; i < cfattn_ctx::NSLOT; i++)
             if (c->buf[i]) (void)hipFree(c->buf[i]);
         if (c->blas && c->blas_release) c->blas_release(c->blas);
@@ -610,6 +611,46 @@ int cfattn_set_ds_limit(cfattn_ctx* c, size_t bytes) {
 }
 
 size_t cfattn_get_ds_limit(const cfattn_ctx* c) { return c ? c->ds_limit : 0; }
+
+int cfattn_fwd_stats_enable(cfattn_ctx* c, int on) {
+    if (!c) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    DeviceGuard dg(c->device);
+    if (on) {
+        if (!c->fwd_settles) CF_HIP(c, hipMalloc(reinterpret_cast<void**>(&c->fwd_settles), sizeof(unsigned)), "hipMalloc");
+        CF_HIP(c, hipMemsetAsync(c->fwd_settles, 0, sizeof(unsigned), c->stream), "hipMemsetAsync");
+        CF_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    } else if (c->fwd_settles) {
+        CF_HIP(c, hipDeviceSynchronize(), "hipDeviceSynchronize");
+        (void)hipFree(c->fwd_settles);
+        c->fwd_settles = nullptr;
+    }
+    return CFATTN_OK;
+}
+
+int cfattn_fwd_stats_read(cfattn_ctx* c, long long* settles) {
+    if (!c || !settles) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    if (!c->fwd_settles) return fail(c, CFATTN_ERR_ARG, "forward statistics are not enabled");
+    DeviceGuard dg(c->device);
+    unsigned v = 0;
+    CF_HIP(c, hipDeviceSynchronize(), "hipDeviceSynchronize");
+    CF_HIP(c, hipMemcpy(&v, c->fwd_settles, sizeof(unsigned), hipMemcpyDeviceToHost), "hipMemcpy");
+    *settles = (long long)v;
+    return CFATTN_OK;
+}
+
+int cfattn_probe_mfma_peak(cfattn_ctx* c, int zeros, int iters, double* tflops) {
+    if (!c || !tflops) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    if (iters <= 0) return fail(c, CFATTN_ERR_ARG, "iters must be positive (got %d)", iters);
+    DeviceGuard dg(c->device);
+    CF_HIP(c, cfattn::probe_mfma_bf16(c->stream, zeros, iters, tflops), "MFMA probe");
+    return CFATTN_OK;
+}
 
 int cfattn_profile_enable(cfattn_ctx* c, int on) {
     if (!c) return CFATTN_ERR_ARG;

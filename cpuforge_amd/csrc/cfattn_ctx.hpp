@@ -140,10 +140,14 @@ struct cfattn_ctx {
     // the context's stream after it before they reuse those slots.
     hipEvent_t dev_done = nullptr;
     bool dev_pending = false;
+    // Device counter of the bf16 head_dim-128 forward's settled wave-tiles
+    // while forward statistics are on (cfattn_fwd_stats_enable), else null.
+    unsigned* fwd_settles = nullptr;
 
     cfattn::Tuning tuning() const {
         cfattn::Tuning t;
         t.timer = timer;
+        t.fwd_settles = fwd_settles;
         // CFATTN_DKDV_KERNEL=ws selects the two-waves-per-SIMD dK/dV kernel
         // (bitwise equal results; kept for comparison and measurement).
         const char* v = std::getenv("CFATTN_DKDV_KERNEL");

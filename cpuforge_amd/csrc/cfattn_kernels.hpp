@@ -57,6 +57,9 @@ struct Tuning {
     int dkdv_variant = kDkdvAuto;
     int fwd_variant = kFwdAuto;
     KernelTimer* timer = nullptr;
+    // Device counter of the bf16 head_dim-128 forward's settled wave-tiles
+    // (the slow path of its row-sum guard), incremented when non-null.
+    unsigned* fwd_settles = nullptr;
 };
 
 // RAII bracket used by the launchers.
@@ -166,5 +169,11 @@ constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
 hipError_t noalloc_init_device(int device);
 // The address noalloc_init_device found for `device`, or null before it.
 void* noalloc_scratch(int device);
+
+// Matrix-pipe throughput probe (probe.hip): `iters` loop iterations of 16
+// bf16 32x32x16 MFMAs per wave, two waves per SIMD on every CU, on
+// pseudo-random operands (zeros = 0) or zero operands; waits for the run and
+// returns its TFLOP/s.
+hipError_t probe_mfma_bf16(hipStream_t st, int zeros, int iters, double* tflops);
 
 }  // namespace cfattn

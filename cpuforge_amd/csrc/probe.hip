@@ -1,0 +1,112 @@
+// Matrix-pipe throughput probe: the ceiling the bf16 attention kernels are
+// measured against on the board they run on.
+//
+// The published MI355X figure (2516.6 TFLOP/s dense bf16) assumes the 2.4 GHz
+// top clock.  Under a sustained MFMA load the board's power limit sets the
+// clock, and the power a bf16 MFMA draws depends on how many operand bits
+// change from one instruction to the next.  The probe therefore runs a loop
+// of v_mfma_f32_32x32x16_bf16 with nothing else in it, on operands that are
+// either pseudo-random bf16 values (bit activity like the attention
+// kernels' inputs) or zeros (the least power the instruction can draw), two
+// waves per SIMD on every CU, and reports FLOPs over the loop's event time.
+#include "cfattn_common.hpp"
+#include "cfattn_kernels.hpp"
+
+namespace cfattn {
+
+namespace {
+
+// A 32-bit integer hash (xorshift-multiply, the "lowbias32" constants of
+// Chris Wellons' public hash survey): consecutive inputs give unrelated
+// outputs, so every lane and operand gets independent bits.
+__device__ __forceinline__ uint32_t probe_hash(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+// Two bf16 values from 32 hash bits: random sign and mantissa, exponent
+// 2^-2 .. 2^1 (magnitudes 0.25 .. 4, like N(0,1) data).
+__device__ __forceinline__ uint32_t probe_pair(uint32_t h) {
+    const uint32_t lo = (h & 0x807fu) | ((125u + ((h >> 7) & 3u)) << 7);
+    const uint32_t hi = ((h >> 16) & 0x807fu) | ((125u + ((h >> 23) & 3u)) << 7);
+    return lo | (hi << 16);
+}
+
+__global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, int zeros, float* sink) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = blockIdx.x * 4u + (threadIdx.x >> 6);
+    bf16x8 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t wa[4], wb[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t seed = ((wave * 64u + lane) * 4u + (uint32_t)i) * 8u + (uint32_t)j;
+            wa[j] = zeros ? 0u : probe_pair(probe_hash(seed));
+            wb[j] = zeros ? 0u : probe_pair(probe_hash(seed + 4u));
+        }
+        a[i] = __builtin_bit_cast(bf16x8, make_uint4(wa[0], wa[1], wa[2], wa[3]));
+        b[i] = __builtin_bit_cast(bf16x8, make_uint4(wb[0], wb[1], wb[2], wb[3]));
+    }
+    f32x16 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) acc[c] = zero16();
+    // Four independent accumulator chains, a different operand pair for
+    // every instruction of an iteration.
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[c] = mfma32(a[(j + c) & 3], b[(j + 2 * c + (c >> 1)) & 3], acc[c]);
+    }
+    // Keeps the loop live; callers pass no sink.
+    if (sink) {
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) s += acc[c][r];
+        sink[wave * 64u + lane] = s;
+    }
+}
+
+}  // namespace
+
+// MFMAs per wave per loop iteration and FLOPs per MFMA (32 x 32 x 16 x 2).
+constexpr double kProbeMfmaPerIter = 16.0, kProbeFlopsPerMfma = 32.0 * 32.0 * 16.0 * 2.0;
+
+hipError_t probe_mfma_bf16(hipStream_t st, int zeros, int iters, double* tflops) {
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    const int wgs = 2 * cus;  // eight waves per CU: two per SIMD
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if ((e = hipEventCreate(&e0)) != hipSuccess) return e;
+    if ((e = hipEventCreate(&e1)) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return e;
+    }
+    float ms = 0.0f;
+    e = hipEventRecord(e0, st);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(mfma_probe_kernel, dim3(wgs), dim3(256), 0, st, iters, zeros, (float*)nullptr);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipEventRecord(e1, st);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (e != hipSuccess) return e;
+    const double flops = (double)wgs * 4.0 * (double)iters * kProbeMfmaPerIter * kProbeFlopsPerMfma;
+    *tflops = ms > 0.0f ? flops / ((double)ms * 1e-3) / 1e12 : 0.0;
+    return hipSuccess;
+}
+
+}  // namespace cfattn

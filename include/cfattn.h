@@ -223,6 +223,25 @@ int cfattn_profile_select(cfattn_ctx* ctx, unsigned kernel_mask);
  * (0 .. cfattn_kernel_count()-1), the summed event time in milliseconds and
  * the number of launches since profiling was enabled. */
 int cfattn_profile_read(cfattn_ctx* ctx, int kernel, double* total_ms, long long* launches);
+/* No reference counterpart: counts the wave-tiles on which the bf16
+ * head_dim-128 forward takes the slow path of its row-sum guard (exact row
+ * max, lazy rescale, P formed again; the first key tile of every wave always
+ * takes it).  Enabling allocates and zeroes a device counter; forward calls
+ * of this context then add to it, whatever stream they run on.  Off (on = 0)
+ * frees it.  For measurement: the count costs one atomic per settled
+ * wave-tile. */
+int cfattn_fwd_stats_enable(cfattn_ctx* ctx, int on);
+/* Waits for the device and returns the count since enabling. */
+int cfattn_fwd_stats_read(cfattn_ctx* ctx, long long* settles);
+/* No reference counterpart: the on-board ceiling of the bf16 roofline.  Runs
+ * `iters` iterations of 16 v_mfma_f32_32x32x16_bf16 per wave (two waves per
+ * SIMD on every CU, nothing but the MFMA loop) on the context's stream, on
+ * pseudo-random bf16 operands (zeros = 0: the bit activity of real data) or
+ * on zero operands (zeros != 0: the least power the instruction draws),
+ * waits for it and returns its TFLOP/s.  The board's power limit, not the
+ * 2.4 GHz top clock, sets the sustained rate: run it long enough (tens of
+ * milliseconds) for the clock to settle. */
+int cfattn_probe_mfma_peak(cfattn_ctx* ctx, int zeros, int iters, double* tflops);
 /* Name of kernel id `kernel` ("attn_fwd", "attn_bwd_dkdv", ...), or NULL. */
 const char* cfattn_kernel_name(int kernel);
 int cfattn_kernel_count(void);

@@ -325,26 +325,35 @@ def test_bf16_running_max_moves(cf, shape):
             assert e <= BF16_TOL, f"{shape} seq {b} {name}: {e}"
 
 
-def test_bf16_guard_trips_with_and_without_a_max_move(cf):
+def _guard_case(Dh=128, S=320, Hq=4, Hk=1):
     """Every query row is one vector u and key j is a multiple of u, so that
-    all rows see the same scores, tile by tile (log2 units against the max so
-    far): 0, then 2 (P = 4 per key: the tile's P sum trips the forward's
-    guard but the max stays within the lazy bound, so m must not move), then
-    12 (m moves), then 14 (trips again without a move), then a ramp.  O and
-    lse must match the oracle."""
-    import torch
-    from cpuforge_amd import device as D
-    mod, ctx = cf
-    S, Hq, Hk, Dh = 320, 4, 1, 128
+    all rows see the same scores, tile by tile (log2 units against the first
+    tile's max): 0, then 60 (P = 2^60 per key: a lane's share of the tile's
+    P sum, 32 such keys, exceeds the forward's guard, 2^64, but the max stays
+    within the lazy bound of 64, so m must not move), then 70 (m moves),
+    then 130 (60 above the new max: trips again without a move), then a ramp
+    to 200 (m moves).  Returns host q, k, v."""
     rng = np.random.default_rng(77)
     u = O.round_bf16(rng.standard_normal(Dh).astype(np.float32))
-    target = np.concatenate([np.zeros(64), np.full(64, 2.0), np.full(64, 12.0), np.full(64, 14.0),
-                             np.linspace(14.0, 30.0, 64)]).astype(np.float64)
+    target = np.concatenate([np.zeros(64), np.full(64, 60.0), np.full(64, 70.0), np.full(64, 130.0),
+                             np.linspace(130.0, 200.0, 64)]).astype(np.float64)[:S]
     dots = target * np.sqrt(Dh) / np.log2(np.e)
     k = (dots[:, None] / float(np.dot(u, u))) * u[None, :]
     q = np.tile(u, (S, Hq, 1)).astype(np.float32).reshape(-1)
     k = O.round_bf16(k.astype(np.float32).reshape(-1))
     v = O.round_bf16(rng.standard_normal(S * Hk * Dh).astype(np.float32))
+    return q, k, v
+
+
+def test_bf16_guard_trips_with_and_without_a_max_move(cf):
+    """The forward on _guard_case's scores: its guard trips on every tile,
+    with and without a move of the running max.  O and lse must match the
+    oracle."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    S, Hq, Hk, Dh = 320, 4, 1, 128
+    q, k, v = _guard_case(Dh, S, Hq, Hk)
     qd, kd, vd = (torch.from_numpy(x).view(1, S, h, Dh).to("cuda").to(torch.bfloat16)
                   for x, h in ((q, Hq), (k, Hk), (v, Hk)))
     o, lse = D.fwd(qd, kd, vd, ctx=ctx)
@@ -352,8 +361,38 @@ def test_bf16_guard_trips_with_and_without_a_max_move(cf):
     ro = np.zeros(S * Hq * Dh, np.float32)
     rl = np.zeros(Hq * S, np.float32)
     O.attention_forward_blocked(q, k, v, ro, rl, S, Hq, Hk, Dh, 128)
+    assert float(np.max(rl)) > 130.0  # the scores reach ~139 natural units
     assert rel_err(o.cpu().numpy().reshape(-1), ro) <= BF16_TOL
     assert rel_err(lse.cpu().numpy().reshape(-1), rl) <= BF16_TOL
+
+
+def test_bf16_forward_settles_exactly_where_the_guard_says(cf):
+    """cfattn_fwd_stats counts the wave-tiles on which the head_dim-128
+    forward takes its guard's slow path.  A wave of 64 queries walks the key
+    tiles up to its diagonal, so a sequence of nqt = ceil(S/64) query tiles
+    has Hq * nqt(nqt+1)/2 wave-tiles.  On _guard_case every one of them
+    trips (the first tile of every wave against m = -inf, every later one
+    above the guard); on N(0,1) scores only each wave's first tile does (no
+    later tile comes near 2^64 times the first one's P)."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    S, Hq, Hk, Dh = 320, 4, 1, 128
+    q, k, v = _guard_case(Dh, S, Hq, Hk)
+    qd, kd, vd = (torch.from_numpy(x).view(1, S, h, Dh).to("cuda").to(torch.bfloat16)
+                  for x, h in ((q, Hq), (k, Hk), (v, Hk)))
+    nqt = (S + 63) // 64
+    ctx.fwd_stats_enable(True)
+    try:
+        D.fwd(qd, kd, vd, ctx=ctx)
+        assert ctx.fwd_stats_read() == Hq * nqt * (nqt + 1) // 2
+        B, S, Hq, Hk = 2, 1000, 8, 2
+        _, (q2, k2, v2, _g) = _fast_inputs((B, S, Hq, Hk, Dh), seed=2400)
+        ctx.fwd_stats_enable(True)  # restarts the count
+        D.fwd(q2, k2, v2, ctx=ctx)
+        assert ctx.fwd_stats_read() == B * Hq * ((S + 63) // 64)
+    finally:
+        ctx.fwd_stats_enable(False)
 
 
 @pytest.mark.parametrize("scratch", ["slots", "generic"])
