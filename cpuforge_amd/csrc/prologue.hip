@@ -358,6 +358,112 @@ __global__ __launch_bounds__(256) void prologue_bwd_rows_staged_kernel(const Pro
     }
 }
 
+// The norm backward of the staged kernel, vectorised, for head dims D = 8 G
+// (G a power of two up to 32) with 16-byte aligned rows and tables: G lanes
+// own a row, lane j of the group holding head dims 8j .. 8j+7 in registers
+// (two 16-byte loads of each operand), so a workgroup covers 256 / G rows per
+// pass and p.chunk_rows rows in all.  Per element the expressions are the
+// staged kernel's; the row dot of dy w x rstd is summed over the lane's
+// eight dims in order and then over the G lanes by a fixed xor-shuffle tree,
+// so results are reproducible bit for bit (the staged kernel sums each row
+// left to right: the two differ in the last bits of the dot).  The lane also
+// keeps the gain-gradient sums of its eight dims over its rows, and the
+// workgroup adds its 256 / G row slots in slot order into partial[chunk],
+// which prologue_bwd_dw_reduce_kernel reduces over chunks as before.  The
+// inverse RoPE reads the partner half of the gradient row (dims i +- D/2) from
+// the cache lines the neighbouring lanes load.
+template <int G>
+__global__ __launch_bounds__(256) void prologue_bwd_norm_vec_kernel(const ProBwdParams p) {
+#pragma clang fp contract(off)
+    constexpr int D = 8 * G, SLOTS = 256 / G;
+    __shared__ float red[SLOTS][D];
+    const int tid = threadIdx.x, j = tid % G, slot = tid / G;
+    const long nbq = (p.rows_q + p.chunk_rows - 1) / p.chunk_rows;
+    long blk = blockIdx.x;
+    const bool isq = blk < nbq;
+    if (!isq) blk -= nbq;
+    const long rows = isq ? p.rows_q : p.rows_k;
+    const long r_begin = blk * p.chunk_rows, r_end = min(rows, r_begin + p.chunk_rows);
+    const int heads = isq ? p.nh : p.nkv, half = D / 2;
+    const float* gbase = isq ? p.dq : p.dk;
+    const float* xbase = isq ? p.q_pre : p.k_pre;
+    const float* rstd = isq ? p.q_rstd : p.k_rstd;
+    float* dxbase = isq ? p.dq_pre : p.dk_pre;
+    const int d0 = 8 * j;                   // the lane's first head dim
+    const int dp = d0 < half ? d0 + half : d0 - half;  // its partner dims under the rotation
+    const int dc = d0 < half ? d0 : d0 - half;         // its cos/sin index
+    float w[8], acc[8];
+    {
+        const float* wp = (isq ? p.qw : p.kw) + d0;
+        const float4 a = *reinterpret_cast<const float4*>(wp), b = *reinterpret_cast<const float4*>(wp + 4);
+        w[0] = a.x, w[1] = a.y, w[2] = a.z, w[3] = a.w, w[4] = b.x, w[5] = b.y, w[6] = b.z, w[7] = b.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+    auto load8 = [](const float* s, float (&v)[8]) {
+        const float4 a = *reinterpret_cast<const float4*>(s), b = *reinterpret_cast<const float4*>(s + 4);
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    };
+    for (long r0 = r_begin; r0 < r_end; r0 += SLOTS) {
+        const long r = r0 + slot;
+        const bool ok = r < r_end;
+        float dy[8], x[8], inv = 0.0f;
+        if (ok) {
+            const float* g = gbase + r * D;
+            if (p.unrot) {
+                const int t = (int)((r / heads) % p.seq);
+                float gs[8], gp[8], c[8], sn[8];
+                load8(g + d0, gs);
+                load8(g + dp, gp);
+                load8(p.cos + (long)(p.pos0 + t) * half + dc, c);
+                load8(p.sin + (long)(p.pos0 + t) * half + dc, sn);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    // unrotate(): element i < half is g[i] c - g[i + half] s,
+                    // element i >= half g[i] c + g[i - half] s, s = -sin.
+                    const float s = -1.0f * sn[i];
+                    dy[i] = d0 < half ? gs[i] * c[i] - gp[i] * s : gs[i] * c[i] + gp[i] * s;
+                }
+            } else {
+                load8(g + d0, dy);
+            }
+            load8(xbase + r * D + d0, x);
+            inv = rstd[r];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) dy[i] = 0.0f, x[i] = 0.0f;
+        }
+        float dot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) dot += dy[i] * w[i] * x[i] * inv;
+#pragma unroll
+        for (int off = G / 2; off >= 1; off >>= 1) dot += __shfl_xor(dot, off, G);
+        if (ok) {
+            const float mean = dot / (float)D;
+            float* dx = dxbase + r * D + d0;
+            float o[8];
+            load8(dx, o);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float xh = x[i] * inv;
+                o[i] += inv * (dy[i] * w[i] - xh * mean);
+                acc[i] += dy[i] * (x[i] * inv);
+            }
+            *reinterpret_cast<float4*>(dx) = make_float4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<float4*>(dx + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        }
+    }
+    // The gain-gradient sums of the workgroup's row slots, added in slot order.
+#pragma unroll
+    for (int i = 0; i < 8; i++) red[slot][d0 + i] = acc[i];
+    __syncthreads();
+    for (int d = tid; d < D; d += 256) {
+        float s = 0.0f;
+        for (int k = 0; k < SLOTS; k++) s += red[k][d];
+        p.partial[(isq ? blk : nbq + blk) * D + d] = s;
+    }
+}
+
 // partial[which][chunk][i] = sum over the chunk's rows of dy[row][i] * xhat[row][i].
 __global__ __launch_bounds__(256) void prologue_bwd_dw_partial_kernel(const ProBwdParams p) {
 #pragma clang fp contract(off)
@@ -476,6 +582,17 @@ hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, cons
 }
 
 static constexpr int kChunkRows = 32;  // rows per partial sum of the norm-gain gradient (row-per-thread path)
+static constexpr int kVecRows = 256;  // rows per workgroup (and gain-gradient chunk) of the vectorised norm backward
+
+static bool aligned16(std::initializer_list<const void*> ptrs) {
+    for (const void* q : ptrs)
+        if (reinterpret_cast<uintptr_t>(q) % 16 != 0) return false;
+    return true;
+}
+template <typename... T>
+static bool aligned16(const T*... ptrs) {
+    return aligned16({static_cast<const void*>(ptrs)...});
+}
 
 // Rows per partial sum of the norm-gain gradient: the staged kernel's block,
 // else kChunkRows.
@@ -523,7 +640,25 @@ hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* d
     const long rows = p.rows_q + p.rows_k;
     if (rows == 0) return hipSuccess;
     TimedLaunch tl(timer, kKernProBwd, st);
-    if (d.hd <= kStageMaxD) {
+    const int G = d.hd / 8;
+    const bool vec = pr.qw && d.hd % 8 == 0 && (G == 4 || G == 8 || G == 16 || G == 32) &&
+                     aligned16(dq, dk, q_pre, k_pre, dq_pre, dk_pre, pr.qw, pr.kw, pr.cos, pr.sin) &&
+                     (d.hd / 2) % 4 == 0;
+    if (vec) {
+        // kVecRows rows per workgroup (a chunk of the gain-gradient sum);
+        // fewer chunks than the staged kernel's, so the scratch suffices.
+        p.chunk_rows = kVecRows;
+        p.n_chunks_q = (int)((p.rows_q + p.chunk_rows - 1) / p.chunk_rows);
+        p.n_chunks_k = (int)((p.rows_k + p.chunk_rows - 1) / p.chunk_rows);
+        const long blocks = (long)p.n_chunks_q + p.n_chunks_k;
+        if (blocks > 0x7fffffffL) return hipErrorInvalidConfiguration;
+        switch (G) {
+            case 4: hipLaunchKernelGGL(prologue_bwd_norm_vec_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, st, p); break;
+            case 8: hipLaunchKernelGGL(prologue_bwd_norm_vec_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, st, p); break;
+            case 16: hipLaunchKernelGGL(prologue_bwd_norm_vec_kernel<16>, dim3((unsigned)blocks), dim3(256), 0, st, p); break;
+            default: hipLaunchKernelGGL(prologue_bwd_norm_vec_kernel<32>, dim3((unsigned)blocks), dim3(256), 0, st, p); break;
+        }
+    } else if (d.hd <= kStageMaxD) {
         p.srows = p.chunk_rows;  // stage_rows(hd + 2, 2): the mean column and w counted as more floats per row
         const long blocks = (p.rows_q + p.srows - 1) / p.srows + (p.rows_k + p.srows - 1) / p.srows;
         if (blocks > 0x7fffffffL) return hipErrorInvalidConfiguration;
