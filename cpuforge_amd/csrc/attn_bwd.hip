@@ -1326,7 +1326,11 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
                            hipStream_t st, const Tuning& tu, void* ds, size_t ds_bytes, const BwdEpilogue* epi) {
     if (d.batch == 0 || d.seq == 0 || d.nh == 0) return hipSuccess;
     const bool fast = fast_bf16_applies(dt, d, d_o, q, k, v, dq, dk, dv, tu);
-    if (epi && epi->mode != kEpiAdd && (!fast || !epi->cos || !epi->sin)) return hipErrorInvalidValue;
+    // The epilogue reads the cos/sin rows 16 bytes at a time.
+    if (epi && epi->mode != kEpiAdd &&
+        (!fast || !epi->cos || !epi->sin ||
+         (reinterpret_cast<uintptr_t>(epi->cos) | reinterpret_cast<uintptr_t>(epi->sin)) % 16 != 0))
+        return hipErrorInvalidValue;
     BwdParams p{};
     p.d_o = d_o;
     p.q = q;

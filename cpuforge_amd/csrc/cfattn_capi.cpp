@@ -518,8 +518,11 @@ int cfattn_fused_bwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, con
     int rc = CFATTN_OK;
     const size_t nq = batch * s.seq * s.n_heads * s.head_dim, nk = batch * s.seq * s.n_kv * s.head_dim;
     if (!d_o || !q || !k || !v || !dq_pre || !dk_pre || !dv) return fail(c, CFATTN_ERR_ARG, "null buffer");
-    if (cfattn::attn_bwd_epilogue_applies((Dtype)dtype, dims_of(s, batch), d_o, q, k, v, dq_pre, dk_pre, dv,
-                                          c->tuning())) {
+    // The epilogue reads the cos/sin rows 16 bytes at a time: tables not
+    // 16-byte aligned take the separate prologue backward instead.
+    const bool tables16 = (reinterpret_cast<uintptr_t>(pr->cos) | reinterpret_cast<uintptr_t>(pr->sin)) % 16 == 0;
+    if (tables16 && cfattn::attn_bwd_epilogue_applies((Dtype)dtype, dims_of(s, batch), d_o, q, k, v, dq_pre, dk_pre,
+                                                      dv, c->tuning())) {
         // The fast kernels unrotate their dQ and dK rows themselves
         // (layer.rs:191-192): without the norm they add them into
         // dq_pre/dk_pre directly; with it they store the unrotated

@@ -118,8 +118,8 @@ bool attn_bwd_epilogue_applies(Dtype dt, const Dims& d, const void* d_o, const v
 // With f32 inputs the same scratch (when large enough) holds the per-head
 // dK/dV contributions of the fp32 fast path (attn_f32.hip), which
 // attn_bwd_ds_bytes reports for kF32.
-// A non-default `epi` needs attn_bwd_epilogue_applies (hipErrorInvalidValue
-// otherwise).  `delta` is scratch of 2 * batch * n_heads * seq floats: the
+// A non-default `epi` needs attn_bwd_epilogue_applies and 16-byte aligned
+// cos/sin tables (hipErrorInvalidValue otherwise).  `delta` is scratch of 2 * batch * n_heads * seq floats: the
 // delta rows, then (head_dim 128, bf16) the lse * log2(e) rows.
 hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
                            const float* o, const float* lse, float* delta, float* dq, float* dk, float* dv,

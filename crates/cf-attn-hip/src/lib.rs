@@ -158,24 +158,37 @@ unsafe impl Send for Handle {}
 // (bf16 inputs, fp32 accumulation); the default is fp32, the reference's precision.
 static CTX: Mutex<Option<Handle>> = Mutex::new(None);
 
-fn with_ctx<R>(f: impl FnOnce(*mut ffi::Ctx) -> R) -> R {
-    let mut g = CTX.lock().unwrap();
-    if g.is_none() {
-        let mut p = std::ptr::null_mut();
-        let rc = unsafe { ffi::cfattn_create(0, &mut p) };
-        assert!(rc == ffi::CFATTN_OK, "cfattn_create failed ({rc}): no usable MI355X");
-        if std::env::var("CPUFORGE_ATTN_BF16").is_ok() {
-            unsafe { ffi::cfattn_set_mode(p, ffi::CFATTN_BF16) };
+/// Runs one library call on the process's context and panics, as the reference's
+/// asserts do, when it fails.  The panic comes after the context lock is released,
+/// so a caught panic (a failed shape check, say) leaves the context usable.
+fn call(f: impl FnOnce(*mut ffi::Ctx) -> c_int) {
+    let err = {
+        // A lock poisoned by a panic elsewhere still guards a consistent context.
+        let mut g = CTX.lock().unwrap_or_else(|e| e.into_inner());
+        let mut err: Option<String> = None;
+        if g.is_none() {
+            let mut p = std::ptr::null_mut();
+            let rc = unsafe { ffi::cfattn_create(0, &mut p) };
+            if rc != ffi::CFATTN_OK {
+                err = Some(format!("cfattn_create failed ({rc}): no usable MI355X"));
+            } else {
+                if std::env::var("CPUFORGE_ATTN_BF16").is_ok() {
+                    unsafe { ffi::cfattn_set_mode(p, ffi::CFATTN_BF16) };
+                }
+                *g = Some(Handle(p));
+            }
         }
-        *g = Some(Handle(p));
-    }
-    f(g.as_ref().unwrap().0)
-}
-
-fn check(ctx: *mut ffi::Ctx, rc: c_int) {
-    if rc != ffi::CFATTN_OK {
-        // The library words its shape errors as the reference's assert! does.
-        panic!("{}", last_error(ctx));
+        if let Some(h) = g.as_ref() {
+            let c = h.0;
+            // The library words its shape errors after the reference's assert_eq!.
+            if f(c) != ffi::CFATTN_OK {
+                err = Some(last_error(c));
+            }
+        }
+        err
+    };
+    if let Some(msg) = err {
+        panic!("{msg}");
     }
 }
 
@@ -189,13 +202,11 @@ pub fn attention_forward(q: &[f32], k: &[f32], v: &[f32], o: &mut [f32], lse: &m
 pub fn attention_forward_blocked(
     q: &[f32], k: &[f32], v: &[f32], o: &mut [f32], lse: &mut [f32], s: AttnShape, q_block: usize,
 ) {
-    with_ctx(|c| {
-        check(c, unsafe {
-            ffi::cfattn_attention_forward_blocked(
-                c, q.as_ptr(), q.len(), k.as_ptr(), k.len(), v.as_ptr(), v.len(), o.as_mut_ptr(), o.len(),
-                lse.as_mut_ptr(), lse.len(), s.c(), q_block,
-            )
-        })
+    call(|c| unsafe {
+        ffi::cfattn_attention_forward_blocked(
+            c, q.as_ptr(), q.len(), k.as_ptr(), k.len(), v.as_ptr(), v.len(), o.as_mut_ptr(), o.len(),
+            lse.as_mut_ptr(), lse.len(), s.c(), q_block,
+        )
     })
 }
 
@@ -214,14 +225,12 @@ pub fn attention_backward_blocked(
     d_o: &[f32], q: &[f32], k: &[f32], v: &[f32], o: &[f32], lse: &[f32], dq: &mut [f32], dk: &mut [f32],
     dv: &mut [f32], s: AttnShape, q_block: usize,
 ) {
-    with_ctx(|c| {
-        check(c, unsafe {
-            ffi::cfattn_attention_backward_blocked(
-                c, d_o.as_ptr(), d_o.len(), q.as_ptr(), q.len(), k.as_ptr(), k.len(), v.as_ptr(), v.len(),
-                o.as_ptr(), o.len(), lse.as_ptr(), lse.len(), dq.as_mut_ptr(), dq.len(), dk.as_mut_ptr(),
-                dk.len(), dv.as_mut_ptr(), dv.len(), s.c(), q_block,
-            )
-        })
+    call(|c| unsafe {
+        ffi::cfattn_attention_backward_blocked(
+            c, d_o.as_ptr(), d_o.len(), q.as_ptr(), q.len(), k.as_ptr(), k.len(), v.as_ptr(), v.len(),
+            o.as_ptr(), o.len(), lse.as_ptr(), lse.len(), dq.as_mut_ptr(), dq.len(), dk.as_mut_ptr(), dk.len(),
+            dv.as_mut_ptr(), dv.len(), s.c(), q_block,
+        )
     })
 }
 
@@ -474,16 +483,38 @@ mod tests {
         assert!(e <= 1e-4, "max abs error {e}");
     }
 
+    /// A wrong q length panics, as the reference's `assert_eq!(q, seq * q_stride)` does
+    /// (attention.rs:37).  The text is the library's: it starts as Rust's assert_eq!
+    /// message does ("assertion `left == right` failed") but names the operand and
+    /// both lengths on one line where Rust prints `left:` and `right:` lines.
     #[test]
     #[ignore]
-    #[should_panic(expected = "q.len()")]
-    fn wrong_q_length_panics_like_the_reference() {
+    #[should_panic(expected = "assertion `left == right` failed: q.len() = 3, expected 64")]
+    fn wrong_q_length_panics() {
         let s = AttnShape { seq: 4, n_heads: 2, n_kv: 1, head_dim: 8 };
         let q = vec![0.0f32; 3];
         let kv = vec![0.0f32; 4 * 8];
         let mut o = vec![0.0f32; 3];
         let mut lse = vec![0.0f32; 8];
         attention_forward(&q, &kv, &kv, &mut o, &mut lse, s);
+    }
+
+    /// A caught shape panic leaves the process's context usable: the next call runs.
+    #[test]
+    #[ignore]
+    fn a_call_after_a_caught_shape_panic_still_runs() {
+        let s = AttnShape { seq: 4, n_heads: 2, n_kv: 1, head_dim: 8 };
+        let bad = std::panic::catch_unwind(|| {
+            let (q, kv) = (vec![0.0f32; 3], vec![0.0f32; 4 * 8]);
+            let (mut o, mut lse) = (vec![0.0f32; 3], vec![0.0f32; 8]);
+            attention_forward(&q, &kv, &kv, &mut o, &mut lse, s);
+        });
+        assert!(bad.is_err());
+        let (q, kv) = (vec![0.25f32; 4 * 2 * 8], vec![0.5f32; 4 * 8]);
+        let (mut o, mut lse) = (vec![0.0f32; 4 * 2 * 8], vec![0.0f32; 8]);
+        attention_forward(&q, &kv, &kv, &mut o, &mut lse, s);
+        // All keys equal: every output row is v's row.
+        assert!(o.iter().all(|&x| (x - 0.5).abs() <= 1e-6), "{o:?}");
     }
 
     #[test]

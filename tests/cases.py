@@ -81,5 +81,13 @@ def rel_err(a, r) -> float:
     return float(np.abs(a - r).max() / (den if den > 0 else 1.0))
 
 
+def grad_metric(a, r) -> float:
+    """max |a - r| / (1 + |r|): the reference's gradcheck metric
+    (crates/core/src/gradcheck.rs:31-48), reported beside rel_err for bf16."""
+    a = np.asarray(a, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64)
+    return float((np.abs(a - r) / (1.0 + np.abs(r))).max())
+
+
 def max_abs(a, r) -> float:
     return float(np.abs(np.asarray(a, dtype=np.float64) - np.asarray(r, dtype=np.float64)).max())

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.cases import CASES, CONFIGS, case, max_abs, rel_err, rope_tables, seq_inputs
+from tests.cases import CASES, CONFIGS, case, grad_metric, max_abs, rel_err, rope_tables, seq_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -173,7 +173,7 @@ def _device_check(cf, cfg, mode, seqs, head_groups):
     dq, dk, dv = D.bwd(g, q, k, v, o, lse, ctx=ctx)
     torch.cuda.synchronize()
     o, lse, dq, dk, dv = (x.cpu().numpy() for x in (o, lse, dq, dk, dv))
-    worst = {}
+    worst, gworst = {}, {}
     for b in seqs:
         hq, hk, hv, hg = host[b]
         for grp_i in head_groups:
@@ -197,10 +197,17 @@ def _device_check(cf, cfg, mode, seqs, head_groups):
             for name, (a, r) in pairs.items():
                 e = max_abs(a, r) if mode == "f32" else rel_err(a, r)
                 worst[name] = max(worst.get(name, 0.0), e)
+                if mode == "bf16":
+                    gworst[name] = max(gworst.get(name, 0.0), grad_metric(a, r))
     print(f"{cfg.name} {mode}: " + ", ".join(f"{n} {e:.3e}" for n, e in worst.items()), flush=True)
+    if mode == "bf16":
+        print(f"{cfg.name} {mode} gradcheck |a-r|/(1+|r|): " + ", ".join(f"{n} {e:.3e}" for n, e in gworst.items()),
+              flush=True)
     tol = F32_TOL if mode == "f32" else BF16_TOL
     for name, e in worst.items():
         assert e <= tol, f"{cfg.name} {mode} {name}: {e}"
+    for name, e in gworst.items():
+        assert e <= BF16_TOL, f"{cfg.name} {mode} {name} gradcheck metric: {e}"
 
 
 @pytest.mark.parametrize("mode", ["f32", "bf16"])

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.cases import CONFIGS, max_abs, rel_err, seq_inputs, norm_gains
+from tests.cases import CONFIGS, grad_metric, max_abs, rel_err, seq_inputs, norm_gains
 
 pytestmark = pytest.mark.gpu
 
@@ -193,7 +193,7 @@ def test_fused_config_bf16(env, cfg_name):
     o, lse, q, k, qr, kr = D.fused_fwd(q_pre, k_pre, vd, pr, ctx=ctx)
     dqp, dkp, dv, dqw, dkw = D.fused_bwd(gd, q_pre, k_pre, q, k, vd, o, lse, qr, kr, pr, ctx=ctx)
     torch.cuda.synchronize()
-    worst = {}
+    worst, gworst = {}, {}
     for b in (0, B - 1):
         qp, kp, v, g = host[b]
         for gi in (0, Hk - 1):
@@ -209,9 +209,14 @@ def test_fused_config_bf16(env, cfg_name):
                      "dv": (selk(dv[b].cpu().numpy()), selk(rdv))}
             for nm, (a, r) in pairs.items():
                 worst[nm] = max(worst.get(nm, 0.0), rel_err(a, r))
+                gworst[nm] = max(gworst.get(nm, 0.0), grad_metric(a, r))
     print(f"{cfg_name} bf16 fused: " + ", ".join(f"{n} {e:.3e}" for n, e in worst.items()), flush=True)
+    print(f"{cfg_name} bf16 fused gradcheck |a-r|/(1+|r|): " + ", ".join(f"{n} {e:.3e}" for n, e in gworst.items()),
+          flush=True)
     for nm, e in worst.items():
         assert e <= BF16_TOL, f"{cfg_name} {nm}: {e}"
+    for nm, e in gworst.items():
+        assert e <= BF16_TOL, f"{cfg_name} {nm} gradcheck metric: {e}"
 
 
 # Shapes of the fast bf16 kernels (head_dim 64 and 128; stored-dS dQ at 128),
@@ -225,13 +230,17 @@ EPILOGUE_SHAPES = {
 }
 
 
-@pytest.mark.parametrize("name", sorted(EPILOGUE_SHAPES))
+@pytest.mark.parametrize("name", sorted(EPILOGUE_SHAPES) + ["rope128-offset-tables", "qknorm64-offset-tables"])
 def test_fused_bwd_epilogue_matches_separate_passes(env, name):
     """In bf16 mode cfattn_fused_bwd folds the inverse RoPE into the dQ and
     dK kernels' epilogues (adding into dq_pre/dk_pre, or with the norm storing
     the unrotated rows for the norm-only pass).  It must give the same bits
     as the attention backward into zeroed dq/dk followed by the separate
-    prologue backward, also on top of nonzero dq_pre/dk_pre."""
+    prologue backward, also on top of nonzero dq_pre/dk_pre.  With cos/sin
+    tables 4 bytes off a 16-byte boundary (the epilogue reads them 16 bytes
+    at a time) the fused call takes the separate passes itself."""
+    offset_tables = name.endswith("-offset-tables")
+    name = name.replace("-offset-tables", "")
     torch, cf, D, ctx = env
     B, S, Hq, Hk, Dh, theta, sc, qkn, pos0 = EPILOGUE_SHAPES[name]
     max_pos = S + pos0
@@ -241,6 +250,13 @@ def test_fused_bwd_epilogue_matches_separate_passes(env, name):
         qw = torch.from_numpy((1.0 + O.rand(Dh, 950, 0.02)).astype(np.float32)).cuda()
         kw = torch.from_numpy((1.0 + O.rand(Dh, 951, 0.02)).astype(np.float32)).cuda()
     pr = D.DeviceRope(rope, "cuda", pos0, qw, kw, 1e-6)
+    if offset_tables:
+        for nm in ("cos", "sin"):
+            t = getattr(pr, nm)
+            buf = torch.zeros(t.numel() + 1, dtype=t.dtype, device="cuda")
+            buf[1:] = t.reshape(-1)
+            setattr(pr, nm, buf[1:].view(t.shape))
+            assert getattr(pr, nm).data_ptr() % 16 == 4
     torch.manual_seed(31)
     q_pre = torch.randn(B, S, Hq, Dh, device="cuda")
     k_pre = torch.randn(B, S, Hk, Dh, device="cuda")
