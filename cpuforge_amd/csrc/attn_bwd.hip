@@ -490,12 +490,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 
     // Q and -dO operands of the lane's query: the dP^T product accumulates
     // the negated products onto delta, giving delta - dP (as the dK/dV
-    // kernels form it, so both dQ paths see the same dS).  At head_dim 64
-    // (two softmax elements per MFMA) Q is held times scale*log2(e), rounded
-    // to bf16 once, and the score product starts from -lse*log2(e) of the
-    // lane's query: it yields the exponent of P, with no multiply-add per
-    // element (the two-wave dK/dV kernel forms P the same way at head_dim 64).
-    constexpr bool kPre = DP == 64;
+    // kernels form it, so both dQ paths see the same dS).
     bf16x8 qf[NKD], of[NKD];
     {
         const bf16_bits* qr = static_cast<const bf16_bits*>(p.q) + qoff + hh * HALF;
@@ -507,20 +502,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             uint4 u = row_ok ? *reinterpret_cast<const uint4*>(orr + kd * 8) : make_uint4(0, 0, 0, 0);
             u.x ^= 0x80008000u, u.y ^= 0x80008000u, u.z ^= 0x80008000u, u.w ^= 0x80008000u;
             of[kd] = __builtin_bit_cast(bf16x8, u);
-            if constexpr (kPre) {
-                float f[8];
-#pragma unroll
-                for (int i = 0; i < 8; i++) f[i] = (float)qf[kd][i] * p.sl2;
-                qf[kd] = cvt_bf16x8(f);
-            }
         }
     }
     const long lrow = ((long)b * p.nh + head) * p.seq + tq;
     const float lse2 = row_ok ? p.lse[lrow] * kLog2e : INFINITY;
     const float dlt = row_ok ? p.delta[lrow] : 0.0f;
-    f32x16 s_init;  // the score product's start: -lse*log2(e) with kPre, else 0
-#pragma unroll
-    for (int r = 0; r < 16; r++) s_init[r] = kPre ? -lse2 : 0.0f;
 
     // Row reads (K and V rows, MFMA row l32 = key qperm(l32)) and transposed
     // reads (K^T: tile rows 4k + hh (+2, +16, +18)), as in the forward.
@@ -571,7 +557,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
             auto block = [&](int kb, bool masked) {
                 // S^T first, then dP^T: P = exp2(...) needs only S^T and runs
                 // while the dP^T products are in flight.
-                f32x16 sc = s_init, dp;
+                f32x16 sc = zero16(), dp;
 #pragma unroll
                 for (int r = 0; r < 16; r++) dp[r] = dlt;
 #pragma unroll
@@ -588,7 +574,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
                 float pr[16];
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    pr[r] = kPre ? __builtin_amdgcn_exp2f(sc[r]) : __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lse2));
+                    pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lse2));
                     if (masked && kb0 + qperm((r >> 2) * 8 + hh * 4 + (r & 3)) > tq) pr[r] = 0.0f;
                 }
                 // dS^T = P^T * -(delta - dP^T) without the softmax scale
@@ -859,18 +845,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     static_assert(L::NB % 4 == 0 && 2 * BM <= NT / 2, "tile must split evenly over the four dS waves");
     static_assert(BM % 32 == 0, "query tile must be whole 32-row blocks");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NQB = BM / 32;
-    // At head_dim 64 (two softmax elements per MFMA of a P wave) the P waves
-    // hold K^T times scale*log2(e), rounded to bf16 once when they load it,
-    // and start the score product from -lse*log2(e): the product is the
-    // exponent of P, with no multiply-add per element.  At head_dim 128 the
-    // kernel keeps the form of attn_bwd_dkdv_k64_kernel (and its bits).
-    constexpr bool kPre = DP == 64;
     // Query tiles: MFMA row i of block qb is query q0 + 32*qb + qperm(i).
     __shared__ __attribute__((aligned(16))) bf16_bits sQ0[L::SIZE];
     __shared__ __attribute__((aligned(16))) bf16_bits sQ1[L::SIZE];
     __shared__ __attribute__((aligned(16))) bf16_bits sO0[L::SIZE];  // dO rows
     __shared__ __attribute__((aligned(16))) bf16_bits sO1[L::SIZE];
-    __shared__ __attribute__((aligned(16))) float sL[2][BM];  // lse * log2(e) (kPre: negated), by MFMA row
+    __shared__ __attribute__((aligned(16))) float sL[2][BM];  // lse * log2(e), by MFMA row
     __shared__ __attribute__((aligned(16))) float sD[2][BM];  // delta, by MFMA row
     // P of each (key slice, query block) as the P waves' bf16 MFMA operands:
     // lane l's eight values of row groups 2h and 2h + 1 (h = 0, 1).
@@ -970,11 +950,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int t = step_q0(s) + lrow;
         if (dt < 0) return;
         if (dt < BM)
-            // rows past the end: P = 0
-            if constexpr (kPre)
-                sL[st][dt] = t < p.seq ? -(pl * kLog2e) : -INFINITY;
-            else
-                sL[st][dt] = t < p.seq ? pl * kLog2e : INFINITY;
+            sL[st][dt] = t < p.seq ? pl * kLog2e : INFINITY;  // rows past the end: P = 0
         else if (dt < 2 * BM)
             sD[st][dt - BM] = t < p.seq ? pl : 0.0f;
     };
@@ -999,12 +975,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 uint4 u = ok ? *reinterpret_cast<const uint4*>(xr + kd * 8) : make_uint4(0, 0, 0, 0);
                 u.x ^= sgn, u.y ^= sgn, u.z ^= sgn, u.w ^= sgn;
                 xf[kd] = __builtin_bit_cast(bf16x8, u);
-                if constexpr (kPre && PW) {
-                    float f[8];
-#pragma unroll
-                    for (int i = 0; i < 8; i++) f[i] = (float)xf[kd][i] * p.sl2;
-                    xf[kd] = cvt_bf16x8(f);
-                }
             }
         }
         f32x16 acc[NDB];  // dV^T (P waves) or dK^T (dS waves)
@@ -1038,18 +1008,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             // to LDS in f32 for the dS waves and to registers as bf16 operands.
             // lse of MFMA rows g4*8 + hh*4 + [0, 4) of block qb.
             auto lse4 = [&](int qb, int g4) { return *reinterpret_cast<const float4*>(&Ls[qb * 32 + g4 * 8 + hh * 4]); };
-            // Initial accumulator of block qb's product: 0 for S (-lse*log2e
-            // of the rows with kPre), delta of the lane's MFMA rows
-            // g4*8 + hh*4 + [0, 4) for the dS waves.
+            // Initial accumulator of block qb's product: 0 for S, delta of
+            // the lane's MFMA rows g4*8 + hh*4 + [0, 4) for the dS waves.
             auto init16 = [&](int qb) {
                 f32x16 c = zero16();
-                if constexpr (PW && kPre) {
-#pragma unroll
-                    for (int g4 = 0; g4 < 4; g4++) {
-                        const float4 l4 = lse4(qb, g4);
-                        c[g4 * 4 + 0] = l4.x, c[g4 * 4 + 1] = l4.y, c[g4 * 4 + 2] = l4.z, c[g4 * 4 + 3] = l4.w;
-                    }
-                }
                 if constexpr (!PW) {
 #pragma unroll
                     for (int g4 = 0; g4 < 4; g4++) {
@@ -1067,8 +1029,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        float pv = kPre ? __builtin_amdgcn_exp2f(sc[g4 * 4 + i])
-                                        : __builtin_amdgcn_exp2f(__builtin_fmaf(sc[g4 * 4 + i], p.sl2, -lv[i]));
+                        float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[g4 * 4 + i], p.sl2, -lv[i]));
                         if (masked && kw > q0 + qb * 32 + qperm(g4 * 8 + hh * 4 + i)) pv = 0.0f;
                         pr[g4 * 4 + i] = pv;
                     }
@@ -1085,7 +1046,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 // (With more than two query blocks the registers are not there:
                 // each block's values are read just before its softmax.)
                 float4 l4s[NQB][4];
-                if constexpr (PW && NQB <= 2 && !kPre) {
+                if constexpr (PW && NQB <= 2) {
 #pragma unroll
                     for (int qb = 0; qb < NQB; qb++)
 #pragma unroll
@@ -1102,7 +1063,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                 for (int qb = 0; qb < NQB; qb++) {
                     if constexpr (PW) {
-                        if constexpr (NQB > 2 && !kPre)
+                        if constexpr (NQB > 2)
 #pragma unroll
                             for (int g4 = 0; g4 < 4; g4++) l4s[qb][g4] = lse4(qb, g4);
                         p_block(qb, sc[qb], false, l4s[qb]);
@@ -1120,9 +1081,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     for (int kd = 0; kd < NKD; kd++) sc = mfma32(row_read(qb, kd), xf[kd], sc);
                     if constexpr (PW) {
                         float4 l4s[4];
-                        if constexpr (!kPre)
 #pragma unroll
-                            for (int g4 = 0; g4 < 4; g4++) l4s[g4] = lse4(qb, g4);
+                        for (int g4 = 0; g4 < 4; g4++) l4s[g4] = lse4(qb, g4);
                         p_block(qb, sc, tq0 < key0 + 31, l4s);
                     } else {
                         dpv[qb] = sc;
