@@ -95,6 +95,11 @@ def parse():
     ap.add_argument("--fwd-dist", action="store_true",
                     help="time the C5 bf16 forward on score distributions that move the running max (and count "
                          "the wave-tiles whose row-sum guard settles); prints its own JSON line")
+    ap.add_argument("--power", type=float, default=0.0, metavar="SECONDS",
+                    help="board power and GFX clocks (amd-smi) while the C5 forward, backward and whole step each "
+                         "run back to back for SECONDS; prints its own JSON line")
+    ap.add_argument("--ds-limit", type=int, default=None, metavar="BYTES",
+                    help="stored-dS scratch limit of the context (0: dQ recomputes the softmax instead)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the C2/C3/C4 bf16 sub-objects of the default run")
     ap.add_argument("--traffic-file", default=None,
@@ -258,6 +263,78 @@ def fwd_distributions(a):
                       "data": "synthetic (torch.randn, seed 77), changed per distribution as documented",
                       "distributions": out,
                       "slowdown_vs_normal": {d: round(out[d]["fwd_ms"] / base - 1.0, 4) for d in out}}), flush=True)
+
+
+def power_clock(a):
+    """Board power (SOCKET_POWER) and the GFX clocks of the 8 XCDs, read with
+    amd-smi every ~0.1 s while the C5 bf16 forward, backward or whole step
+    runs back to back for a.power seconds each.  Samples from the first 0.5 s
+    of each run (the clock settling) are dropped.  Reports per phase the
+    median power, median XCD clock and the kernels' mean time."""
+    import re
+    import shutil
+    import subprocess
+    import threading
+
+    import torch
+
+    import cpuforge_amd as cf
+    from cpuforge_amd import device as dev
+    smi = shutil.which("amd-smi") or "/opt/rocm/bin/amd-smi"
+    B, S, Hq, Hk, D = CONFIGS["C5"][:5]
+    ctx = cf.Context(0)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1234)
+    q = torch.randn(B, S, Hq, D, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(B, S, Hk, D, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(B, S, Hk, D, device="cuda", generator=g).to(torch.bfloat16)
+    d_o = torch.randn(B, S, Hq, D, device="cuda", generator=g).to(torch.bfloat16)
+    o, lse = torch.empty(B, S, Hq, D, device="cuda"), torch.empty(B, Hq, S, device="cuda")
+    dq, dk, dv = torch.zeros_like(o), torch.zeros(B, S, Hk, D, device="cuda"), torch.zeros(B, S, Hk, D, device="cuda")
+    dev.fwd(q, k, v, o, lse, ctx=ctx)
+    torch.cuda.synchronize()
+
+    def sample(stop, out):
+        while not stop.is_set():
+            r = subprocess.run([smi, "metric", "-g", "0", "-p", "-c"], capture_output=True, text=True)
+            t = r.stdout
+            pw = re.search(r"SOCKET_POWER:\s*([0-9.]+)\s*W", t)
+            clk = [int(c) for c in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*(\d+)\s*MHz", t)]
+            if pw and clk:
+                out.append((time.perf_counter(), float(pw.group(1)), sorted(clk)[len(clk) // 2]))
+
+    phases = {"fwd": lambda: dev.fwd(q, k, v, o, lse, ctx=ctx),
+              "bwd": lambda: dev.bwd(d_o, q, k, v, o, lse, dq, dk, dv, ctx=ctx),
+              "step": lambda: (dev.fwd(q, k, v, o, lse, ctx=ctx), dev.bwd(d_o, q, k, v, o, lse, dq, dk, dv, ctx=ctx))}
+    out = {}
+    for name, fn in phases.items():
+        samples, stop = [], threading.Event()
+        th = threading.Thread(target=sample, args=(stop, samples), daemon=True)
+        t0 = time.perf_counter()
+        th.start()
+        n = 0
+        while time.perf_counter() - t0 < a.power:
+            for _ in range(10):
+                fn()
+            torch.cuda.synchronize()
+            n += 10
+        dt = time.perf_counter() - t0
+        stop.set()
+        th.join()
+        kept = [(w, c) for ts, w, c in samples if ts - t0 > 0.5]
+        ws, cs = sorted(w for w, _ in kept), sorted(c for _, c in kept)
+        out[name] = {"ms": round(dt / n * 1e3, 4), "samples": len(kept),
+                     "power_w_median": ws[len(ws) // 2] if ws else None,
+                     "power_w_range": [ws[0], ws[-1]] if ws else None,
+                     "gfx_clock_mhz_median": cs[len(cs) // 2] if cs else None,
+                     "gfx_clock_mhz_range": [cs[0], cs[-1]] if cs else None}
+        print(f"bench: power {name}: {out[name]}", file=sys.stderr, flush=True)
+    ctx.close()
+    print(json.dumps({"metric": "board power and GFX clock under the C5 bf16 kernels (amd-smi)",
+                      "value": out["step"]["power_w_median"], "unit": "W", "higher_is_better": False,
+                      "dtype": "bf16", "seconds_per_phase": a.power,
+                      "config": {"workload": WORKLOAD["C5"], "config": "C5"},
+                      "data": "synthetic (torch.randn, seed 1234)", "phases": out}), flush=True)
 
 
 def read_traffic(path, kernel, workload_key):
@@ -758,6 +835,9 @@ def main():
     if a.fwd_dist:
         fwd_distributions(a)
         return
+    if a.power > 0:
+        power_clock(a)
+        return
     if a.peak:
         import cpuforge_amd as cf
         ctx = cf.Context(0)
@@ -779,6 +859,8 @@ def main():
         print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
         sys.exit(1)
     ctx = cf.Context(0)
+    if a.ds_limit is not None:
+        ctx.ds_limit = a.ds_limit
     r = attn_timing(a.config, mode, a.steps, a.warmup, ctx, a.traffic_file, a.copy_probe)
     pk = peak_probe(ctx) if mode == "bf16" else None
     out = {
