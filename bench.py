@@ -98,6 +98,9 @@ def parse():
     ap.add_argument("--power", type=float, default=0.0, metavar="SECONDS",
                     help="board power and GFX clocks (amd-smi) while the C5 forward, backward and whole step each "
                          "run back to back for SECONDS; prints its own JSON line")
+    ap.add_argument("--zero-inputs", action="store_true",
+                    help="diagnostic: q, k, v, dO all zero (the same kernels and instructions with the least bit "
+                         "activity, to show what the board's power limit costs); not a benchmark figure")
     ap.add_argument("--ds-limit", type=int, default=None, metavar="BYTES",
                     help="stored-dS scratch limit of the context (0: dQ recomputes the softmax instead)")
     ap.add_argument("--no-configs", action="store_true",
@@ -711,7 +714,7 @@ def io_formats(a):
                       "io": out, "cpu_baseline": cpu or None}), flush=True)
 
 
-def attn_timing(cfg, mode, steps, warmup, ctx, traffic_file, copy_probe):
+def attn_timing(cfg, mode, steps, warmup, ctx, traffic_file, copy_probe, zero_inputs=False):
     """Times `steps` attention steps (cfattn_fwd then cfattn_bwd on
     device-resident tensors) of config `cfg` after `warmup` untimed ones.
     Returns the step time (the larger of the hipEvent span and the host wall
@@ -738,6 +741,9 @@ def attn_timing(cfg, mode, steps, warmup, ctx, traffic_file, copy_probe):
     pr = dev.DeviceRope(rope, "cuda", 0, qn, kn, 1e-6)
     q, k, _, _ = dev.prologue_fwd(q_pre, k_pre, pr, dtype=dt, ctx=ctx)
     del q_pre, k_pre
+    if zero_inputs:
+        for t in (q, k, v, d_o):
+            t.zero_()
     o = torch.empty(B, S, Hq, D, device="cuda", dtype=torch.float32)
     lse = torch.empty(B, Hq, S, device="cuda", dtype=torch.float32)
     dq = torch.zeros(B, S, Hq, D, device="cuda", dtype=torch.float32)
@@ -861,7 +867,7 @@ def main():
     ctx = cf.Context(0)
     if a.ds_limit is not None:
         ctx.ds_limit = a.ds_limit
-    r = attn_timing(a.config, mode, a.steps, a.warmup, ctx, a.traffic_file, a.copy_probe)
+    r = attn_timing(a.config, mode, a.steps, a.warmup, ctx, a.traffic_file, a.copy_probe, a.zero_inputs)
     pk = peak_probe(ctx) if mode == "bf16" else None
     out = {
         "metric": "attention fwd+bwd TFLOP/s + % MFMA peak at 1 MI355X; SmolLM-135M train tok/s",
@@ -875,7 +881,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": mode,
-        "data": "synthetic (torch.randn N(0,1), RoPE prologue applied before timing)",
+        "data": ("ZERO inputs (diagnostic, not a benchmark figure)" if a.zero_inputs else
+                 "synthetic (torch.randn N(0,1), RoPE prologue applied before timing)"),
         "config": {"workload": WORKLOAD[a.config], "config": a.config, "batch": B, "seq": S, "n_heads": Hq,
                    "n_kv": Hk, "head_dim": D, "mode": mode, "causal": True},
         "pct_peak": r["pct_peak"],
