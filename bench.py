@@ -96,8 +96,8 @@ def parse():
                     help="time the C5 bf16 forward on score distributions that move the running max (and count "
                          "the wave-tiles whose row-sum guard settles); prints its own JSON line")
     ap.add_argument("--power", type=float, default=0.0, metavar="SECONDS",
-                    help="board power and GFX clocks (amd-smi) while the C5 forward, backward and whole step each "
-                         "run back to back for SECONDS; prints its own JSON line")
+                    help="board power and GFX clocks (amd-smi) while the --config forward, backward and whole step "
+                         "(bf16) each run back to back for SECONDS; prints its own JSON line")
     ap.add_argument("--zero-inputs", action="store_true",
                     help="diagnostic: q, k, v, dO all zero (the same kernels and instructions with the least bit "
                          "activity, to show what the board's power limit costs); not a benchmark figure")
@@ -270,7 +270,8 @@ def fwd_distributions(a):
 
 def power_clock(a):
     """Board power (SOCKET_POWER) and the GFX clocks of the 8 XCDs, read with
-    amd-smi every ~0.1 s while the C5 bf16 forward, backward or whole step
+    amd-smi every ~0.1 s while the bf16 forward, backward or whole step of
+    config a.config (C5 by default; q, k, v, dO drawn from N(0,1), no RoPE)
     runs back to back for a.power seconds each.  Samples from the first 0.5 s
     of each run (the clock settling) are dropped.  Reports per phase the
     median power, median XCD clock and the kernels' mean time."""
@@ -284,7 +285,7 @@ def power_clock(a):
     import cpuforge_amd as cf
     from cpuforge_amd import device as dev
     smi = shutil.which("amd-smi") or "/opt/rocm/bin/amd-smi"
-    B, S, Hq, Hk, D = CONFIGS["C5"][:5]
+    B, S, Hq, Hk, D = CONFIGS[a.config][:5]
     ctx = cf.Context(0)
     g = torch.Generator(device="cuda")
     g.manual_seed(1234)
@@ -333,10 +334,10 @@ def power_clock(a):
                      "gfx_clock_mhz_range": [cs[0], cs[-1]] if cs else None}
         print(f"bench: power {name}: {out[name]}", file=sys.stderr, flush=True)
     ctx.close()
-    print(json.dumps({"metric": "board power and GFX clock under the C5 bf16 kernels (amd-smi)",
+    print(json.dumps({"metric": f"board power and GFX clock under the {a.config} bf16 kernels (amd-smi)",
                       "value": out["step"]["power_w_median"], "unit": "W", "higher_is_better": False,
                       "dtype": "bf16", "seconds_per_phase": a.power,
-                      "config": {"workload": WORKLOAD["C5"], "config": "C5"},
+                      "config": {"workload": WORKLOAD[a.config], "config": a.config},
                       "data": "synthetic (torch.randn, seed 1234)", "phases": out}), flush=True)
 
 

@@ -93,8 +93,32 @@ static int stage_rows(int hd, int nbuf) {
 }
 
 // Copy n consecutive floats of `src` (rows of D) into LDS rows LD apart, 256
-// threads, eight loads in flight per thread before their stores.
-__device__ __forceinline__ void stage_rows_to_lds(float* dst, const float* src, int n, int D, int LD, int tid) {
+// threads, eight loads in flight per thread before their stores.  With
+// `vec` (src 16-byte aligned, D a multiple of 4) the loads are 16 bytes
+// each: a block of 64 rows of 128 floats is then one round of loads.
+__device__ __forceinline__ void stage_rows_to_lds(float* dst, const float* src, int n, int D, int LD, int tid,
+                                                  bool vec = false) {
+    if (vec) {
+        const float4* s4 = reinterpret_cast<const float4*>(src);
+        const int n4 = n / 4;
+        for (int j0 = 0; j0 < n4; j0 += 256 * 8) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int j = j0 + u * 256 + tid;
+                v[u] = j < n4 ? s4[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int j = j0 + u * 256 + tid;
+                if (j < n4) {
+                    float* d = dst + (j * 4 / D) * LD + (j * 4) % D;
+                    d[0] = v[u].x, d[1] = v[u].y, d[2] = v[u].z, d[3] = v[u].w;
+                }
+            }
+        }
+        return;
+    }
     for (int j0 = 0; j0 < n; j0 += 256 * 8) {
         float v[8];
 #pragma unroll
@@ -128,7 +152,7 @@ __global__ __launch_bounds__(256) void prologue_fwd_staged_kernel(const ProParam
     const float* w = isq ? p.qw : p.kw;
     float* srstd = stage + p.srows * LD;
     if (w) {
-        stage_rows_to_lds(stage, x, nr * D, D, LD, tid);
+        stage_rows_to_lds(stage, x, nr * D, D, LD, tid, p.vec4);
         __syncthreads();
         if (tid < nr) {
             const float* xr = stage + tid * LD;
