@@ -101,6 +101,11 @@ def parse():
     ap.add_argument("--zero-inputs", action="store_true",
                     help="diagnostic: q, k, v, dO all zero (the same kernels and instructions with the least bit "
                          "activity, to show what the board's power limit costs); not a benchmark figure")
+    ap.add_argument("--sweep", action="store_true",
+                    help="per-kernel times of the bf16 step at the --config heads and head_dim, the tokens held at "
+                         "the config's batch x seq and the sequence halved from 4x seq (B shrinking to match) down "
+                         "to seq/4, with a least-squares split of each backward kernel's time into a per-step and a "
+                         "per-workgroup part; prints its own JSON line")
     ap.add_argument("--ds-limit", type=int, default=None, metavar="BYTES",
                     help="stored-dS scratch limit of the context (0: dQ recomputes the softmax instead)")
     ap.add_argument("--no-configs", action="store_true",
@@ -266,6 +271,89 @@ def fwd_distributions(a):
                       "data": "synthetic (torch.randn, seed 77), changed per distribution as documented",
                       "distributions": out,
                       "slowdown_vs_normal": {d: round(out[d]["fwd_ms"] / base - 1.0, 4) for d in out}}), flush=True)
+
+
+def shape_sweep(a):
+    """Per-kernel times (the library's hipEvents around every launch, 10
+    steps after 3 warm-up ones) of the bf16 step at the heads and head_dim of
+    a.config with batch x seq fixed, and for each backward kernel of the
+    one-workgroup-per-CU grids the least-squares fit
+        time = step_us x (steps per CU) + wg_us x (workgroups per CU).
+    The dK/dV grid has one workgroup per 128 keys of a KV head, walking
+    group x (query tiles of 64 from its key tile to the end) steps; the
+    stored-dS dQ grid one workgroup per (KV head, tile of 8 query blocks),
+    walking the key tiles of 64 up to its last query.  Both run one workgroup
+    per CU, so the workgroups (steps) per CU are the grid's (its steps) / CUs.
+    Inputs are N(0,1) without RoPE."""
+    import numpy as np
+    import torch
+
+    import cpuforge_amd as cf
+    from cpuforge_amd import device as dev
+    B0, S0, Hq, Hk, D = CONFIGS[a.config][:5]
+    tokens = B0 * S0
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    group = Hq // Hk
+    ctx = cf.Context(0)
+    rows = []
+    for S in (4 * S0, 2 * S0, S0, S0 // 2, S0 // 4):
+        if S < 256 or tokens % S:
+            continue
+        B = tokens // S
+        g = torch.Generator(device="cuda")
+        g.manual_seed(1234)
+        q = torch.randn(B, S, Hq, D, device="cuda", generator=g).to(torch.bfloat16)
+        k = torch.randn(B, S, Hk, D, device="cuda", generator=g).to(torch.bfloat16)
+        v = torch.randn(B, S, Hk, D, device="cuda", generator=g).to(torch.bfloat16)
+        d_o = torch.randn(B, S, Hq, D, device="cuda", generator=g).to(torch.bfloat16)
+        o, lse = torch.empty(B, S, Hq, D, device="cuda"), torch.empty(B, Hq, S, device="cuda")
+        dq, dk, dv = torch.zeros_like(o), torch.zeros(B, S, Hk, D, device="cuda"), torch.zeros(B, S, Hk, D, device="cuda")
+
+        def step():
+            dev.fwd(q, k, v, o, lse, ctx=ctx)
+            dev.bwd(d_o, q, k, v, o, lse, dq, dk, dv, ctx=ctx)
+
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        ctx.profile_select(None)
+        ctx.profile_enable(True)
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+        ms = {n: round(t / c, 4) for n, (t, c) in ctx.profile_read().items() if c}
+        ctx.profile_enable(False)
+        nqt, nkt = S // 64, S // 128
+        # dK/dV: key tile j of a head walks group * (nqt - 2j) steps.
+        kv_wgs = B * Hk * nkt
+        kv_steps = B * Hk * group * sum(nqt - 2 * j for j in range(nkt))
+        # stored-dS dQ (head_dim 128): tiles of 8 query blocks over the group's
+        # heads (hpw heads x 8 / hpw blocks); tile t walks key tiles up to its end.
+        hpw = 4 if group % 4 == 0 else 2 if group % 2 == 0 else 1
+        tq = 32 * (8 // hpw)
+        ntt = S // tq
+        q_wgs = B * Hk * (group // hpw) * ntt
+        q_steps = B * Hk * (group // hpw) * sum(((t + 1) * tq + 63) // 64 for t in range(ntt))
+        rows.append({"batch": B, "seq": S, "kernels_ms": ms,
+                     "dkdv": {"steps_per_cu": kv_steps / cus, "wgs_per_cu": kv_wgs / cus},
+                     "dq": {"steps_per_cu": q_steps / cus, "wgs_per_cu": q_wgs / cus}})
+        print(f"bench: sweep B{B} S{S} {ms}", file=sys.stderr, flush=True)
+        del q, k, v, d_o, o, lse, dq, dk, dv
+        torch.cuda.empty_cache()
+    fits = {}
+    for kern, key in (("attn_bwd_dkdv", "dkdv"), ("attn_bwd_dq", "dq")):
+        A = np.array([[r[key]["steps_per_cu"], r[key]["wgs_per_cu"]] for r in rows])
+        y = np.array([r["kernels_ms"].get(kern, 0.0) * 1e3 for r in rows])
+        if len(rows) >= 2 and D == 128:
+            coef = np.linalg.lstsq(A, y, rcond=None)[0]
+            fits[kern] = {"step_us": round(float(coef[0]), 3), "wg_us": round(float(coef[1]), 2),
+                          "max_residual_us": round(float(np.max(np.abs(A @ coef - y))), 2)}
+    ctx.close()
+    print(json.dumps({"metric": f"per-kernel times across sequence lengths at {a.config}'s heads and head_dim",
+                      "value": None, "unit": "ms", "dtype": "bf16", "tokens": tokens, "n_heads": Hq, "n_kv": Hk,
+                      "head_dim": D, "cus": cus, "data": "synthetic (torch.randn, seed 1234, no RoPE)",
+                      "config": {"workload": WORKLOAD[a.config], "config": a.config}, "rows": rows,
+                      "fit": fits}), flush=True)
 
 
 def power_clock(a):
@@ -844,6 +932,9 @@ def main():
         return
     if a.power > 0:
         power_clock(a)
+        return
+    if a.sweep:
+        shape_sweep(a)
         return
     if a.peak:
         import cpuforge_amd as cf
