@@ -1029,9 +1029,14 @@ def main():
     if not a.no_train:
         # SmolLM-135M LoRA r=16 train step (cmd_bench.rs:52-99), seq 512, batch 8,
         # f32 like the reference, attention through the fused GPU path.
+        # The step is timed as replays of a HIP graph of it (the same kernels
+        # in the same order, bitwise the eager step's results:
+        # tests/test_gpu_train_graph.py), and eagerly beside it.
         from cpuforge_amd.train_bench import train_tok_s
         print("bench: SmolLM-135M train step ...", file=sys.stderr, flush=True)
-        tr = train_tok_s(batch=8, seq=512, steps=a.train_steps)
+        tr = train_tok_s(batch=8, seq=512, steps=a.train_steps, graph=True)
+        ea = train_tok_s(batch=8, seq=512, steps=a.train_steps)
+        tr["eager"] = {"value": round(ea["value"], 3), "ms_per_step": round(ea["ms_per_step"], 3)}
         tr["reference_tok_s"] = 122.0  # README.md:95, 2-core CPU, batch 1, same shape and LoRA
         out["smollm_train"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in tr.items()}
     if not a.no_cpu:

@@ -81,6 +81,7 @@ SIGNATURES = {
     "cfops_silu_mul_backward": (C.c_int, [_vp] * 6 + [_sz, _vp]),
     "cfops_cross_entropy_fwd_bwd": (C.c_int, [_vp] * 4 + [_sz, _sz, _fp, _vp]),
     "cfops_lm_head_ce": (C.c_int, [_vp] * 4 + [_sz, _sz, _sz, _vp, _vp, _fp, _vp]),
+    "cfops_lm_head_ce_dev": (C.c_int, [_vp] * 4 + [_sz, _sz, _sz, _vp, _vp, _vp, _vp]),
     "cfops_set_head_chunk_limit": (C.c_int, [_vp, _sz]),
     "cfops_linear_forward": (C.c_int, [_vp] * 5 + [C.c_float] + [_sz] * 4 + [_vp] * 3),
     "cfops_linear_backward": (C.c_int, [_vp] * 7 + [C.c_float] + [_sz] * 4 + [_vp] * 5),

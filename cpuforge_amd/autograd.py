@@ -169,6 +169,33 @@ class LMHeadCEFn(torch.autograd.Function):
         return (dhn * g).view(ctx.shape), (dhead * g if ctx.has_dhead else None), None
 
 
+class LMHeadCEDevFn(torch.autograd.Function):
+    """LMHeadCEFn with no host wait (ops.lm_head_ce_dev), for a step captured
+    in a HIP graph: returns the loss as a device tensor and the loss block
+    (cfops_ce_result), whose target check the caller runs after the stream
+    drains (ops.ce_check)."""
+
+    @staticmethod
+    def forward(ctx, hn, head, targets):
+        d = hn.shape[-1]
+        h2 = _flat(hn, d)
+        t, vocab = h2.shape[0], head.shape[0]
+        dhn = torch.empty_like(h2)
+        dhead = torch.zeros_like(head) if ctx.needs_input_grad[1] else None
+        result = P.ce_result_buffer(hn.device)
+        P.lm_head_ce_dev(h2, head, targets.contiguous().view(-1), t, d, vocab, dhn, dhead, result)
+        ctx.save_for_backward(dhn, dhead if dhead is not None else torch.empty(0))
+        ctx.has_dhead = dhead is not None
+        ctx.shape = hn.shape
+        ctx.mark_non_differentiable(result)
+        return P.ce_result_loss(result).clone(), result
+
+    @staticmethod
+    def backward(ctx, g, _g_result):
+        dhn, dhead = ctx.saved_tensors
+        return (dhn * g).view(ctx.shape), (dhead * g if ctx.has_dhead else None), None
+
+
 def rmsnorm(x, w, eps):
     return RMSNormFn.apply(x, w, eps)
 
@@ -190,3 +217,8 @@ def shared_input_linears(x, specs):
 
 def lm_head_ce(hn, head, targets):
     return LMHeadCEFn.apply(hn, head, targets)
+
+
+def lm_head_ce_dev(hn, head, targets):
+    """(loss, cfops_ce_result block): the loss with no host wait."""
+    return LMHeadCEDevFn.apply(hn, head, targets)

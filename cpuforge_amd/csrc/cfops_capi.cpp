@@ -7,6 +7,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <climits>
+#include <cstddef>
 #include <cstring>
 #include <map>
 #include <tuple>
@@ -256,22 +257,15 @@ int cfops_set_head_chunk_limit(cfattn_ctx* c, size_t bytes) {
     return CFATTN_OK;
 }
 
-int cfops_lm_head_ce(cfattn_ctx* c, const float* hn, const float* head, const int64_t* targets, size_t t, size_t d,
-                     size_t vocab, float* dhn, float* dhead, float* loss, void* stream) {
-    CF_LOCK(c);
-    if (!loss) return fail(c, CFATTN_ERR_ARG, "null loss");
-    *loss = 0.0f;
-    if (t == 0) return CFATTN_OK;
-    if (!hn || !head || !targets || !dhn) return fail(c, CFATTN_ERR_ARG, "null buffer");
-    if (vocab == 0) return fail(c, CFATTN_ERR_ARG, "vocab must be positive");
-    if (t > (size_t)INT_MAX) return fail(c, CFATTN_ERR_UNSUPPORTED, "t=%zu above 2^31", t);
-    const hipStream_t st = to_stream(stream);
+// The LM head and loss queued on `st` with the loss block at `misc` (device
+// memory: n_valid, bad_row, loss); the caller holds the context lock and
+// has checked the arguments.
+static int lm_head_ce_queue(cfattn_ctx* c, const float* hn, const float* head, const int64_t* targets, size_t t, size_t d,
+                     size_t vocab, float* dhn, float* dhead, void* misc, hipStream_t st) {
     size_t chunk = c->head_chunk_bytes / (vocab * sizeof(float));
     if (chunk < 1) chunk = 1;
     if (chunk > t) chunk = t;
     int rc = CFATTN_OK;
-    void* misc = slot(c, cfattn_ctx::OPS_MISC, cfattn::kCeMiscBytes, &rc);
-    if (!misc) return rc;
     float* row_loss = static_cast<float*>(slot(c, cfattn_ctx::OPS_ROWLOSS, t * sizeof(float), &rc));
     if (!row_loss) return rc;
     float* logits = static_cast<float*>(slot(c, cfattn_ctx::OPS_LOGITS, chunk * vocab * sizeof(float), &rc));
@@ -288,7 +282,40 @@ int cfops_lm_head_ce(cfattn_ctx* c, const float* hn, const float* head, const in
         if (dhead) CF_TRY(gemm(c, CFOPS_TN, logits, hn + r0 * d, dhead, vocab, nr, d, 1.0f, true, st));
     }
     CF_HIP(c, cfattn::launch_ce_finish(targets, row_loss, t, misc, st), "cross-entropy launch");
+    return CFATTN_OK;
+}
+
+int cfops_lm_head_ce(cfattn_ctx* c, const float* hn, const float* head, const int64_t* targets, size_t t, size_t d,
+                     size_t vocab, float* dhn, float* dhead, float* loss, void* stream) {
+    CF_LOCK(c);
+    if (!loss) return fail(c, CFATTN_ERR_ARG, "null loss");
+    *loss = 0.0f;
+    if (t == 0) return CFATTN_OK;
+    if (!hn || !head || !targets || !dhn) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (vocab == 0) return fail(c, CFATTN_ERR_ARG, "vocab must be positive");
+    if (t > (size_t)INT_MAX) return fail(c, CFATTN_ERR_UNSUPPORTED, "t=%zu above 2^31", t);
+    const hipStream_t st = to_stream(stream);
+    int rc = CFATTN_OK;
+    void* misc = slot(c, cfattn_ctx::OPS_MISC, cfattn::kCeMiscBytes, &rc);
+    if (!misc) return rc;
+    CF_TRY(lm_head_ce_queue(c, hn, head, targets, t, d, vocab, dhn, dhead, misc, st));
     return ce_result(c, misc, targets, vocab, loss, st);
+}
+
+static_assert(sizeof(cfops_ce_result) == sizeof(cfattn::CeMisc) &&
+                  offsetof(cfops_ce_result, bad_row) == offsetof(cfattn::CeMisc, bad_row) &&
+                  offsetof(cfops_ce_result, loss) == offsetof(cfattn::CeMisc, loss),
+              "cfops_ce_result is the kernels' loss block");
+
+int cfops_lm_head_ce_dev(cfattn_ctx* c, const float* hn, const float* head, const int64_t* targets, size_t t,
+                         size_t d, size_t vocab, float* dhn, float* dhead, cfops_ce_result* result, void* stream) {
+    CF_LOCK(c);
+    if (!result) return fail(c, CFATTN_ERR_ARG, "null result");
+    if (t == 0) return fail(c, CFATTN_ERR_ARG, "t must be positive");
+    if (!hn || !head || !targets || !dhn) return fail(c, CFATTN_ERR_ARG, "null buffer");
+    if (vocab == 0) return fail(c, CFATTN_ERR_ARG, "vocab must be positive");
+    if (t > (size_t)INT_MAX) return fail(c, CFATTN_ERR_UNSUPPORTED, "t=%zu above 2^31", t);
+    return lm_head_ce_queue(c, hn, head, targets, t, d, vocab, dhn, dhead, result, to_stream(stream));
 }
 
 int cfops_linear_forward(cfattn_ctx* c, const float* x, const float* w, const float* lora_a, const float* lora_b,

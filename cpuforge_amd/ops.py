@@ -9,6 +9,7 @@ the holder of device memory and the current HIP stream:
     silu_mul_forward / silu_mul_backward crates/core/src/ops/swiglu.rs
     cross_entropy_fwd_bwd               crates/core/src/ops/loss.rs:9-55
     lm_head_ce                          crates/model/src/model.rs:436-457
+      (lm_head_ce_dev: the same, its loss left in device memory)
     linear_forward / linear_backward    crates/model/src/linear.rs:56-91
     adamw_update                        crates/train/src/optim.rs:9-30
 
@@ -138,6 +139,43 @@ def lm_head_ce(hn, head, targets, t, d, vocab, dhn, dhead=None, ctx: Context | N
     _call(ctx, "cfops_lm_head_ce", _f32(hn, "hn", t * d), _f32(head, "head", vocab * d), _targets(targets, t), t, d,
           vocab, _f32(dhn, "dhn", t * d), _opt(dhead, "dhead", vocab * d), C.byref(loss), _stream())
     return loss.value
+
+
+CE_RESULT_WORDS = 3  # cfops_ce_result: n_valid, bad_row (int32), loss (float32)
+_NO_BAD_ROW = 2 ** 31 - 1
+
+
+def ce_result_buffer(device) -> torch.Tensor:
+    """A device block for lm_head_ce_dev's result (cfops_ce_result)."""
+    return torch.empty(CE_RESULT_WORDS, dtype=torch.int32, device=device)
+
+
+def ce_result_loss(result: torch.Tensor) -> torch.Tensor:
+    """The loss of a cfops_ce_result block, as a 0-d float32 device tensor
+    (a view of the block)."""
+    return result.view(torch.float32)[2]
+
+
+def lm_head_ce_dev(hn, head, targets, t, d, vocab, dhn, dhead, result, ctx: Context | None = None) -> None:
+    """lm_head_ce queued on the current stream with no host wait: the loss
+    block goes to `result` (ce_result_buffer), for a step captured in a HIP
+    graph.  The target check is the caller's, after the stream drains
+    (ce_check)."""
+    ctx = ctx or default_context()
+    if not isinstance(result, torch.Tensor) or not result.is_cuda or result.dtype != torch.int32 \
+            or result.numel() < CE_RESULT_WORDS or not result.is_contiguous():
+        raise TypeError("result must be a contiguous int32 device tensor of 3 words")
+    _call(ctx, "cfops_lm_head_ce_dev", _f32(hn, "hn", t * d), _f32(head, "head", vocab * d), _targets(targets, t), t,
+          d, vocab, _f32(dhn, "dhn", t * d), _opt(dhead, "dhead", vocab * d), result.data_ptr(), _stream())
+
+
+def ce_check(result: torch.Tensor, targets: torch.Tensor, vocab: int) -> None:
+    """Waits for `result` (a cfops_ce_result written by lm_head_ce_dev) and
+    raises, with lm_head_ce's error, for a target outside [0, vocab)."""
+    bad = int(result[1].item())
+    if bad != _NO_BAD_ROW:
+        t = int(targets.reshape(-1)[bad].item())
+        raise _lib.CfattnError(_lib.ERR_ARG, f"target {t} out of range for vocab {vocab}")
 
 
 def set_head_chunk_limit(nbytes: int, ctx: Context | None = None) -> None:

@@ -133,6 +133,11 @@ class SmolLM:
         self.final_norm = torch.ones(d, device=device, dtype=dtype)
         self.rope = LayerRope(RopeCache(hd, seq, c["theta"]), device)
         self.attention = layer_attention  # (q_pre, k_pre, v, LayerRope) -> o
+        # With ce_on_device the cfops loss leaves its value on the device
+        # (no host wait: a step that can be captured in a HIP graph) and the
+        # target check waits for check_targets().
+        self.ce_on_device = False
+        self._ce = None
         self.lora_cfg = None
         if train == "full":
             for _, p in self.named_params():
@@ -214,16 +219,63 @@ class SmolLM:
             g, u = A.shared_input_linears(n2, [layer[n].spec() for n in ("gate", "up")])
             x = x + layer["down"](A.silu_mul(g, u), cf)
         hn = A.rmsnorm(x, self.final_norm, c["eps"])
+        if self.ce_on_device:
+            loss, res = A.lm_head_ce_dev(hn, self.embed, targets)
+            self._ce = (res, targets)
+            return loss
         return A.lm_head_ce(hn, self.embed, targets)
+
+    def check_targets(self) -> None:
+        """Raises, as the loss would have, if the last device-side loss met
+        a target out of range (waits for it)."""
+        if self._ce is not None:
+            from .ops import ce_check
+            res, targets = self._ce
+            ce_check(res, targets, self.c["vocab"])
+
+
+def capture_step(model: SmolLM, tokens, targets, warmup: int = 2):
+    """The training step (every trained parameter's .grad reset, forward,
+    loss, backward) captured in a HIP graph: `warmup` eager steps on a side
+    stream (the capture recipe: the library's scratch, the GEMM plans and
+    torch's allocations are made there), then the capture.  Returns the graph
+    and the loss tensor its replays write; each replay leaves the step's
+    gradients in the parameters' .grad.  Needs the cfops backend with
+    model.ce_on_device, so that no op waits for the host."""
+    if model.backend != "cfops" or not model.ce_on_device:
+        raise ValueError("graph capture needs the cfops backend with ce_on_device")
+    params = model.params()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(warmup):
+            for p_ in params:
+                p_.grad = None
+            loss = model.loss(tokens, targets)
+            loss.backward()
+            del loss
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    model.check_targets()
+    for p_ in params:
+        p_.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_loss = model.loss(tokens, targets)
+        static_loss.backward()
+    return graph, static_loss
 
 
 def train_tok_s(batch: int = 8, seq: int = 512, layers: int = 30, rank: int = 16, steps: int = 3,
                 dtype=torch.float32, attn_dtype=None, device="cuda", backend: str = "cfops",
-                warmup: int = 3) -> dict:
+                warmup: int = 3, graph: bool = False) -> dict:
     """Build the model, run `warmup` untimed steps (the first allocates the
     library's scratch and plans; the clock settles over the next ones),
     then time `steps` forward+backward passes; returns tok/s and the step
-    time."""
+    time.  With `graph` (cfops backend) the step is captured in a HIP graph
+    after the warm-up steps and the timed steps are its replays: the same
+    kernels in the same order, without the host's launch work between
+    them."""
     model = SmolLM(layers, seq, rank, dtype, device, attn_dtype=attn_dtype, backend=backend)
     gen = torch.Generator(device=device)
     gen.manual_seed(7)
@@ -239,16 +291,28 @@ def train_tok_s(batch: int = 8, seq: int = 512, layers: int = 30, rank: int = 16
         return loss
 
     loss0 = step().item()
-    for _ in range(warmup - 1):
-        step()
+    out = {}
+    if graph:
+        model.ce_on_device = True
+        g, static_loss = capture_step(model, tokens, targets, max(warmup - 1, 1))
+        g.replay()
+        torch.cuda.synchronize()
+        model.check_targets()
+        out["graph_first_loss"] = static_loss.item()
+        run = g.replay
+    else:
+        for _ in range(warmup - 1):
+            step()
+        run = step
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        step()
+        run()
     torch.cuda.synchronize()
     per = (time.perf_counter() - t0) / steps
+    if graph:
+        model.check_targets()
     return {"value": batch * seq / per, "unit": "tok/s", "ms_per_step": per * 1e3, "batch": batch, "seq": seq,
             "layers": layers, "lora_rank": rank, "dtype": str(dtype).replace("torch.", ""),
             "attn_dtype": str(attn_dtype or dtype).replace("torch.", ""), "steps": steps, "warmup": warmup,
-            "first_loss": loss0,
-            "backend": backend}
+            "first_loss": loss0, "backend": backend, "graph": graph, **out}

@@ -80,6 +80,24 @@ int cfops_lm_head_ce(cfattn_ctx* ctx, const float* hn, const float* head, const 
                      size_t vocab, float* dhn, float* dhead, float* loss, void* stream);
 int cfops_set_head_chunk_limit(cfattn_ctx* ctx, size_t bytes);
 
+/* The loss block cfops_lm_head_ce_dev writes, in device memory. */
+typedef struct cfops_ce_result {
+    int32_t n_valid; /* rows scored (target != CFOPS_IGNORE_INDEX) */
+    int32_t bad_row; /* first row whose target is outside [0, vocab), or INT32_MAX */
+    float loss;      /* the mean cross-entropy over the scored rows */
+} cfops_ce_result;
+
+/* No reference counterpart: cfops_lm_head_ce for callers that capture the
+ * training step in a HIP graph or keep host waits out of it.  The same
+ * launches on `stream`, with the loss block written to `result` (device
+ * memory) and no wait for the stream: once the stream has drained,
+ * result->loss is the loss, and result->bad_row != INT32_MAX names a row
+ * whose target is out of range, which the caller reports (cfops_lm_head_ce
+ * fails with "target T out of range for vocab V" there).  t must be
+ * positive; dhn and dhead as in cfops_lm_head_ce. */
+int cfops_lm_head_ce_dev(cfattn_ctx* ctx, const float* hn, const float* head, const int64_t* targets, size_t t,
+                         size_t d, size_t vocab, float* dhn, float* dhead, cfops_ce_result* result, void* stream);
+
 /* Linear::forward (linear.rs:56-71): y [t,out] = x [t,in] . W^T (overwritten),
  * W [out,in].  With an adapter (lora_a non-null; A [rank,in], B [out,rank]):
  * xs [t,rank] = scale * x . A^T (overwritten) and y += xs . B^T. */
