@@ -110,7 +110,7 @@ struct cfattn_ctx {
     enum Slot {
         Q, K, V, O, LSE, DO_, DQ, DK, DV, QB, KB, VB, DOB, DELTA, PARTIAL, DQROT, DKROT, DS, FWD_SPLIT,
         // layer ops (cfops_capi.cpp)
-        OPS_PARTIAL, OPS_ROWLOSS, OPS_MISC, OPS_LOGITS, OPS_DXA, OPS_WS, OPS_LORA,
+        OPS_PARTIAL, OPS_ROWLOSS, OPS_MISC, OPS_LOGITS, OPS_DXA, OPS_WS, OPS_LORA, OPS_WEFF,
         // on-disk formats (cfio_capi.cpp): the two device staging chunks
         IO_STAGE,
         NSLOT

@@ -326,19 +326,27 @@ int cfops_linear_forward(cfattn_ctx* c, const float* x, const float* w, const fl
     if (!x || !w || !y) return fail(c, CFATTN_ERR_ARG, "null buffer");
     if (lora_a && (!lora_b || !xs || rank == 0)) return fail(c, CFATTN_ERR_ARG, "adapter needs A, B, xs and rank > 0");
     const hipStream_t st = to_stream(stream);
-    // linear.rs:58-69
-    CF_TRY(gemm(c, CFOPS_NT, x, w, y, t, in, out, 1.0f, false, st));
-    if (!lora_a) return CFATTN_OK;
-    const void* ptrs[] = {x, lora_a, lora_b, xs};
-    if (cfattn::lora_fused_applies(rank, t, in, out, ptrs, 4)) {
+    // linear.rs:58-69.  With an adapter on the streaming kernels' shapes the
+    // adapter is folded into the weight, y = x (W + scale B A)^T in one GEMM
+    // (the same sum, rounded once per element instead of twice), and xs is
+    // formed beside it for the backward.
+    const void* ptrs[] = {x, lora_a, lora_b, xs, w};
+    if (lora_a && cfattn::lora_fused_applies(rank, t, in, out, ptrs, 5)) {
         int rc = CFATTN_OK;
         float* part = static_cast<float*>(
             slot(c, cfattn_ctx::OPS_LORA, cfattn::lora_partial_floats(rank, t, in, out) * sizeof(float), &rc));
         if (!part) return rc;
-        CF_HIP(c, cfattn::launch_lora_fwd(rank, x, lora_a, lora_b, lora_scale, t, in, out, y, xs, part, st),
+        float* weff = static_cast<float*>(slot(c, cfattn_ctx::OPS_WEFF, out * in * sizeof(float), &rc));
+        if (!weff) return rc;
+        CF_HIP(c, cfattn::launch_lora_merge(rank, w, lora_a, lora_b, lora_scale, out, in, weff, st),
+               "lora merge launch");
+        CF_TRY(gemm(c, CFOPS_NT, x, weff, y, t, in, out, 1.0f, false, st));
+        CF_HIP(c, cfattn::launch_lora_fwd(rank, x, lora_a, lora_b, lora_scale, t, in, out, nullptr, xs, part, st),
                "lora forward launch");
         return CFATTN_OK;
     }
+    CF_TRY(gemm(c, CFOPS_NT, x, w, y, t, in, out, 1.0f, false, st));
+    if (!lora_a) return CFATTN_OK;
     CF_TRY(gemm(c, CFOPS_NT, x, lora_a, xs, t, in, rank, lora_scale, false, st));
     return gemm(c, CFOPS_NT, xs, lora_b, y, t, rank, out, 1.0f, true, st);
 }
@@ -351,23 +359,32 @@ int cfops_linear_backward(cfattn_ctx* c, const float* x, const float* xs, const 
     if (!x || !dy || !w || !dx) return fail(c, CFATTN_ERR_ARG, "null buffer");
     if (lora_a && (!lora_b || !xs || rank == 0)) return fail(c, CFATTN_ERR_ARG, "adapter needs A, B, xs and rank > 0");
     const hipStream_t st = to_stream(stream);
-    // linear.rs:75-90
-    CF_TRY(gemm(c, CFOPS_NN, dy, w, dx, t, out, in, 1.0f, true, st));
-    if (gw) CF_TRY(gemm(c, CFOPS_TN, dy, x, gw, out, t, in, 1.0f, true, st));
-    if (!lora_a) return CFATTN_OK;
+    // linear.rs:75-90.  With an adapter on the streaming kernels' shapes,
+    // dx += dy (W + scale B A) in one GEMM (the forward's folded weight),
+    // and the adapter kernels form dxa = scale dy B and the adapter's
+    // gradients only.
     int rc = CFATTN_OK;
-    const void* ptrs[] = {x, xs, dy, lora_a, lora_b};
-    if (cfattn::lora_fused_applies(rank, t, in, out, ptrs, 5)) {
+    const void* ptrs[] = {x, xs, dy, lora_a, lora_b, w};
+    if (lora_a && cfattn::lora_fused_applies(rank, t, in, out, ptrs, 6)) {
+        float* weff = static_cast<float*>(slot(c, cfattn_ctx::OPS_WEFF, out * in * sizeof(float), &rc));
+        if (!weff) return rc;
+        CF_HIP(c, cfattn::launch_lora_merge(rank, w, lora_a, lora_b, lora_scale, out, in, weff, st),
+               "lora merge launch");
+        CF_TRY(gemm(c, CFOPS_NN, dy, weff, dx, t, out, in, 1.0f, true, st));
+        if (gw) CF_TRY(gemm(c, CFOPS_TN, dy, x, gw, out, t, in, 1.0f, true, st));
         float* dxa = static_cast<float*>(slot(c, cfattn_ctx::OPS_DXA, t * rank * sizeof(float), &rc));
         if (!dxa) return rc;
         float* part = static_cast<float*>(
             slot(c, cfattn_ctx::OPS_LORA, cfattn::lora_partial_floats(rank, t, in, out) * sizeof(float), &rc));
         if (!part) return rc;
-        CF_HIP(c, cfattn::launch_lora_bwd(rank, x, xs, dy, lora_a, lora_b, lora_scale, t, in, out, dx, ga, gb, dxa,
-                                          part, st),
+        CF_HIP(c, cfattn::launch_lora_bwd(rank, x, xs, dy, lora_a, lora_b, lora_scale, t, in, out, nullptr, ga, gb,
+                                          dxa, part, st),
                "lora backward launch");
         return CFATTN_OK;
     }
+    CF_TRY(gemm(c, CFOPS_NN, dy, w, dx, t, out, in, 1.0f, true, st));
+    if (gw) CF_TRY(gemm(c, CFOPS_TN, dy, x, gw, out, t, in, 1.0f, true, st));
+    if (!lora_a) return CFATTN_OK;
     if (gb) CF_TRY(gemm(c, CFOPS_TN, dy, xs, gb, out, t, rank, 1.0f, true, st));
     float* dxa = static_cast<float*>(slot(c, cfattn_ctx::OPS_DXA, t * rank * sizeof(float), &rc));
     if (!dxa) return rc;

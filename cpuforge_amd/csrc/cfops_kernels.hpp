@@ -52,14 +52,18 @@ hipError_t launch_adamw(float* p, const float* g, float* m, float* v, size_t n, 
 // streaming kernels (lora.hip), for ranks 4, 8 and 16 with 16-byte aligned
 // rows; `part` is scratch of lora_partial_floats floats for the per-chunk
 // partial sums, which are added in chunk order:
-//   forward:  xs = scale * x A^T (overwritten), y += xs B^T;
-//   backward: dxa = scale * dy B (into `dxa`, t x rank), dx += dxa A, and when
-//             non-null gb += dy^T xs, ga += dxa^T x.
+//   forward:  xs = scale * x A^T (overwritten), y += xs B^T (y non-null);
+//   backward: dxa = scale * dy B (into `dxa`, t x rank), dx += dxa A (dx
+//             non-null), and when non-null gb += dy^T xs, ga += dxa^T x;
+//   merge:    weff = w + scale * B A ([out x in], w's layout), the base
+//             weight with the adapter folded in.
 constexpr int kLoraChunk = 64;  // tokens per partial sum of the gradients
 bool lora_fused_applies(size_t rank, size_t t, size_t in, size_t out, const void* const* ptrs, int nptr);
 size_t lora_partial_floats(size_t rank, size_t t, size_t in, size_t out);
 hipError_t launch_lora_fwd(size_t rank, const float* x, const float* a, const float* b, float scale, size_t t,
                            size_t in, size_t out, float* y, float* xs, float* part, hipStream_t st);
+hipError_t launch_lora_merge(size_t rank, const float* w, const float* a, const float* b, float scale, size_t out,
+                             size_t in, float* weff, hipStream_t st);
 hipError_t launch_lora_bwd(size_t rank, const float* x, const float* xs, const float* dy, const float* a,
                            const float* b, float scale, size_t t, size_t in, size_t out, float* dx, float* ga,
                            float* gb, float* dxa, float* part, hipStream_t st);

@@ -94,11 +94,11 @@ __global__ __launch_bounds__(256) void lora_rowdot_kernel(const float* __restric
 }
 
 // v[row][j] = scale * (sum over the nkc chunks, in order, of P[c][row][j]),
-// then dst[row][n] += sum_j v[row][j] * nmat(j, n), with nmat(j, n) =
+// then (ADD) dst[row][n] += sum_j v[row][j] * nmat(j, n), with nmat(j, n) =
 // N[n*R + j] (NCOLR: N is [ncol x R], the forward's B) or N[j*ncol + n] (the
 // backward's A, [R x ncol]).  The workgroups of column block 0 also write v
 // to vout (xs, or dxa).  Each lane updates four columns of four rows.
-template <int R, bool NCOLR>
+template <int R, bool NCOLR, bool ADD = true>
 __global__ __launch_bounds__(256) void lora_update_kernel(const float* __restrict__ P, int nkc, float scale,
                                                           const float* __restrict__ N, int t, int ncol,
                                                           float* __restrict__ dst, float* __restrict__ vout) {
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void lora_update_kernel(const float* __restric
     const int tid = threadIdx.x;
     const int n = blockIdx.y * kUpdCols + (tid & 63) * 4;
     const int rq = (tid >> 6) * 4;
-    const bool col_ok = n < ncol;
+    const bool col_ok = ADD && n < ncol;
     // The lane's destination values and N columns first: they do not
     // depend on v, so their latency overlaps the sums below.
     float nb[4][R];
@@ -261,6 +261,37 @@ __global__ __launch_bounds__(256) void lora_grad_reduce_kernel(const float* __re
     }
 }
 
+// Weff[o][i] = W[o][i] + scale * sum_j B[o][j] A[j][i]: the base weight with
+// the adapter merged in, so that x Weff^T = x W^T + (scale x A^T) B^T and
+// dy Weff = dy W + (scale dy B) A in one GEMM each.  The j sum is one FMA
+// chain in j order.  Each lane writes four consecutive columns of one row.
+template <int R>
+__global__ __launch_bounds__(256) void lora_merge_kernel(const float* __restrict__ W, const float* __restrict__ A,
+                                                         const float* __restrict__ B, float scale, int out, int in,
+                                                         float* __restrict__ Weff) {
+    const long e = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (e >= (long)out * in) return;
+    const int o = (int)(e / in), i = (int)(e % in);
+    float b[R];
+#pragma unroll
+    for (int j = 0; j < R; j += 4) {
+        const float4 v = ld4(B + (size_t)o * R + j);
+        b[j] = v.x, b[j + 1] = v.y, b[j + 2] = v.z, b[j + 3] = v.w;
+    }
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const float4 a = ld4(A + (size_t)j * in + i);
+        acc.x = __builtin_fmaf(b[j], a.x, acc.x);
+        acc.y = __builtin_fmaf(b[j], a.y, acc.y);
+        acc.z = __builtin_fmaf(b[j], a.z, acc.z);
+        acc.w = __builtin_fmaf(b[j], a.w, acc.w);
+    }
+    const float4 w = ld4(W + e);
+    *reinterpret_cast<float4*>(Weff + e) = make_float4(__builtin_fmaf(scale, acc.x, w.x), __builtin_fmaf(scale, acc.y, w.y),
+                                                       __builtin_fmaf(scale, acc.z, w.z), __builtin_fmaf(scale, acc.w, w.w));
+}
+
 int nchunks(int n, int c) { return (n + c - 1) / c; }
 
 template <int R>
@@ -270,8 +301,12 @@ hipError_t lora_fwd_r(const float* x, const float* a, const float* b, float scal
     lora_rowdot_kernel<R, true><<<dim3(nchunks(t, kDotRows), nkc), 256, 0, st>>>(x, a, t, in, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    lora_update_kernel<R, true><<<dim3(nchunks(t, kUpdRows), nchunks(out, kUpdCols)), 256, 0, st>>>(
-        part, nkc, scale, b, t, out, y, xs);
+    if (y)
+        lora_update_kernel<R, true><<<dim3(nchunks(t, kUpdRows), nchunks(out, kUpdCols)), 256, 0, st>>>(
+            part, nkc, scale, b, t, out, y, xs);
+    else
+        lora_update_kernel<R, true, false><<<dim3(nchunks(t, kUpdRows), 1), 256, 0, st>>>(part, nkc, scale, b, t, out,
+                                                                                           y, xs);
     return hipGetLastError();
 }
 
@@ -283,8 +318,12 @@ hipError_t lora_bwd_r(const float* x, const float* xs, const float* dy, const fl
     lora_rowdot_kernel<R, false><<<dim3(nchunks(t, kDotRows), nkc), 256, 0, st>>>(dy, b, t, out, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    lora_update_kernel<R, false><<<dim3(nchunks(t, kUpdRows), nchunks(in, kUpdCols)), 256, 0, st>>>(
-        part, nkc, scale, a, t, in, dx, dxa);
+    if (dx)
+        lora_update_kernel<R, false><<<dim3(nchunks(t, kUpdRows), nchunks(in, kUpdCols)), 256, 0, st>>>(
+            part, nkc, scale, a, t, in, dx, dxa);
+    else
+        lora_update_kernel<R, false, false><<<dim3(nchunks(t, kUpdRows), 1), 256, 0, st>>>(part, nkc, scale, a, t, in,
+                                                                                            dx, dxa);
     e = hipGetLastError();
     if (e != hipSuccess || (!ga && !gb)) return e;
     // The rowdot partials are consumed by now (same stream): reuse the buffer.
@@ -324,6 +363,18 @@ hipError_t launch_lora_fwd(size_t rank, const float* x, const float* a, const fl
         case 8: return lora_fwd_r<8>(x, a, b, scale, (int)t, (int)in, (int)out, y, xs, part, st);
         default: return lora_fwd_r<16>(x, a, b, scale, (int)t, (int)in, (int)out, y, xs, part, st);
     }
+}
+
+hipError_t launch_lora_merge(size_t rank, const float* w, const float* a, const float* b, float scale, size_t out,
+                             size_t in, float* weff, hipStream_t st) {
+    const long n4 = (long)((out * in + 3) / 4);
+    const dim3 grid((unsigned)((n4 + 255) / 256));
+    switch (rank) {
+        case 4: lora_merge_kernel<4><<<grid, 256, 0, st>>>(w, a, b, scale, (int)out, (int)in, weff); break;
+        case 8: lora_merge_kernel<8><<<grid, 256, 0, st>>>(w, a, b, scale, (int)out, (int)in, weff); break;
+        default: lora_merge_kernel<16><<<grid, 256, 0, st>>>(w, a, b, scale, (int)out, (int)in, weff); break;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_lora_bwd(size_t rank, const float* x, const float* xs, const float* dy, const float* a,

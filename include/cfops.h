@@ -100,13 +100,17 @@ int cfops_lm_head_ce_dev(cfattn_ctx* ctx, const float* hn, const float* head, co
 
 /* Linear::forward (linear.rs:56-71): y [t,out] = x [t,in] . W^T (overwritten),
  * W [out,in].  With an adapter (lora_a non-null; A [rank,in], B [out,rank]):
- * xs [t,rank] = scale * x . A^T (overwritten) and y += xs . B^T. */
+ * xs [t,rank] = scale * x . A^T (overwritten) and y += xs . B^T.  For ranks
+ * 4, 8 and 16 with in and out multiples of 4 and 16-byte aligned operands,
+ * y is formed as x . (W + scale * B . A)^T in one GEMM: the same sum,
+ * rounded differently (within f32 rounding of the reference's). */
 int cfops_linear_forward(cfattn_ctx* ctx, const float* x, const float* w, const float* lora_a, const float* lora_b,
                          float lora_scale, size_t t, size_t in, size_t out, size_t rank, float* y, float* xs,
                          void* stream);
 /* Linear::backward (linear.rs:73-91): dx += dy . W; gw += dy^T . x when gw is
  * non-null; with an adapter gb += dy^T . xs (gb non-null), and with
- * dxa = scale * dy . B: ga += dxa^T . x (ga non-null) and dx += dxa . A.
+ * dxa = scale * dy . B: ga += dxa^T . x (ga non-null) and dx += dxa . A
+ * (on the forward's fast shapes: dx += dy . (W + scale * B . A) in one GEMM).
  * NULL gradients are frozen tensors (the reference's empty LinGrad vectors). */
 int cfops_linear_backward(cfattn_ctx* ctx, const float* x, const float* xs, const float* dy, const float* w,
                           const float* lora_a, const float* lora_b, float lora_scale, size_t t, size_t in, size_t out,
