@@ -101,6 +101,10 @@ def parse():
     ap.add_argument("--zero-inputs", action="store_true",
                     help="diagnostic: q, k, v, dO all zero (the same kernels and instructions with the least bit "
                          "activity, to show what the board's power limit costs); not a benchmark figure")
+    ap.add_argument("--energy", type=float, default=0.0, metavar="SECONDS",
+                    help="board power (amd-smi) while loops of one instruction class run back to back for SECONDS "
+                         "each (LDS reads, v_fma_f32, bf16 MFMA on random and zero operands, an HBM copy) and at "
+                         "idle; prints its own JSON line")
     ap.add_argument("--sweep", action="store_true",
                     help="per-kernel times of the bf16 step at the --config heads and head_dim, the tokens held at "
                          "the config's batch x seq and the sequence halved from 4x seq (B shrinking to match) down "
@@ -354,6 +358,97 @@ def shape_sweep(a):
                       "head_dim": D, "cus": cus, "data": "synthetic (torch.randn, seed 1234, no RoPE)",
                       "config": {"workload": WORKLOAD[a.config], "config": a.config}, "rows": rows,
                       "fit": fits}), flush=True)
+
+
+def _smi_sampler(stop, out):
+    """amd-smi samples (time, board power W, median XCD GFX clock MHz) into
+    `out` until `stop` is set."""
+    import re
+    import shutil
+    import subprocess
+    smi = shutil.which("amd-smi") or "/opt/rocm/bin/amd-smi"
+    while not stop.is_set():
+        t = subprocess.run([smi, "metric", "-g", "0", "-p", "-c"], capture_output=True, text=True).stdout
+        pw = re.search(r"SOCKET_POWER:\s*([0-9.]+)\s*W", t)
+        clk = [int(c) for c in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*(\d+)\s*MHz", t)]
+        if pw and clk:
+            out.append((time.perf_counter(), float(pw.group(1)), sorted(clk)[len(clk) // 2]))
+
+
+def energy_probes(a):
+    """Board power per instruction class: each loop (cfattn_probe_loop,
+    cfattn_probe_mfma_peak, torch's device copy) runs back to back for
+    a.energy seconds while amd-smi is sampled (samples of the first 0.7 s
+    dropped), and the board is read idle.  Per class: median power and
+    clock, the loop's rate, and (power - idle power) / rate, an upper bound
+    of the energy per unit (it also carries the clocked-but-idle power,
+    which grows with the clock)."""
+    import threading
+
+    import torch
+
+    import cpuforge_amd as cf
+    ctx = cf.Context(0)
+
+    def run_for(fn):
+        samples, stop = [], threading.Event()
+        th = threading.Thread(target=_smi_sampler, args=(stop, samples), daemon=True)
+        t0 = time.perf_counter()
+        th.start()
+        rates = []
+        while time.perf_counter() - t0 < a.energy:
+            rates.append(fn())
+        torch.cuda.synchronize()
+        stop.set()
+        th.join()
+        kept = [(w, c) for ts, w, c in samples if ts - t0 > 0.7]
+        ws, cs = sorted(w for w, _ in kept), sorted(c for _, c in kept)
+        rs = sorted(r for r in rates if r)
+        return (ws[len(ws) // 2] if ws else None, cs[len(cs) // 2] if cs else None,
+                rs[len(rs) // 2] if rs else None, len(kept))
+
+    samples, stop = [], threading.Event()
+    th = threading.Thread(target=_smi_sampler, args=(stop, samples), daemon=True)
+    t0 = time.perf_counter()
+    th.start()
+    time.sleep(a.energy)
+    stop.set()
+    th.join()
+    idle = sorted(w for ts, w, _ in samples if ts - t0 > 0.5)
+    idle_w = idle[len(idle) // 2] if idle else None
+    x = torch.empty(1 << 28, device="cuda")
+    y = torch.empty_like(x)
+    x.normal_()
+    cp_bytes = 2.0 * x.numel() * 4
+
+    def copy_rate():
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        y.copy_(x)
+        e1.record()
+        e1.synchronize()
+        return cp_bytes / (e0.elapsed_time(e1) * 1e-3)
+
+    classes = {
+        "lds_read": (lambda: ctx.probe_loop("lds"), "B/s", "pJ/B"),
+        "valu_fma_f32": (lambda: ctx.probe_loop("valu"), "lane-op/s", "pJ/lane-op"),
+        "mfma_bf16_random": (lambda: ctx.probe_mfma_peak(False, 20000) * 1e12 / 32768.0, "MFMA/s", "pJ/MFMA"),
+        "mfma_bf16_zeros": (lambda: ctx.probe_mfma_peak(True, 20000) * 1e12 / 32768.0, "MFMA/s", "pJ/MFMA"),
+        "hbm_copy": (copy_rate, "B/s", "pJ/B"),
+    }
+    out = {}
+    for name, (fn, unit, eunit) in classes.items():
+        fn()
+        pw, ck, rate, n = run_for(fn)
+        e = round((pw - idle_w) / rate * 1e12, 3) if pw and idle_w and rate else None
+        out[name] = {"power_w": pw, "clock_mhz": ck, "rate": rate, "unit": unit, "samples": n,
+                     "over_idle": e, "over_idle_unit": eunit}
+        print(f"bench: energy {name}: {out[name]}", file=sys.stderr, flush=True)
+    ctx.close()
+    print(json.dumps({"metric": "board power per instruction class (amd-smi)", "value": idle_w, "unit": "W idle",
+                      "higher_is_better": False, "seconds_per_class": a.energy, "idle_w": idle_w,
+                      "data": "loop probes (cfattn_probe_loop, cfattn_probe_mfma_peak) and torch's device copy",
+                      "classes": out}), flush=True)
 
 
 def power_clock(a):
@@ -935,6 +1030,9 @@ def main():
         return
     if a.sweep:
         shape_sweep(a)
+        return
+    if a.energy > 0:
+        energy_probes(a)
         return
     if a.peak:
         import cpuforge_amd as cf

@@ -67,6 +67,7 @@ SIGNATURES = {
     "cfattn_profile_select": (C.c_int, [_vp, C.c_uint]),
     "cfattn_profile_read": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]),
     "cfattn_probe_mfma_peak": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(C.c_double)]),
+    "cfattn_probe_loop": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(C.c_double)]),
     "cfattn_fwd_stats_enable": (C.c_int, [_vp, C.c_int]),
     "cfattn_fwd_stats_read": (C.c_int, [_vp, C.POINTER(C.c_longlong)]),
     "cfattn_kernel_name": (C.c_char_p, [C.c_int]),

@@ -128,6 +128,15 @@ class Context:
                    self.handle)
         return out.value
 
+    def probe_loop(self, kind: str, iters: int = 20000) -> float:
+        """Rate of a loop of one instruction class on every SIMD
+        (cfattn_probe_loop): "lds" (16-byte LDS reads, bytes/s) or "valu"
+        (v_fma_f32, lane operations/s)."""
+        code = {"lds": 0, "valu": 1}[kind]
+        out = C.c_double()
+        _lib.check(self._lib.cfattn_probe_loop(self.handle, code, int(iters), C.byref(out)), self.handle)
+        return out.value
+
     def profile_read(self) -> dict:
         """{kernel name: (total ms, launches)} since profiling was enabled."""
         out = {}

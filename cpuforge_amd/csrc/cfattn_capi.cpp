@@ -655,6 +655,18 @@ int cfattn_probe_mfma_peak(cfattn_ctx* c, int zeros, int iters, double* tflops) 
     return CFATTN_OK;
 }
 
+int cfattn_probe_loop(cfattn_ctx* c, int kind, int iters, double* rate) {
+    if (!c || !rate) return CFATTN_ERR_ARG;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->err.clear();
+    if (iters <= 0) return fail(c, CFATTN_ERR_ARG, "iters must be positive (got %d)", iters);
+    if (kind != cfattn::kProbeLds && kind != cfattn::kProbeValu)
+        return fail(c, CFATTN_ERR_ARG, "unknown probe %d", kind);
+    DeviceGuard dg(c->device);
+    CF_HIP(c, cfattn::probe_loop(c->stream, kind, iters, rate), "loop probe");
+    return CFATTN_OK;
+}
+
 int cfattn_profile_enable(cfattn_ctx* c, int on) {
     if (!c) return CFATTN_ERR_ARG;
     std::lock_guard<std::mutex> lk(c->mu);

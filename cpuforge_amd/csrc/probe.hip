@@ -1,5 +1,6 @@
-// Matrix-pipe throughput probe: the ceiling the bf16 attention kernels are
-// measured against on the board they run on.
+// Throughput probes: the matrix-pipe ceiling the bf16 attention kernels are
+// measured against on the board they run on, and loops of LDS reads and of
+// VALU operations for the power each instruction class draws.
 //
 // The published MI355X figure (2516.6 TFLOP/s dense bf16) assumes the 2.4 GHz
 // top clock.  Under a sustained MFMA load the board's power limit sets the
@@ -74,6 +75,49 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, int zeros, f
     }
 }
 
+// Loops of one other instruction class, one 1024-thread workgroup per CU
+// (four waves per SIMD), for the board power each draws at its rate:
+//   LDS: 16-byte reads of a 64 KiB LDS buffer, a wave's 64 lanes on 1 KiB of
+//        consecutive bytes (no bank conflict), eight per loop iteration;
+//   VALU: v_fma_f32 on eight independent registers, sixteen per iteration.
+__global__ __launch_bounds__(1024) void lds_probe_kernel(int iters, float* sink) {
+    __shared__ float4 buf[4096];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < 4096; i += 1024)
+        buf[i] = make_float4((float)i, (float)(i ^ 0x55), (float)(i * 3), (float)(i + 7));
+    __syncthreads();
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int idx = tid & 4095;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float4 v = buf[(idx + u * 64) & 4095];
+            acc.x += v.x, acc.y += v.y, acc.z += v.z, acc.w += v.w;
+        }
+        idx = (idx + 512) & 4095;
+    }
+    // Keeps the loop live; callers pass no sink.
+    if (sink) sink[blockIdx.x * 1024 + tid] = acc.x + acc.y + acc.z + acc.w;
+}
+
+__global__ __launch_bounds__(1024) void valu_probe_kernel(int iters, float* sink) {
+    float a[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) a[i] = (float)threadIdx.x * 1e-3f + 0.1f * (float)i;
+    const float m = 0.999f, c = 0.001f;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            asm volatile("v_fma_f32 %0, %0, %1, %2\n\tv_fma_f32 %0, %0, %1, %2" : "+v"(a[i]) : "v"(m), "v"(c));
+    }
+    if (sink) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) s += a[i];
+        sink[blockIdx.x * 1024 + threadIdx.x] = s;
+    }
+}
+
 }  // namespace
 
 // MFMAs per wave per loop iteration and FLOPs per MFMA (32 x 32 x 16 x 2).
@@ -106,6 +150,40 @@ hipError_t probe_mfma_bf16(hipStream_t st, int zeros, int iters, double* tflops)
     if (e != hipSuccess) return e;
     const double flops = (double)wgs * 4.0 * (double)iters * kProbeMfmaPerIter * kProbeFlopsPerMfma;
     *tflops = ms > 0.0f ? flops / ((double)ms * 1e-3) / 1e12 : 0.0;
+    return hipSuccess;
+}
+
+hipError_t probe_loop(hipStream_t st, int kind, int iters, double* rate) {
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if ((e = hipEventCreate(&e0)) != hipSuccess) return e;
+    if ((e = hipEventCreate(&e1)) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return e;
+    }
+    float ms = 0.0f;
+    e = hipEventRecord(e0, st);
+    if (e == hipSuccess) {
+        if (kind == kProbeLds)
+            hipLaunchKernelGGL(lds_probe_kernel, dim3(cus), dim3(1024), 0, st, iters, (float*)nullptr);
+        else
+            hipLaunchKernelGGL(valu_probe_kernel, dim3(cus), dim3(1024), 0, st, iters, (float*)nullptr);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipEventRecord(e1, st);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (e != hipSuccess) return e;
+    // Bytes read from LDS, or lane operations (one per lane per v_fma_f32).
+    const double per_iter = kind == kProbeLds ? 8.0 * 16.0 : 16.0;
+    const double units = (double)cus * 1024.0 * (double)iters * per_iter;
+    *rate = ms > 0.0f ? units / ((double)ms * 1e-3) : 0.0;
     return hipSuccess;
 }
 

@@ -242,6 +242,12 @@ int cfattn_fwd_stats_read(cfattn_ctx* ctx, long long* settles);
  * 2.4 GHz top clock, sets the sustained rate: run it long enough (tens of
  * milliseconds) for the clock to settle. */
 int cfattn_probe_mfma_peak(cfattn_ctx* ctx, int zeros, int iters, double* tflops);
+/* No reference counterpart: loops of one instruction class for the board
+ * power each draws (read beside it with amd-smi).  kind 0: 16-byte LDS reads
+ * (rate in bytes/s); kind 1: v_fma_f32 (rate in lane operations/s).  Four
+ * waves per SIMD on every CU, `iters` loop iterations, on the context's
+ * stream; waits for the run. */
+int cfattn_probe_loop(cfattn_ctx* ctx, int kind, int iters, double* rate);
 /* Name of kernel id `kernel` ("attn_fwd", "attn_bwd_dkdv", ...), or NULL. */
 const char* cfattn_kernel_name(int kernel);
 int cfattn_kernel_count(void);
