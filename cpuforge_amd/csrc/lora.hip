@@ -288,8 +288,9 @@ __global__ __launch_bounds__(256) void lora_merge_kernel(const float* __restrict
         acc.w = __builtin_fmaf(b[j], a.w, acc.w);
     }
     const float4 w = ld4(W + e);
-    *reinterpret_cast<float4*>(Weff + e) = make_float4(__builtin_fmaf(scale, acc.x, w.x), __builtin_fmaf(scale, acc.y, w.y),
-                                                       __builtin_fmaf(scale, acc.z, w.z), __builtin_fmaf(scale, acc.w, w.w));
+    const float4 r = make_float4(__builtin_fmaf(scale, acc.x, w.x), __builtin_fmaf(scale, acc.y, w.y),
+                                 __builtin_fmaf(scale, acc.z, w.z), __builtin_fmaf(scale, acc.w, w.w));
+    *reinterpret_cast<float4*>(Weff + e) = r;
 }
 
 int nchunks(int n, int c) { return (n + c - 1) / c; }
@@ -367,8 +368,9 @@ hipError_t launch_lora_fwd(size_t rank, const float* x, const float* a, const fl
 
 hipError_t launch_lora_merge(size_t rank, const float* w, const float* a, const float* b, float scale, size_t out,
                              size_t in, float* weff, hipStream_t st) {
-    const long n4 = (long)((out * in + 3) / 4);
-    const dim3 grid((unsigned)((n4 + 255) / 256));
+    const long blocks = (long)((out * in / 4 + 255) / 256);  // in % 4 == 0: whole float4 rows
+    if (blocks > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    const dim3 grid((unsigned)blocks);
     switch (rank) {
         case 4: lora_merge_kernel<4><<<grid, 256, 0, st>>>(w, a, b, scale, (int)out, (int)in, weff); break;
         case 8: lora_merge_kernel<8><<<grid, 256, 0, st>>>(w, a, b, scale, (int)out, (int)in, weff); break;
