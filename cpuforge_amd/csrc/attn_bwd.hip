@@ -23,6 +23,8 @@
 #include "cfattn_kernels.hpp"
 #include "attn_bwd_common.hpp"
 
+#include <algorithm>
+
 namespace cfattn {
 
 // Eight consecutive values as f32 (16-byte aligned source).
@@ -620,6 +622,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         if (kt + 1 < n_kt) step(kt + 1, sK1, sV1, sK0, sV0);
     }
 
+    if (p.epi == kEpiUnrotNorm) {
+        // Every lane takes part (the row's lane pair, the wave's gain sums).
+        // LDS is free (the loop ends with a barrier): wave w stages its q_pre
+        // rows in the K or V buffer w.
+        const bool ok = wave_active && row_ok;
+        const int wu = wave_uniform(wave);
+        float* xs = reinterpret_cast<float*>(wu == 0 ? sK0 : wu == 1 ? sK1 : wu == 2 ? sV0 : sV1);
+        const long r = ((long)b * p.seq + tq) * p.nh + head;
+        stage_norm_row<NDB>(p.norm_qx + (ok ? r : 0) * DP, xs, hh);
+#pragma unroll
+        for (int db = 0; db < NDB; db++) dqt[db] *= p.scale;
+        const float inv = ok ? p.norm_qr[r] : 0.0f;
+        float4 cur[NDB][4];
+        load_grad_row<NDB>(cur, p.dq + qoff, hh, ok);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        write_grad_row_norm<NDB>(p.dq + qoff, xs, inv, p.norm_qw, dqt, lane, tq, ok, p, cur);
+        const int slot = blockIdx.x * NW + wave;
+        norm_partial_store<NDB>(dqt, lane, xs, p.norm_part + (long)slot * DP, slot < p.norm_nq);
+        return;
+    }
     if (!wave_active || !row_ok) return;
 #pragma unroll
     for (int db = 0; db < NDB; db++) dqt[db] *= p.scale;  // dS was accumulated without the softmax scale
@@ -807,6 +829,26 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
         if (kt + 2 < n_kt) step(kt + 2, sK2, sS2, sK1, sS1);
     }
 
+    if (p.epi == kEpiUnrotNorm) {
+        // Every lane takes part (the row's lane pair, the wave's gain sums).
+        // The ring is free: every wave has passed the loop's last barrier.
+        // Wave w stages its q_pre rows in 16 KiB of it: waves 0-5 in the dS
+        // buffers, 6 and 7 in the first two K buffers.
+        bf16_bits* region = wv == 7 ? sK1 : wv == 6 ? sK0 : wv >= 4 ? sS2 : wv >= 2 ? sS1 : sS0;
+        if (wv < 6) region += (wv & 1) * (NW * NKB * SB / 2);
+        float* xs = reinterpret_cast<float*>(region);
+        const long r = ((long)b * p.seq + tq) * p.nh + head;
+        stage_norm_row<NDB>(p.norm_qx + (row_ok ? r : 0) * DP, xs, hh);
+#pragma unroll
+        for (int db = 0; db < NDB; db++) dqt[db] *= p.scale;
+        const float inv = row_ok ? p.norm_qr[r] : 0.0f;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // A row past the end (pre false) writes nothing: dq_pre is unused.
+        write_grad_row_norm<NDB>(dq_row, xs, inv, p.norm_qw, dqt, lane, tq, row_ok, p, dq_pre);
+        const int slot = blockIdx.x * NW + wave;
+        norm_partial_store<NDB>(dqt, lane, xs, p.norm_part + (long)slot * DP, slot < p.norm_nq);
+        return;
+    }
     if (!row_ok) return;
 #pragma unroll
     for (int db = 0; db < NDB; db++) dqt[db] *= p.scale;  // dS was stored without the softmax scale
@@ -1203,6 +1245,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             if (s + 1 < n_steps) step(s + 1, sQ1, sO1, sQ0, sO0);
         }
 
+        if (p.epi == kEpiUnrotNorm) {
+            // Both roles: after this barrier no wave reads the Q/dO tiles,
+            // whose buffers the dS waves' epilogue then reuses.
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
+        if constexpr (!PW) {
+            if (p.epi == kEpiUnrotNorm) {
+                // Every lane of the dS wave takes part (the row's lane pair,
+                // the wave's gain sums); slice s stages its k_pre rows in
+                // buffer s of the Q and dO tiles.
+                const bool ok = wave_active && kw < p.seq;
+                float* xs = reinterpret_cast<float*>(slice == 0 ? sQ0 : slice == 1 ? sQ1 : slice == 2 ? sO0 : sO1);
+                const long r = ((long)b * p.seq + kw) * p.nkv + g;
+                stage_norm_row<NDB>(p.norm_kx + (ok ? r : 0) * DP, xs, hh);
+#pragma unroll
+                for (int db = 0; db < NDB; db++) acc[db] *= p.scale;
+                const float inv = ok ? p.norm_kr[r] : 0.0f;
+                float4 cur[NDB][4];
+                load_grad_row<NDB>(cur, p.dk + r * DP, hh, ok);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                write_grad_row_norm<NDB>(p.dk + r * DP, xs, inv, p.norm_kw, acc, lane, kw, ok, p, cur);
+                const int slot = blockIdx.x * 4 + slice;
+                norm_partial_store<NDB>(acc, lane, xs, p.norm_part + (long)(p.norm_nq + slot) * DP, slot < p.norm_nk);
+                return;
+            }
+        }
         if (!wave_active || kw >= p.seq) return;
         float* row = (PW ? p.dv : p.dk) + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
         if constexpr (PW) {
@@ -1276,6 +1346,27 @@ static bool fast_bf16_applies(Dtype dt, const Dims& d, const void* d_o, const vo
     return dt == kBF16 && vec_ok && g_vec_ok && (d.hd == 64 || d.hd == 128) && tu.bwd_kv_waves == 0;
 }
 
+bool attn_bwd_norm_dk_epilogue(const Dims& d, const Tuning& tu) {
+    return !(d.hd == 128 && tu.dkdv_variant != kDkdvWaveSpecialised);
+}
+
+size_t attn_bwd_norm_part_floats(const Dims& d, const Tuning& tu) {
+    if (d.batch <= 0 || d.seq <= 0 || d.nh <= 0 || d.nkv <= 0 || d.nh % d.nkv != 0) return 0;
+    // The fast path's grids (launch_attn_bwd): the larger of the two dQ
+    // kernels' wave counts, and the dK waves of either dK/dV kernel.
+    const int group = d.nh / d.nkv;
+    const int hpw = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    const long n_sub = group / hpw;
+    long nq = 0;
+    for (int waves : {kDqWaves, kDqDsWaves}) {
+        const int tpw = waves / hpw;
+        const long n_tt = (d.seq + 32L * tpw - 1) / (32L * tpw);
+        nq = std::max(nq, n_tt * d.nkv * n_sub * d.batch * waves);
+    }
+    const long n_wg_kv = (d.seq + 127L) / 128L * d.nkv * d.batch;
+    return (size_t)(nq + (attn_bwd_norm_dk_epilogue(d, tu) ? n_wg_kv * 4 : 0)) * d.hd;
+}
+
 bool attn_bwd_epilogue_applies(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k,
                                const void* v, const float* dq, const float* dk, const float* dv, const Tuning& tu) {
     return fast_bf16_applies(dt, d, d_o, q, k, v, dq, dk, dv, tu);
@@ -1286,11 +1377,24 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
                            hipStream_t st, const Tuning& tu, void* ds, size_t ds_bytes, const BwdEpilogue* epi) {
     if (d.batch == 0 || d.seq == 0 || d.nh == 0) return hipSuccess;
     const bool fast = fast_bf16_applies(dt, d, d_o, q, k, v, dq, dk, dv, tu);
-    // The epilogue reads the cos/sin rows 16 bytes at a time.
+    // The epilogue reads the cos/sin rows (and with the norm the pre-norm
+    // rows and the gains) 16 bytes at a time.
     if (epi && epi->mode != kEpiAdd &&
         (!fast || !epi->cos || !epi->sin ||
          (reinterpret_cast<uintptr_t>(epi->cos) | reinterpret_cast<uintptr_t>(epi->sin)) % 16 != 0))
         return hipErrorInvalidValue;
+    const int mode_k = !epi ? kEpiAdd : epi->mode_k < 0 ? epi->mode : epi->mode_k;
+    if (epi && mode_k != epi->mode && !(epi->mode == kEpiUnrotNorm && mode_k == kEpiUnrotStore))
+        return hipErrorInvalidValue;
+    if (mode_k == kEpiUnrotNorm && !attn_bwd_norm_dk_epilogue(d, tu)) return hipErrorInvalidValue;
+    if (epi && epi->mode == kEpiUnrotNorm) {
+        const BwdNorm& n = epi->norm;
+        if (!n.q_x || !n.k_x || !n.q_rstd || !n.k_rstd || !n.qw || !n.kw || !n.dqw || !n.dkw || !n.part ||
+            (reinterpret_cast<uintptr_t>(n.q_x) | reinterpret_cast<uintptr_t>(n.k_x) |
+             reinterpret_cast<uintptr_t>(n.qw) | reinterpret_cast<uintptr_t>(n.kw) |
+             reinterpret_cast<uintptr_t>(n.part)) % 16 != 0)
+            return hipErrorInvalidValue;
+    }
     BwdParams p{};
     p.d_o = d_o;
     p.q = q;
@@ -1342,6 +1446,15 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
         p.rope_cos = epi->cos;
         p.rope_sin = epi->sin;
         p.rope_pos0 = epi->pos0;
+        if (epi->mode == kEpiUnrotNorm) {
+            p.norm_qx = epi->norm.q_x;
+            p.norm_kx = epi->norm.k_x;
+            p.norm_qr = epi->norm.q_rstd;
+            p.norm_kr = epi->norm.k_rstd;
+            p.norm_qw = epi->norm.qw;
+            p.norm_kw = epi->norm.kw;
+            p.norm_part = epi->norm.part;
+        }
     }
     if (fast) {
         // Fast paths: the dQ kernel runs kDqWaves waves per workgroup, dK/dV eight.
@@ -1353,9 +1466,28 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
         if (nq_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
         p.n_wg_q = (int)nq_wg;
         const long rows = (long)p.batch * p.seq * p.nh;
+        const bool k64 = d.hd == 128 && tu.dkdv_variant != kDkdvWaveSpecialised;
         // The one-wave-per-SIMD dK/dV kernel reads lse * log2(e) rows, which
         // the delta kernel writes after the delta rows.
-        if (d.hd == 128 && tu.dkdv_variant != kDkdvWaveSpecialised) p.lse2 = delta + rows;
+        if (k64) p.lse2 = delta + rows;
+        const size_t need = attn_bwd_ds_bytes(dt, d);
+        const bool use_ds = ds != nullptr && need > 0 && ds_bytes >= need;
+        // The stored-dS dQ kernel's grid: kDqDsWaves waves per workgroup, the
+        // group's heads x query blocks.
+        const int tpw_ds = kDqDsWaves / p.hpw;
+        const int n_ttiles_ds = (d.seq + 32 * tpw_ds - 1) / (32 * tpw_ds);
+        const long n_wg_ds = (long)n_ttiles_ds * d.nkv * p.n_sub * d.batch;
+        if (use_ds && n_wg_ds > 0x7fffffffL) return hipErrorInvalidConfiguration;
+        if (p.epi == kEpiUnrotNorm) {
+            // One gain partial per wave that writes dQ rows, then per dS wave
+            // of the two-waves-per-SIMD dK/dV kernel (four per workgroup)
+            // when dK has the norm epilogue too.
+            const long nq = use_ds ? n_wg_ds * kDqDsWaves : (long)p.n_wg_q * kDqWaves;
+            const long nk = mode_k == kEpiUnrotNorm ? (long)p.n_wg_kv * 4 : 0;
+            if (nq + nk > 0x7fffffffL || (size_t)(nq + nk) * d.hd > epi->norm.part_floats) return hipErrorInvalidValue;
+            p.norm_nq = (int)nq;
+            p.norm_nk = (int)nk;
+        }
         hipError_t e;
         {
             TimedLaunch tl(tu.timer, kKernBwdDelta, st);
@@ -1364,16 +1496,17 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
             e = hipGetLastError();
         }
         if (e != hipSuccess) return e;
-        const size_t need = attn_bwd_ds_bytes(dt, d);
-        const bool use_ds = ds != nullptr && need > 0 && ds_bytes >= need;
         if (use_ds) {
             p.ds = static_cast<bf16_bits*>(ds);
             const long nqb = (d.seq + 31) / 32;
             p.ds_ntri = nqb * (nqb + 1) / 2;
         }
+        // The dK/dV kernel writes dK rows per mode_k; dQ rows follow `mode`.
+        const int epi_q = p.epi;
+        p.epi = mode_k;
         {
             TimedLaunch tl(tu.timer, kKernBwdDkdv, st);
-            if (d.hd == 128 && tu.dkdv_variant != kDkdvWaveSpecialised) {
+            if (k64) {
                 launch_attn_bwd_dkdv_k64(p, use_ds, st);
             } else if (d.hd == 128) {
                 if (use_ds)
@@ -1386,25 +1519,26 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
             e = hipGetLastError();
         }
         if (e != hipSuccess) return e;
-        TimedLaunch tl(tu.timer, kKernBwdDq, st);
-        if (use_ds) {
-            // kDqDsWaves waves per workgroup: the group's heads x query blocks.
-            p.tpw = kDqDsWaves / p.hpw;
-            p.n_ttiles = (d.seq + 32 * p.tpw - 1) / (32 * p.tpw);
-            const long n = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
-            if (n > 0x7fffffffL) return hipErrorInvalidConfiguration;
-            p.n_wg_q = (int)n;
-            hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<128, 64, kDqDsWaves>), dim3(p.n_wg_q), dim3(64 * kDqDsWaves), 0,
-                               st, p);
-            return hipGetLastError();
+        p.epi = epi_q;
+        {
+            TimedLaunch tl(tu.timer, kKernBwdDq, st);
+            if (use_ds) {
+                p.tpw = tpw_ds;
+                p.n_ttiles = n_ttiles_ds;
+                p.n_wg_q = (int)n_wg_ds;
+                hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<128, 64, kDqDsWaves>), dim3(p.n_wg_q),
+                                   dim3(64 * kDqDsWaves), 0, st, p);
+            } else if (d.hd == 128) {
+                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 64, kDqWaves>), dim3(p.n_wg_q), dim3(64 * kDqWaves),
+                                   0, st, p);
+            } else {
+                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, 128, kDqWaves>), dim3(p.n_wg_q), dim3(64 * kDqWaves),
+                                   0, st, p);
+            }
+            e = hipGetLastError();
         }
-        if (d.hd == 128)
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 64, kDqWaves>), dim3(p.n_wg_q), dim3(64 * kDqWaves), 0, st,
-                               p);
-        else
-            hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, 128, kDqWaves>), dim3(p.n_wg_q), dim3(64 * kDqWaves), 0, st,
-                               p);
-        return hipGetLastError();
+        if (e != hipSuccess || p.epi != kEpiUnrotNorm) return e;
+        return launch_norm_gain_reduce(p.norm_part, p.norm_nq, p.norm_nk, d.hd, epi->norm.dqw, epi->norm.dkw, st);
     }
     if (dt == kF32 && attn_f32_fast_applies(d, p.vec_ok, p.g_vec_ok) && tu.bwd_kv_waves == 0 && ds != nullptr &&
         ds_bytes >= attn_f32_scratch_bytes(d)) {

@@ -74,6 +74,18 @@ struct BwdParams {
     const float* rope_cos;
     const float* rope_sin;
     int rope_pos0;
+    // kEpiUnrotNorm (BwdNorm): pre-norm rows, rstd and gains of q and k;
+    // the wave writing dQ rows w of its kernel's grid puts its gain partial
+    // in row w of norm_part (w < norm_nq), the wave writing dK rows w in row
+    // norm_nq + w (w < norm_nk).
+    const float* norm_qx;
+    const float* norm_kx;
+    const float* norm_qr;
+    const float* norm_kr;
+    const float* norm_qw;
+    const float* norm_kw;
+    float* norm_part;
+    int norm_nq, norm_nk;
 };
 
 // fp32 fast path (attn_f32.hip): head_dim 64 or 128, 16-byte aligned rows.

@@ -6,6 +6,7 @@
 // There is no CPU compute path: every result comes from the HIP kernels.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -535,6 +536,50 @@ int cfattn_fused_bwd(cfattn_ctx* c, cfattn_shape s, size_t batch, int dtype, con
         if (!pr->q_norm) {
             epi.mode = cfattn::kEpiUnrotAdd;
             return cfattn_bwd_locked(c, s, batch, dtype, d_o, q, k, v, o, lse, dq_pre, dk_pre, dv, stream, &epi);
+        }
+        if (!q_pre || !k_pre || !q_rstd || !k_rstd || !dq_norm || !dk_norm)
+            return fail(c, CFATTN_ERR_ARG, "q/k norm backward needs q_pre, k_pre, rstd and gain-gradient buffers");
+        // With the norm the epilogues also run its backward (layer.rs:195-206)
+        // when its rows and gains can be read 16 bytes at a time: dq_pre/dk_pre
+        // get the same bits as from the separate pass below, the gain
+        // gradients the same sums in another fixed order.  Where the dK/dV
+        // kernel has no norm epilogue (head_dim 128) it stores the unrotated
+        // dK rows and K's norm backward runs as its own pass.
+        const uintptr_t al = reinterpret_cast<uintptr_t>(q_pre) | reinterpret_cast<uintptr_t>(k_pre) |
+                             reinterpret_cast<uintptr_t>(P.qw) | reinterpret_cast<uintptr_t>(P.kw);
+        const cfattn::Tuning tu = c->tuning();
+        if (tu.norm_epilogue && al % 16 == 0) {
+            const cfattn::Dims dd = dims_of(s, batch);
+            const bool kfused = cfattn::attn_bwd_norm_dk_epilogue(dd, tu);
+            const size_t nf = cfattn::attn_bwd_norm_part_floats(dd, tu);
+            const size_t pf = kfused ? nf : std::max(nf, cfattn::prologue_bwd_scratch_floats(dd));
+            float* part = static_cast<float*>(slot(c, cfattn_ctx::PARTIAL, pf * 4, &rc));
+            if (!part) return rc;
+            float* dk_dst = dk_pre;
+            if (!kfused) {
+                dk_dst = static_cast<float*>(slot(c, cfattn_ctx::DKROT, nk * 4, &rc));
+                if (!dk_dst) return rc;
+            }
+            epi.mode = cfattn::kEpiUnrotNorm;
+            epi.mode_k = kfused ? cfattn::kEpiUnrotNorm : cfattn::kEpiUnrotStore;
+            epi.norm.q_x = q_pre;
+            epi.norm.k_x = k_pre;
+            epi.norm.q_rstd = q_rstd;
+            epi.norm.k_rstd = k_rstd;
+            epi.norm.qw = P.qw;
+            epi.norm.kw = P.kw;
+            epi.norm.dqw = dq_norm;
+            epi.norm.dkw = dk_norm;
+            epi.norm.part = part;
+            epi.norm.part_floats = nf;
+            CF_TRY(cfattn_bwd_locked(c, s, batch, dtype, d_o, q, k, v, o, lse, dq_pre, dk_dst, dv, stream, &epi));
+            if (kfused) return CFATTN_OK;
+            CF_HIP(c,
+                   cfattn::launch_prologue_bwd(dd, P, nullptr, dk_dst, nullptr, k_pre, nullptr, k_rstd, nullptr, dk_pre,
+                                               nullptr, dk_norm, part, pick_stream(c, stream), c->timer,
+                                               /*unrotated=*/true, /*k_only=*/true),
+                   "prologue backward launch");
+            return CFATTN_OK;
         }
         epi.mode = cfattn::kEpiUnrotStore;
         float* dy_q = static_cast<float*>(slot(c, cfattn_ctx::DQROT, nq * 4, &rc));

@@ -156,6 +156,11 @@ struct cfattn_ctx {
         // at head_dim 128 (kept for comparison and measurement).
         const char* f = std::getenv("CFATTN_FWD_KERNEL");
         if (f && std::strcmp(f, "two") == 0) t.fwd_variant = cfattn::kFwdTwoPerSimd;
+        // CFATTN_NORM_EPILOGUE=0 runs the fused backward's Qwen3 norm as its
+        // own pass after the attention kernels (same dq_pre/dk_pre bits; kept
+        // for comparison and measurement).
+        const char* n = std::getenv("CFATTN_NORM_EPILOGUE");
+        if (n && std::strcmp(n, "0") == 0) t.norm_epilogue = 0;
         return t;
     }
 };

@@ -56,6 +56,9 @@ struct Tuning {
     int bwd_kv_waves = 0;
     int dkdv_variant = kDkdvAuto;
     int fwd_variant = kFwdAuto;
+    // The fused backward's Qwen3 norm in the dQ/dK epilogues (kEpiUnrotNorm);
+    // 0: the epilogues store the unrotated rows and a separate norm pass runs.
+    int norm_epilogue = 1;
     KernelTimer* timer = nullptr;
     // Device counter of the bf16 head_dim-128 forward's settled wave-tiles
     // (the slow path of its row-sum guard), incremented when non-null.
@@ -103,23 +106,59 @@ size_t attn_bwd_ds_bytes(Dtype dt, const Dims& d);
 enum EpilogueMode {
     kEpiAdd = 0,          // dq/dk += rows
     kEpiUnrotAdd = 1,     // dq/dk += inverse-RoPE(rows)
-    kEpiUnrotStore = 2    // dq/dk  = inverse-RoPE(rows), every row written once
+    kEpiUnrotStore = 2,   // dq/dk  = inverse-RoPE(rows), every row written once
+    kEpiUnrotNorm = 3     // dq/dk += RMSNorm-backward(inverse-RoPE(rows)), gain gradients += their row sums
+};
+// kEpiUnrotNorm's operands (the Qwen3 per-head q/k norm, layer.rs:195-206):
+// the pre-norm rows (the gradient rows' layout), their rstd, the gains
+// ([head_dim] each, accumulated into dqw/dkw), and scratch for the per-wave
+// gain-gradient partial sums of attn_bwd_norm_part_floats floats.
+struct BwdNorm {
+    const float* q_x = nullptr;
+    const float* k_x = nullptr;
+    const float* q_rstd = nullptr;
+    const float* k_rstd = nullptr;
+    const float* qw = nullptr;
+    const float* kw = nullptr;
+    float* dqw = nullptr;
+    float* dkw = nullptr;
+    float* part = nullptr;
+    size_t part_floats = 0;
 };
 struct BwdEpilogue {
     int mode = kEpiAdd;
+    // The dK rows' mode: -1 for `mode`; with kEpiUnrotNorm also
+    // kEpiUnrotStore (the dK/dV kernel stores the unrotated rows into dk, and
+    // their norm backward is left to the caller) -- the only choice where the
+    // dK/dV kernel has no norm epilogue (attn_bwd_norm_dk_epilogue).
+    int mode_k = -1;
     const float* cos = nullptr;
     const float* sin = nullptr;
     int pos0 = 0;
+    BwdNorm norm;
 };
 // True when launch_attn_bwd takes the fast bf16 kernels for these operands,
 // the only ones that honour a BwdEpilogue other than kEpiAdd.
 bool attn_bwd_epilogue_applies(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k,
                                const void* v, const float* dq, const float* dk, const float* dv, const Tuning& tu);
+// Whether the fast dK/dV kernel for d has the norm epilogue: the
+// two-waves-per-SIMD kernel does; the one-wave-per-SIMD kernel (head_dim
+// 128), whose registers are all taken by its step loop, does not.
+bool attn_bwd_norm_dk_epilogue(const Dims& d, const Tuning& tu);
+// Scratch floats a kEpiUnrotNorm backward needs for its gain-gradient
+// partials (one head_dim row per wave that writes dQ rows, or dK rows with
+// the norm epilogue), for either dQ kernel.
+size_t attn_bwd_norm_part_floats(const Dims& d, const Tuning& tu);
+// The fixed-order reduction of the partials (prologue.hip): dqw[i] += the sum
+// over rows [0, nq) of part[.][i], dkw[i] over rows [nq, nq + nk).
+hipError_t launch_norm_gain_reduce(float* part, int nq, int nk, int hd, float* dqw, float* dkw, hipStream_t st);
 // With f32 inputs the same scratch (when large enough) holds the per-head
 // dK/dV contributions of the fp32 fast path (attn_f32.hip), which
 // attn_bwd_ds_bytes reports for kF32.
 // A non-default `epi` needs attn_bwd_epilogue_applies and 16-byte aligned
-// cos/sin tables (hipErrorInvalidValue otherwise).  `delta` is scratch of 2 * batch * n_heads * seq floats: the
+// cos/sin tables; kEpiUnrotNorm also 16-byte aligned pre-norm rows and gains
+// and part_floats >= attn_bwd_norm_part_floats (hipErrorInvalidValue
+// otherwise).  `delta` is scratch of 2 * batch * n_heads * seq floats: the
 // delta rows, then (head_dim 128, bf16) the lse * log2(e) rows.
 hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void* q, const void* k, const void* v,
                            const float* o, const float* lse, float* delta, float* dq, float* dk, float* dv,
@@ -148,10 +187,11 @@ hipError_t launch_prologue_fwd(Dtype dt, const Dims& d, const Prologue& pr, cons
 size_t prologue_bwd_scratch_floats(const Dims& d);
 // With `unrotated`, dq/dk already hold the inverse-RoPE'd gradients (a
 // kEpiUnrotStore backward) and only the norm backward runs (pr.qw/kw set).
+// With `k_only`, only the k rows (the q arguments are not used).
 hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* dq, const float* dk,
                                const float* q_pre, const float* k_pre, const float* q_rstd, const float* k_rstd,
                                float* dq_pre, float* dk_pre, float* dqw, float* dkw, float* partial, hipStream_t st,
-                               KernelTimer* timer = nullptr, bool unrotated = false);
+                               KernelTimer* timer = nullptr, bool unrotated = false, bool k_only = false);
 
 // Elementwise helpers.
 hipError_t launch_f32_to_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t st);

@@ -526,6 +526,7 @@ __global__ __launch_bounds__(256) void prologue_bwd_dw_reduce_kernel(const ProBw
     const int i = blockIdx.x % p.hd;
     const bool isq = blockIdx.x < p.hd;
     const int n = isq ? p.n_chunks_q : p.n_chunks_k;
+    if (n == 0) return;  // no rows of this side in the launch: its gradient is left as it is
     const long base = isq ? 0 : p.n_chunks_q;
     float acc = 0.0f;
     for (int c = tid; c < n; c += 256) acc += p.partial[(base + c) * p.hd + i];
@@ -632,7 +633,7 @@ size_t prologue_bwd_scratch_floats(const Dims& d) {
 hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* dq, const float* dk,
                                const float* q_pre, const float* k_pre, const float* q_rstd, const float* k_rstd,
                                float* dq_pre, float* dk_pre, float* dqw, float* dkw, float* partial, hipStream_t st,
-                               KernelTimer* timer, bool unrotated) {
+                               KernelTimer* timer, bool unrotated, bool k_only) {
     ProBwdParams p{};
     p.unrot = unrotated ? 0 : 1;
     p.dq = dq;
@@ -656,7 +657,7 @@ hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* d
     p.nh = d.nh;
     p.nkv = d.nkv;
     p.hd = d.hd;
-    p.rows_q = (long)d.batch * d.seq * d.nh;
+    p.rows_q = k_only ? 0 : (long)d.batch * d.seq * d.nh;
     p.rows_k = (long)d.batch * d.seq * d.nkv;
     p.chunk_rows = dw_chunk_rows(d.hd);
     p.n_chunks_q = (int)((p.rows_q + p.chunk_rows - 1) / p.chunk_rows);
@@ -699,6 +700,19 @@ hipError_t launch_prologue_bwd(const Dims& d, const Prologue& pr, const float* d
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(prologue_bwd_dw_reduce_kernel, dim3(2 * d.hd), dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_norm_gain_reduce(float* part, int nq, int nk, int hd, float* dqw, float* dkw, hipStream_t st) {
+    if (hd <= 0) return hipSuccess;
+    ProBwdParams p{};
+    p.partial = part;
+    p.n_chunks_q = nq;
+    p.n_chunks_k = nk;
+    p.hd = hd;
+    p.dqw = dqw;
+    p.dkw = dkw;
+    hipLaunchKernelGGL(prologue_bwd_dw_reduce_kernel, dim3(2 * hd), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 

@@ -230,18 +230,60 @@ EPILOGUE_SHAPES = {
 }
 
 
-@pytest.mark.parametrize("name", sorted(EPILOGUE_SHAPES) + ["rope128-offset-tables", "qknorm64-offset-tables"])
-def test_fused_bwd_epilogue_matches_separate_passes(env, name):
+class _DsLimit:
+    def __init__(self, ctx, nbytes):
+        self.ctx, self.nbytes = ctx, nbytes
+
+    def __enter__(self):
+        self.old = self.ctx.ds_limit
+        self.ctx.ds_limit = self.nbytes
+
+    def __exit__(self, *a):
+        self.ctx.ds_limit = self.old
+
+
+# The Qwen3 shapes again through each variant of the fused backward: the norm
+# backward in the epilogues (default) with the stored-dS dQ kernel, with the
+# recompute dQ kernel (no dS scratch), with the two-waves-per-SIMD dK/dV
+# kernel; and the unrotated rows stored for a separate norm pass
+# (CFATTN_NORM_EPILOGUE=0).
+NORM_VARIANTS = ["qknorm-nods", "qknorm-ws", "qknorm-sep", "qknorm64-sep", "qknorm-ragged", "qknorm-offset-x"]
+EPILOGUE_SHAPES["qknorm-ragged"] = (3, 161, 8, 2, 128, 1e6, None, True, 4)
+
+
+@pytest.mark.parametrize("name", sorted(EPILOGUE_SHAPES) + ["rope128-offset-tables", "qknorm64-offset-tables"] +
+                         NORM_VARIANTS)
+def test_fused_bwd_epilogue_matches_separate_passes(env, name, monkeypatch):
     """In bf16 mode cfattn_fused_bwd folds the inverse RoPE into the dQ and
-    dK kernels' epilogues (adding into dq_pre/dk_pre, or with the norm storing
-    the unrotated rows for the norm-only pass).  It must give the same bits
-    as the attention backward into zeroed dq/dk followed by the separate
-    prologue backward, also on top of nonzero dq_pre/dk_pre.  With cos/sin
-    tables 4 bytes off a 16-byte boundary (the epilogue reads them 16 bytes
-    at a time) the fused call takes the separate passes itself."""
+    dK kernels' epilogues (adding into dq_pre/dk_pre) and, with the Qwen3
+    norm, the norm backward too (or, with CFATTN_NORM_EPILOGUE=0, stores the
+    unrotated rows for a norm-only pass).  dq_pre, dk_pre and dv must be the
+    same bits as the attention backward into zeroed dq/dk followed by the
+    separate prologue backward, also on top of nonzero dq_pre/dk_pre.  The
+    norm gains' gradients are the same sums over every (token, head) row in
+    another fixed order when the epilogues form them (their own partial sums
+    per wave): within |a-r|/(1+|r|) <= 1e-5 of the separate pass's, and the
+    same bits with the norm-only pass.  With cos/sin tables 4 bytes off a
+    16-byte boundary (the epilogue reads them 16 bytes at a time) the fused
+    call takes the separate passes itself; so it does with q_pre/k_pre rows
+    off a 16-byte boundary."""
     offset_tables = name.endswith("-offset-tables")
-    name = name.replace("-offset-tables", "")
+    offset_x = name.endswith("-offset-x")
+    name = name.replace("-offset-tables", "").replace("-offset-x", "")
+    variant = None
+    for suffix in ("-nods", "-ws", "-sep"):
+        if name.endswith(suffix):
+            variant, name = suffix[1:], name[: -len(suffix)]
+    if variant == "ws":
+        monkeypatch.setenv("CFATTN_DKDV_KERNEL", "ws")
+    if variant == "sep":
+        monkeypatch.setenv("CFATTN_NORM_EPILOGUE", "0")
     torch, cf, D, ctx = env
+    with _DsLimit(ctx, 0 if variant == "nods" else ctx.ds_limit):
+        _epilogue_case(torch, cf, D, ctx, name, offset_tables, offset_x, norm_in_epilogue=variant != "sep")
+
+
+def _epilogue_case(torch, cf, D, ctx, name, offset_tables, offset_x, norm_in_epilogue):
     B, S, Hq, Hk, Dh, theta, sc, qkn, pos0 = EPILOGUE_SHAPES[name]
     max_pos = S + pos0
     rope = cf.RopeCache(Dh, max_pos, theta, cf.Llama3Scaling(*sc) if sc else None)
@@ -260,6 +302,13 @@ def test_fused_bwd_epilogue_matches_separate_passes(env, name):
     torch.manual_seed(31)
     q_pre = torch.randn(B, S, Hq, Dh, device="cuda")
     k_pre = torch.randn(B, S, Hk, Dh, device="cuda")
+    if offset_x:
+        # Rows one float off a 16-byte boundary: the forward and the separate
+        # passes take any alignment, the norm epilogue does not.
+        bq = torch.zeros(q_pre.numel() + 1, device="cuda")
+        bq[1:] = q_pre.reshape(-1)
+        q_pre = bq[1:].view(B, S, Hq, Dh)
+        assert q_pre.data_ptr() % 16 == 4
     vd = torch.randn(B, S, Hk, Dh, device="cuda").to(torch.bfloat16)
     gd = torch.randn(B, S, Hq, Dh, device="cuda").to(torch.bfloat16)
     init_q = torch.randn(B, S, Hq, Dh, device="cuda")
@@ -272,12 +321,19 @@ def test_fused_bwd_epilogue_matches_separate_passes(env, name):
     torch.cuda.synchronize()
     got = {"dq_pre": fz[0], "dk_pre": fz[1], "dv": fz[2]}
     want = {"dq_pre": sp[0], "dk_pre": sp[1], "dv": dv}
-    if qkn:
-        got.update(dq_norm=fz[3], dk_norm=fz[4])
-        want.update(dq_norm=sp[2], dk_norm=sp[3])
     for nm in got:
         a, r = got[nm].cpu().numpy(), want[nm].cpu().numpy()
         assert np.array_equal(a, r), f"{name} {nm}: max diff {np.abs(a - r).max():.3e}"
+    if qkn:
+        for i, j, nm in ((3, 2, "dq_norm"), (4, 3, "dk_norm")):
+            a, r = fz[i].cpu().numpy(), sp[j].cpu().numpy()
+            if norm_in_epilogue and not (offset_tables or offset_x):
+                e = float(np.max(np.abs(a - r) / (1.0 + np.abs(r))))
+                print(f"{name} {nm}: |a-r|/(1+|r|) {e:.2e} against the separate pass", flush=True)
+                assert e <= 1e-5, f"{name} {nm}: {e:.3e}"
+                assert not np.array_equal(a, np.zeros_like(a))
+            else:
+                assert np.array_equal(a, r), f"{name} {nm}: max diff {np.abs(a - r).max():.3e}"
 
 
 def test_forward_and_backward_are_bitwise_repeatable(env):
