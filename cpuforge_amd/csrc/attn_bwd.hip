@@ -447,7 +447,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 // go straight from global memory into double-buffered blocked LDS tiles
 // (global_load_lds, issued one tile ahead by all the waves).  MFMA row i of
 // a 32-key block is key qperm(i) of the block (see BlkTile).
-template <int DP, int BN, int NW>
+// The NORM instance runs the kEpiUnrotNorm epilogue, the other one every
+// other mode.
+template <int DP, int BN, int NW, bool NORM>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq_bf16_kernel(
     const BwdParams p) {
     constexpr int CPR = DP / 8;
@@ -622,7 +624,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
         if (kt + 1 < n_kt) step(kt + 1, sK1, sV1, sK0, sV0);
     }
 
-    if (p.epi == kEpiUnrotNorm) {
+    if constexpr (NORM) {
         // Every lane takes part (the row's lane pair, the wave's gain sums).
         // LDS is free (the loop ends with a barrier): wave w stages its q_pre
         // rows in the K or V buffer w.
@@ -674,7 +676,9 @@ __device__ __forceinline__ void ring_barrier() {
     asm volatile("" ::: "memory");
 }
 
-template <int DP, int BN, int NW>
+// The NORM instance runs the kEpiUnrotNorm epilogue (the Qwen3 norm
+// backward, write_grad_row_norm), the other one every other mode.
+template <int DP, int BN, int NW, bool NORM>
 __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams p) {
     constexpr int CPR = DP / 8;
     using L = BlkTile<DP, BN>;
@@ -771,7 +775,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
     // tiles stream in, instead of as a dependent read at the end.
     float* const dq_row = p.dq + (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
     float4 dq_pre[NDB][4];
-    const bool pre = row_ok && grad_row_prefetch<NDB>(dq_pre, dq_row, hh, p);
+    const bool pre = row_ok && grad_row_prefetch<NDB, NORM>(dq_pre, dq_row, hh, p);
 
     // Step kt reads buffer kt % 3 and fills buffer (kt + 2) % 3, which the
     // barrier closing step kt - 1 has freed.
@@ -829,7 +833,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
         if (kt + 2 < n_kt) step(kt + 2, sK2, sS2, sK1, sS1);
     }
 
-    if (p.epi == kEpiUnrotNorm) {
+    if constexpr (NORM) {
         // Every lane takes part (the row's lane pair, the wave's gain sums).
         // The ring is free: every wave has passed the loop's last barrier.
         // Wave w stages its q_pre rows in 16 KiB of it: waves 0-5 in the dS
@@ -874,7 +878,9 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
 // With WDS the dS waves also store each 32x32 block of dS (bf16, the values
 // their dK product uses) for attn_bwd_dq_ds_kernel; the layout is given at
 // kDsBlock.
-template <int DP, int BM, bool WDS>
+// The NORM instance runs the kEpiUnrotNorm epilogue for the dK rows, the
+// other one every other mode.
+template <int DP, int BM, bool WDS, bool NORM>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dkdv_ws_kernel(
     const BwdParams p) {
     constexpr int NT = 512;
@@ -1245,15 +1251,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             if (s + 1 < n_steps) step(s + 1, sQ1, sO1, sQ0, sO0);
         }
 
-        if (p.epi == kEpiUnrotNorm) {
+        if constexpr (NORM) {
             // Both roles: after this barrier no wave reads the Q/dO tiles,
             // whose buffers the dS waves' epilogue then reuses.
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
         }
-        if constexpr (!PW) {
-            if (p.epi == kEpiUnrotNorm) {
+        if constexpr (!PW && NORM) {
+            {
                 // Every lane of the dS wave takes part (the row's lane pair,
                 // the wave's gain sums); slice s stages its k_pre rows in
                 // buffer s of the Q and dO tiles.
@@ -1509,12 +1515,21 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
             if (k64) {
                 launch_attn_bwd_dkdv_k64(p, use_ds, st);
             } else if (d.hd == 128) {
-                if (use_ds)
-                    hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64, true>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
+                const dim3 g(p.n_wg_kv), blk(512);
+                if (use_ds && mode_k == kEpiUnrotNorm)
+                    hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64, true, true>), g, blk, 0, st, p);
+                else if (use_ds)
+                    hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64, true, false>), g, blk, 0, st, p);
+                else if (mode_k == kEpiUnrotNorm)
+                    hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64, false, true>), g, blk, 0, st, p);
                 else
-                    hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64, false>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
+                    hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64, false, false>), g, blk, 0, st, p);
             } else {
-                hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<64, 128, false>), dim3(p.n_wg_kv), dim3(512), 0, st, p);
+                const dim3 g(p.n_wg_kv), blk(512);
+                if (mode_k == kEpiUnrotNorm)
+                    hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<64, 128, false, true>), g, blk, 0, st, p);
+                else
+                    hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<64, 128, false, false>), g, blk, 0, st, p);
             }
             e = hipGetLastError();
         }
@@ -1526,14 +1541,23 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
                 p.tpw = tpw_ds;
                 p.n_ttiles = n_ttiles_ds;
                 p.n_wg_q = (int)n_wg_ds;
-                hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<128, 64, kDqDsWaves>), dim3(p.n_wg_q),
-                                   dim3(64 * kDqDsWaves), 0, st, p);
-            } else if (d.hd == 128) {
-                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 64, kDqWaves>), dim3(p.n_wg_q), dim3(64 * kDqWaves),
-                                   0, st, p);
+                if (p.epi == kEpiUnrotNorm)
+                    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<128, 64, kDqDsWaves, true>), dim3(p.n_wg_q),
+                                       dim3(64 * kDqDsWaves), 0, st, p);
+                else
+                    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<128, 64, kDqDsWaves, false>), dim3(p.n_wg_q),
+                                       dim3(64 * kDqDsWaves), 0, st, p);
             } else {
-                hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, 128, kDqWaves>), dim3(p.n_wg_q), dim3(64 * kDqWaves),
-                                   0, st, p);
+                const dim3 g(p.n_wg_q), blk(64 * kDqWaves);
+                const bool norm = p.epi == kEpiUnrotNorm;
+                if (d.hd == 128 && norm)
+                    hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 64, kDqWaves, true>), g, blk, 0, st, p);
+                else if (d.hd == 128)
+                    hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 64, kDqWaves, false>), g, blk, 0, st, p);
+                else if (norm)
+                    hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, 128, kDqWaves, true>), g, blk, 0, st, p);
+                else
+                    hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<64, 128, kDqWaves, false>), g, blk, 0, st, p);
             }
             e = hipGetLastError();
         }

@@ -298,12 +298,12 @@ __device__ __forceinline__ void load_grad_row(float4 (&v)[NDB][4], const float* 
                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
-// The lane's part of a gradient row, read ahead for the += epilogue modes;
-// false (nothing read) for the others.
-template <int NDB>
+// The lane's part of a gradient row, read ahead for the += epilogue modes
+// (kEpiUnrotNorm too with NORM); false (nothing read) for the others.
+template <int NDB, bool NORM = false>
 __device__ __forceinline__ bool grad_row_prefetch(float4 (&pre)[NDB][4], const float* row, int hh,
                                                   const BwdParams& p) {
-    if (p.epi != kEpiAdd && p.epi != kEpiUnrotAdd && p.epi != kEpiUnrotNorm) return false;
+    if (p.epi != kEpiAdd && p.epi != kEpiUnrotAdd && !(NORM && p.epi == kEpiUnrotNorm)) return false;
     load_grad_row<NDB>(pre, row, hh, true);
     return true;
 }
