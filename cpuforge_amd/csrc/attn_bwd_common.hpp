@@ -57,12 +57,15 @@ __device__ __forceinline__ void add_row_block(float* row, const f32x16& acc, int
 // With PRE (the += modes), the row's current values come from `pre` instead
 // of memory: grad_row_prefetch read them earlier, so that the read is not a
 // dependent round trip at the end of the kernel.
+// `mode` is p.epi unless given (>= 0).
 template <int NDB, bool PRE = false>
 __device__ __forceinline__ void write_grad_row(float* row, const f32x16 (&acc)[NDB], int hh, int t,
-                                               const BwdParams& p, const float4 (*pre)[4] = nullptr) {
+                                               const BwdParams& p, const float4 (*pre)[4] = nullptr,
+                                               int mode = -1) {
 #pragma clang fp contract(off)
     constexpr int DP = NDB * 32, HALF = DP / 2;
-    if (p.epi == kEpiAdd) {
+    if (mode < 0) mode = p.epi;
+    if (mode == kEpiAdd) {
         if constexpr (PRE) {
 #pragma unroll
             for (int db = 0; db < NDB; db++)
@@ -83,13 +86,24 @@ __device__ __forceinline__ void write_grad_row(float* row, const f32x16 (&acc)[N
     }
     const float* cs = p.rope_cos + (long)(p.rope_pos0 + t) * HALF;
     const float* sn = p.rope_sin + (long)(p.rope_pos0 + t) * HALF;
+    // The row's cos/sin entries, read before the first store (a store may
+    // alias them as far as the compiler knows, which would hold each later
+    // read behind it).
+    float4 cs4[NDB / 2][4], sn4[NDB / 2][4];
+#pragma unroll
+    for (int db = 0; db < NDB / 2; db++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            cs4[db][rq] = *reinterpret_cast<const float4*>(cs + db * 32 + rq * 8 + hh * 4);
+            sn4[db][rq] = *reinterpret_cast<const float4*>(sn + db * 32 + rq * 8 + hh * 4);
+        }
 #pragma unroll
     for (int db = 0; db < NDB / 2; db++) {
 #pragma unroll
         for (int rq = 0; rq < 4; rq++) {
             const int d0 = db * 32 + rq * 8 + hh * 4;
-            const float4 c4 = *reinterpret_cast<const float4*>(cs + d0);
-            const float4 s4 = *reinterpret_cast<const float4*>(sn + d0);
+            const float4 c4 = cs4[db][rq];
+            const float4 s4 = sn4[db][rq];
             const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
             float lo[4], hi[4];
 #pragma unroll
@@ -101,7 +115,7 @@ __device__ __forceinline__ void write_grad_row(float* row, const f32x16 (&acc)[N
             }
             float4* r1 = reinterpret_cast<float4*>(row + d0);
             float4* r2 = reinterpret_cast<float4*>(row + d0 + HALF);
-            if (p.epi == kEpiUnrotAdd) {
+            if (mode == kEpiUnrotAdd) {
                 float4 a, b;
                 if constexpr (PRE) {
                     a = pre[db][rq];

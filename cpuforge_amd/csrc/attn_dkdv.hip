@@ -329,23 +329,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         acc_wait8(acc[0][0], acc[0][1], acc[1][0], acc[1][1], acc[2][0], acc[2][1], acc[3][0], acc[3][1]);
     };
     // dV rows are added; dK rows (scaled: dS was accumulated without the
-    // softmax scale) go through the epilogue mode.
+    // softmax scale) go through the epilogue mode.  The current values of
+    // the lane's rows (both key blocks) are read before any is written, so
+    // that the wave waits for one round of reads rather than one per block.
     auto store_rows = [&](float* dst, f32x16 (&acc)[NDB][NKB], bool dk_rows) {
         if (!pair_live) return;
+        const int mode = dk_rows ? p.epi : kEpiAdd;
+        float* row[NKB];
+        bool ok[NKB];
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
             const int kw = key0 + kb * 32 + l32;
-            if (kw >= p.seq) continue;
-            float* row = dst + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
-            if (dk_rows) {
-                f32x16 r[NDB];
+            ok[kb] = kw < p.seq;
+            row[kb] = dst + (long)b * p.kv_bs + (long)kw * kvrs + (long)g * DP;
+        }
+        float4 cur[NKB][NDB][4];
+        if (mode == kEpiAdd || mode == kEpiUnrotAdd) {
 #pragma unroll
-                for (int db = 0; db < NDB; db++) r[db] = acc[db][kb] * p.scale;
-                write_grad_row<NDB>(row, r, hh, kw, p);
-            } else {
+            for (int kb = 0; kb < NKB; kb++) load_grad_row<NDB>(cur[kb], row[kb], hh, ok[kb]);
+        }
 #pragma unroll
-                for (int db = 0; db < NDB; db++) add_row_block(row, acc[db][kb], db * 32, hh, DP, true);
-            }
+        for (int kb = 0; kb < NKB; kb++) {
+            if (!ok[kb]) continue;
+            const int kw = key0 + kb * 32 + l32;
+            f32x16 r[NDB];
+#pragma unroll
+            for (int db = 0; db < NDB; db++) r[db] = dk_rows ? acc[db][kb] * p.scale : acc[db][kb];
+            if (mode == kEpiAdd || mode == kEpiUnrotAdd)
+                write_grad_row<NDB, true>(row[kb], r, hh, kw, p, cur[kb], mode);
+            else
+                write_grad_row<NDB>(row[kb], r, hh, kw, p, nullptr, mode);
         }
     };
     // Per-row values (lse or delta) of MFMA rows 8*g4 + 4*hh + [0, 4) of
