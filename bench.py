@@ -206,6 +206,20 @@ def peak_probe(ctx, runs=3, iters=40000):
     return out
 
 
+def mfma_shape_probe(ctx, runs=3, iters=40000):
+    """The 16x16x32 bf16 MFMA loop (cfattn_probe_loop kind "mfma16") against
+    the 32x32x16 one on the same pseudo-random operands, alternating, median
+    TFLOP/s of each: which shape does more FLOPs under the board's power
+    limit."""
+    ctx.probe_mfma_peak(False, iters)  # warm-up
+    r32, r16 = [], []
+    for _ in range(runs):
+        r32.append(ctx.probe_mfma_peak(False, iters))
+        r16.append(ctx.probe_loop("mfma16", iters) / 1e12)
+    return {"mfma_32x32x16_random": round(sorted(r32)[runs // 2], 1),
+            "mfma_16x16x32_random": round(sorted(r16)[runs // 2], 1)}
+
+
 def fwd_distributions(a):
     """The C5 bf16 forward (attn_fwd_q64_kernel) on inputs whose scores move
     the running max, against N(0,1) inputs.  The kernel forms P against the
@@ -1038,13 +1052,16 @@ def main():
         import cpuforge_amd as cf
         ctx = cf.Context(0)
         pk = peak_probe(ctx, runs=5)
+        shapes = mfma_shape_probe(ctx, runs=5)
         ctx.close()
         print(json.dumps({"metric": "on-board bf16 MFMA ceiling (loop of v_mfma_f32_32x32x16_bf16, two waves per "
                                     "SIMD, every CU)", "value": pk["random"], "unit": "TFLOP/s", "n_gpus": 1,
                           "higher_is_better": True, "dtype": "bf16", "spec_peak": PEAK_TFLOPS["bf16"],
                           "frac_of_spec": round(pk["random"] / PEAK_TFLOPS["bf16"], 4), "zero_operands": pk["zeros"],
+                          "mfma_shapes": shapes,
                           "data": "pseudo-random bf16 operands in registers (median of 5 runs of ~20 ms after a "
-                                  "warm-up); zero_operands: the same loop on zeros"}), flush=True)
+                                  "warm-up); zero_operands: the same loop on zeros; mfma_shapes: the 32x32x16 and "
+                                  "16x16x32 loops alternating on the same operands"}), flush=True)
         return
 
     import torch

@@ -130,9 +130,10 @@ class Context:
 
     def probe_loop(self, kind: str, iters: int = 20000) -> float:
         """Rate of a loop of one instruction class on every SIMD
-        (cfattn_probe_loop): "lds" (16-byte LDS reads, bytes/s) or "valu"
-        (v_fma_f32, lane operations/s)."""
-        code = {"lds": 0, "valu": 1}[kind]
+        (cfattn_probe_loop): "lds" (16-byte LDS reads, bytes/s), "valu"
+        (v_fma_f32, lane operations/s) or "mfma16" (bf16 16x16x32 MFMAs on
+        pseudo-random operands, FLOP/s)."""
+        code = {"lds": 0, "valu": 1, "mfma16": 2}[kind]
         out = C.c_double()
         _lib.check(self._lib.cfattn_probe_loop(self.handle, code, int(iters), C.byref(out)), self.handle)
         return out.value

@@ -705,7 +705,7 @@ int cfattn_probe_loop(cfattn_ctx* c, int kind, int iters, double* rate) {
     std::lock_guard<std::mutex> lk(c->mu);
     c->err.clear();
     if (iters <= 0) return fail(c, CFATTN_ERR_ARG, "iters must be positive (got %d)", iters);
-    if (kind != cfattn::kProbeLds && kind != cfattn::kProbeValu)
+    if (kind != cfattn::kProbeLds && kind != cfattn::kProbeValu && kind != cfattn::kProbeMfma16)
         return fail(c, CFATTN_ERR_ARG, "unknown probe %d", kind);
     DeviceGuard dg(c->device);
     CF_HIP(c, cfattn::probe_loop(c->stream, kind, iters, rate), "loop probe");

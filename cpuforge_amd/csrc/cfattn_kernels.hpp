@@ -216,9 +216,10 @@ void* noalloc_scratch(int device);
 // returns its TFLOP/s.
 hipError_t probe_mfma_bf16(hipStream_t st, int zeros, int iters, double* tflops);
 // LDS-read (kProbeLds: bytes/s) or v_fma_f32 (kProbeValu: lane operations/s)
-// loop of `iters` iterations, four waves per SIMD on every CU; waits for the
-// run and returns its rate.
-enum ProbeKind { kProbeLds = 0, kProbeValu = 1 };
+// loop of `iters` iterations, four waves per SIMD on every CU, or a bf16
+// 16x16x32 MFMA loop (kProbeMfma16: FLOP/s, two waves per SIMD); waits for
+// the run and returns its rate.
+enum ProbeKind { kProbeLds = 0, kProbeValu = 1, kProbeMfma16 = 2 };
 hipError_t probe_loop(hipStream_t st, int kind, int iters, double* rate);
 
 }  // namespace cfattn

@@ -17,6 +17,8 @@ namespace cfattn {
 
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 // A 32-bit integer hash (xorshift-multiply, the "lowbias32" constants of
 // Chris Wellons' public hash survey): consecutive inputs give unrelated
 // outputs, so every lane and operand gets independent bits.
@@ -71,6 +73,47 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(int iters, int zeros, f
         for (int c = 0; c < 4; c++)
 #pragma unroll
             for (int r = 0; r < 16; r++) s += acc[c][r];
+        sink[wave * 64u + lane] = s;
+    }
+}
+
+// The same loop with v_mfma_f32_16x16x32_bf16 (half the FLOPs per
+// instruction, a quarter of the accumulator per product): eight independent
+// accumulator chains, 32 MFMAs (the 32x32x16 loop's FLOPs) per iteration, on
+// pseudo-random operands.  Whether the other shape draws less energy per FLOP
+// (and so runs faster under the power limit) is what it measures.
+__global__ __launch_bounds__(256) void mfma16_probe_kernel(int iters, float* sink) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = blockIdx.x * 4u + (threadIdx.x >> 6);
+    bf16x8 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t wa[4], wb[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t seed = ((wave * 64u + lane) * 4u + (uint32_t)i) * 8u + (uint32_t)j;
+            wa[j] = probe_pair(probe_hash(seed));
+            wb[j] = probe_pair(probe_hash(seed + 4u));
+        }
+        a[i] = __builtin_bit_cast(bf16x8, make_uint4(wa[0], wa[1], wa[2], wa[3]));
+        b[i] = __builtin_bit_cast(bf16x8, make_uint4(wb[0], wb[1], wb[2], wb[3]));
+    }
+    f32x4 acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int c = 0; c < 8; c++)
+                acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[(j + c) & 3], b[(j + 2 * c + (c >> 1)) & 3], acc[c],
+                                                                  0, 0, 0);
+    }
+    // Keeps the loop live; callers pass no sink.
+    if (sink) {
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) s += acc[c][0] + acc[c][1] + acc[c][2] + acc[c][3];
         sink[wave * 64u + lane] = s;
     }
 }
@@ -170,8 +213,10 @@ hipError_t probe_loop(hipStream_t st, int kind, int iters, double* rate) {
     if (e == hipSuccess) {
         if (kind == kProbeLds)
             hipLaunchKernelGGL(lds_probe_kernel, dim3(cus), dim3(1024), 0, st, iters, (float*)nullptr);
-        else
+        else if (kind == kProbeValu)
             hipLaunchKernelGGL(valu_probe_kernel, dim3(cus), dim3(1024), 0, st, iters, (float*)nullptr);
+        else  // kProbeMfma16: two waves per SIMD, as the 32x32x16 probe
+            hipLaunchKernelGGL(mfma16_probe_kernel, dim3(2 * cus), dim3(256), 0, st, iters, (float*)nullptr);
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipEventRecord(e1, st);
@@ -180,9 +225,14 @@ hipError_t probe_loop(hipStream_t st, int kind, int iters, double* rate) {
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     if (e != hipSuccess) return e;
-    // Bytes read from LDS, or lane operations (one per lane per v_fma_f32).
-    const double per_iter = kind == kProbeLds ? 8.0 * 16.0 : 16.0;
-    const double units = (double)cus * 1024.0 * (double)iters * per_iter;
+    // Bytes read from LDS, lane operations (one per lane per v_fma_f32), or
+    // FLOPs (32 MFMAs of 16 x 16 x 32 x 2 per wave and iteration, 8 waves
+    // per CU).
+    double units;
+    if (kind == kProbeMfma16)
+        units = (double)cus * 8.0 * (double)iters * 32.0 * (16.0 * 16.0 * 32.0 * 2.0);
+    else
+        units = (double)cus * 1024.0 * (double)iters * (kind == kProbeLds ? 8.0 * 16.0 : 16.0);
     *rate = ms > 0.0f ? units / ((double)ms * 1e-3) : 0.0;
     return hipSuccess;
 }

@@ -244,9 +244,11 @@ int cfattn_fwd_stats_read(cfattn_ctx* ctx, long long* settles);
 int cfattn_probe_mfma_peak(cfattn_ctx* ctx, int zeros, int iters, double* tflops);
 /* No reference counterpart: loops of one instruction class for the board
  * power each draws (read beside it with amd-smi).  kind 0: 16-byte LDS reads
- * (rate in bytes/s); kind 1: v_fma_f32 (rate in lane operations/s).  Four
- * waves per SIMD on every CU, `iters` loop iterations, on the context's
- * stream; waits for the run. */
+ * (rate in bytes/s); kind 1: v_fma_f32 (rate in lane operations/s), both four
+ * waves per SIMD on every CU; kind 2: v_mfma_f32_16x16x32_bf16 on
+ * pseudo-random operands (rate in FLOP/s, two waves per SIMD: the other MFMA
+ * shape against cfattn_probe_mfma_peak's).  `iters` loop iterations, on the
+ * context's stream; waits for the run. */
 int cfattn_probe_loop(cfattn_ctx* ctx, int kind, int iters, double* rate);
 /* Name of kernel id `kernel` ("attn_fwd", "attn_bwd_dkdv", ...), or NULL. */
 const char* cfattn_kernel_name(int kernel);
