@@ -1573,7 +1573,7 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        return launch_attn_bwd_f32(d, p, ds, st, tu.timer);
+        return launch_attn_bwd_f32(d, p, ds, tu.f32_persistent != 0, st, tu.timer);
     }
     const int q_waves = p.hpw * p.tpw;
     const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;

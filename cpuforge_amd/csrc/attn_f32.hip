@@ -54,6 +54,9 @@ __device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
 // row0 .. row0 + 31 (clamped to last_row, so padding rows repeat finite
 // data) of a DP-wide f32 tensor with row stride `rs` floats.  A 1 KiB block
 // is 64 chunk slots; slot p holds chunk (p % CPR) ^ swz(row) of row p / CPR.
+// The loads are issued from inline assembly, so the compiler's wait-count
+// tracking does not see them: the kernels wait for them with exact counts
+// (f32_tile_wait), which lets a tile stay in flight across a barrier.
 template <int DP, int NW>
 __device__ __forceinline__ void f32_tile_dma(const float* __restrict__ g, long rs, int row0, int last_row,
                                              float* __restrict__ tile, int wv, int lane) {
@@ -68,8 +71,46 @@ __device__ __forceinline__ void f32_tile_dma(const float* __restrict__ g, long r
         const int r = slot / CPR;
         const int c = (slot % CPR) ^ f32_swz(r & 15);
         const long row = min(row0 + r, last_row);
-        __builtin_amdgcn_global_load_lds(g + row * rs + c * 4, tile + blk * 256, 16, 0, 0);
+        lds_load16_asm(g + row * rs + c * 4, tile + blk * 256);
     }
+}
+
+// End of a ring step: this wave's loads for the next step have landed (with
+// `newer`, the EXTRA + two tiles' loads issued after them may still be in
+// flight: loads complete in issue order) and its LDS reads of this step are
+// done; then a barrier without __syncthreads' workgroup fence, whose
+// vmcnt(0) would also wait for the newer loads.  Only the ring's
+// direct-to-LDS loads are outstanding where it is called.
+template <int DP, int NW, int EXTRA = 0>
+__device__ __forceinline__ void f32_step_end(bool newer) {
+    constexpr int kNewer = 2 * (32 * DP / 256) / NW + EXTRA;
+    if (newer)
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kNewer) : "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Work unit `it` of a persistent workgroup of the forward or dQ grid (no key
+// split): the XCD of workgroup w (w % 8; the dispatcher deals workgroups
+// round robin) takes a contiguous run of the n_groups (sequence, KV head,
+// head subset) groups, so that its L2 holds few KV heads, and its W
+// workgroups walk the run's query tiles longest first in a snake (positions
+// l, 2W - 1 - l, 2W + l, ...), which gives every workgroup nearly the same
+// number of key tiles.  (A grid of one workgroup per unit leaves CUs idle
+// while units remain: units of very different lengths stall the in-order
+// dispatch.)  False past the run.
+__device__ __forceinline__ bool f32_persistent_item(int it, int n_groups, int n_ttiles, int W, int& tile, int& grp) {
+    const int xq = blockIdx.x % 8, xl = blockIdx.x / 8;
+    const int q = n_groups / 8, r = n_groups % 8;
+    const int g0 = xq < r ? xq * (q + 1) : r * (q + 1) + (xq - r) * q;
+    const int gn = q + (xq < r ? 1 : 0);
+    const int pos = (it >> 1) * 2 * W + ((it & 1) ? 2 * W - 1 - xl : xl);
+    if (gn == 0 || pos >= gn * n_ttiles) return false;
+    tile = n_ttiles - 1 - pos / gn;
+    grp = g0 + pos % gn;
+    return true;
 }
 
 // Query tile, key split and split count of work unit u of one (sequence, KV
@@ -94,25 +135,23 @@ __device__ __forceinline__ F32Unit f32_unit(int u, int n_ttiles, int tt, int seq
 // ------------------------------------------------------------------ forward
 // A wave owns 32 queries of one head; a workgroup of four waves covers hpw
 // heads of one GQA group x tpw query blocks and shares 32-key K/V tiles.
+// One work unit of the forward: query tile un.tile (key run un.split of
+// un.ns) of group `rest` = (sequence * nkv + KV head) * n_sub + head subset.
+// Every wave passes the same barriers; after the last one no wave reads the
+// K/V buffers, so the next unit of a persistent workgroup may load into them.
 template <int DP>
-__global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
+__device__ __forceinline__ void fwd_f32_unit(const FwdParams& p, const F32Unit un, int rest, float* sK0, float* sK1,
+                                             float* sK2, float* sV0, float* sV1, float* sV2) {
     constexpr int NW = 4, BN = 32, HALF = DP / 2, NDB = DP / 32;
     constexpr float kLazy = 8.0f;
-    __shared__ __attribute__((aligned(16))) float sK0[BN * DP];
-    __shared__ __attribute__((aligned(16))) float sK1[BN * DP];
-    __shared__ __attribute__((aligned(16))) float sV0[BN * DP];
-    __shared__ __attribute__((aligned(16))) float sV1[BN * DP];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int l32 = lane & 31, hh = lane >> 5;
     const int wv = wave_uniform(wave);
 
-    const int id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
     const int TT = 32 * p.tpw;
-    const F32Unit un = f32_unit(id % p.units, p.n_ttiles, TT, p.seq, p.ksplit);
-    const int tile = un.tile;  // longest tiles first
-    int rest = id / p.units;
+    const int tile = un.tile;
     const int sub = rest % p.n_sub;
     rest /= p.n_sub;
     const int g = rest % p.nkv;
@@ -131,6 +170,12 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
     const float* kg = static_cast<const float*>(p.k) + (long)b * p.kv_bs + (long)g * DP;
     const float* vg = static_cast<const float*>(p.v) + (long)b * p.kv_bs + (long)g * DP;
 
+    auto dma = [&](int kt, float* Kd, float* Vd) {
+        f32_tile_dma<DP, NW>(kg, kvrs, kt * BN, p.seq - 1, Kd, wv, lane);
+        f32_tile_dma<DP, NW>(vg, kvrs, kt * BN, p.seq - 1, Vd, wv, lane);
+    };
+    dma(kt0, sK0, sV0);
+
     // Q^T operand: query tq, head dims hh*HALF + kd.
     float qf[HALF];
     {
@@ -145,22 +190,25 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
             qf[4 * i + 3] = v.w;
         }
     }
+    // The Q rows and tile kt0 have landed; a wait the compiler sees, so that
+    // it puts none for the Q rows inside the loop (where the asm-issued tile
+    // loads are in flight).
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
     f32x16 oacc[NDB];
 #pragma unroll
     for (int i = 0; i < NDB; i++) oacc[i] = zero16();
     float m2 = -INFINITY, lsum = 0.0f;
 
-    auto dma = [&](int kt, float* Kd, float* Vd) {
-        f32_tile_dma<DP, NW>(kg, kvrs, kt * BN, p.seq - 1, Kd, wv, lane);
-        f32_tile_dma<DP, NW>(vg, kvrs, kt * BN, p.seq - 1, Vd, wv, lane);
-    };
-
+    // Three K/V buffers: the tile two steps ahead is loaded during a step,
+    // into the buffer the previous step read.
     auto step = [&](int kt, const float* Ks, const float* Vs, float* Kn, float* Vn) {
-        const bool more = kt + 1 < n_kt;
+        const bool ahead = kt + 2 < n_kt;
         const int k0 = kt * BN;
         if (wave_active && k0 <= wave_last) {
             // S^T: rows = keys k0 + [0, 32), columns = this wave's queries.
+            // The loads two tiles ahead issue behind the first MFMAs, whose
+            // shadow covers their address arithmetic.
             f32x16 sc = zero16();
 #pragma unroll
             for (int c = 0; c < HALF / 4; c++) {
@@ -169,8 +217,8 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
                 sc = mfma_f32(a.y, qf[4 * c + 1], sc);
                 sc = mfma_f32(a.z, qf[4 * c + 2], sc);
                 sc = mfma_f32(a.w, qf[4 * c + 3], sc);
+                if (c == 0 && ahead) dma(kt + 2, Kn, Vn);
             }
-            if (more) dma(kt + 1, Kn, Vn);
             float mx = -INFINITY;
             const bool masked = k0 + 31 > t_wave;
 #pragma unroll
@@ -201,19 +249,18 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
 #pragma unroll
                 for (int j = 0; j < 16; j++)
                     oacc[db] = mfma_f32(Vs[f32_at<DP>(acc_row(j, hh), db * 32 + l32)], pr[j], oacc[db]);
-        } else if (more) {
-            dma(kt + 1, Kn, Vn);
+        } else if (ahead) {
+            dma(kt + 2, Kn, Vn);
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        f32_step_end<DP, NW>(ahead);  // tile kt + 1 is in LDS
     };
 
-    dma(kt0, sK0, sV0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    for (int kt = kt0; kt < n_kt; kt += 2) {
-        step(kt, sK0, sV0, sK1, sV1);
+    if (kt0 + 1 < n_kt) dma(kt0 + 1, sK1, sV1);
+    f32_step_end<DP, NW>(kt0 + 1 < n_kt);
+    for (int kt = kt0; kt < n_kt; kt += 3) {
+        step(kt, sK0, sV0, sK2, sV2);
         if (kt + 1 < n_kt) step(kt + 1, sK1, sV1, sK0, sV0);
+        if (kt + 2 < n_kt) step(kt + 2, sK2, sV2, sK1, sV1);
     }
 
     if (!wave_active) return;
@@ -246,31 +293,44 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
     if (hh == 0) p.lse[((long)b * p.nh + head) * p.seq + tq] = (m2 + __log2f(ltot)) * kLn2;
 }
 
+template <int DP>
+__global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
+    constexpr int BN = 32;
+    __shared__ __attribute__((aligned(16))) float sK0[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sK1[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sK2[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sV0[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sV1[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sV2[BN * DP];
+    if (p.xcd_wgs > 0) {
+        const int n_groups = p.n_items / p.n_ttiles;
+        int tile, grp;
+        for (int it = 0; f32_persistent_item(it, n_groups, p.n_ttiles, p.xcd_wgs, tile, grp); it++)
+            fwd_f32_unit<DP>(p, F32Unit{tile, 0, 1}, grp, sK0, sK1, sK2, sV0, sV1, sV2);
+        return;
+    }
+    const int id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
+    const F32Unit un = f32_unit(id % p.units, p.n_ttiles, 32 * p.tpw, p.seq, p.ksplit);  // longest tiles first
+    fwd_f32_unit<DP>(p, un, id / p.units, sK0, sK1, sK2, sV0, sV1, sV2);
+}
+
 // -------------------------------------------------------------------- dQ
 // The forward's decomposition; per 32-key tile: S^T = K Q^T, dP^T = V dO^T,
 // dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T.  The softmax scale is applied
 // once to dQ.
-// Two waves per SIMD at head_dim 64 (the registers fit; measured 7% faster
-// at B8 S2048 9/3 heads), one at 128.
+// One work unit of the dQ grid, as fwd_f32_unit.
 template <int DP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 2 : 1, DP == 64 ? 2 : 1))) void
-attn_bwd_dq_f32_kernel(const BwdParams p) {
+__device__ __forceinline__ void dq_f32_unit(const BwdParams& p, const F32Unit un, int rest, float* sK0, float* sK1,
+                                            float* sK2, float* sV0, float* sV1, float* sV2) {
     constexpr int NW = 4, BN = 32, HALF = DP / 2, NDB = DP / 32;
-    __shared__ __attribute__((aligned(16))) float sK0[BN * DP];
-    __shared__ __attribute__((aligned(16))) float sK1[BN * DP];
-    __shared__ __attribute__((aligned(16))) float sV0[BN * DP];
-    __shared__ __attribute__((aligned(16))) float sV1[BN * DP];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int l32 = lane & 31, hh = lane >> 5;
     const int wv = wave_uniform(wave);
 
-    const int id = xcd_remap(blockIdx.x, p.n_wg_q, p.xcd);
     const int TT = 32 * p.tpw;
-    const F32Unit un = f32_unit(id % p.units_q, p.n_ttiles, TT, p.seq, p.ksplit);
     const int tile = un.tile;
-    int rest = id / p.units_q;
     const int sub = rest % p.n_sub;
     rest /= p.n_sub;
     const int g = rest % p.nkv;
@@ -290,6 +350,12 @@ attn_bwd_dq_f32_kernel(const BwdParams p) {
     const float* vg = static_cast<const float*>(p.v) + (long)b * p.kv_bs + (long)g * DP;
     const long qoff = (long)b * p.q_bs + (long)min(tq, p.seq - 1) * qrs + (long)head * DP + hh * HALF;
 
+    auto dma = [&](int kt, float* Kd, float* Vd) {
+        f32_tile_dma<DP, NW>(kg, kvrs, kt * BN, p.seq - 1, Kd, wv, lane);
+        f32_tile_dma<DP, NW>(vg, kvrs, kt * BN, p.seq - 1, Vd, wv, lane);
+    };
+    dma(kt0, sK0, sV0);
+
     float qf[HALF], of[HALF];
 #pragma unroll
     for (int i = 0; i < HALF / 4; i++) {
@@ -301,17 +367,16 @@ attn_bwd_dq_f32_kernel(const BwdParams p) {
     const long lrow = ((long)b * p.nh + head) * p.seq + min(tq, p.seq - 1);
     const float lq = p.lse[lrow] * kLog2e;
     const float dlq = p.delta[lrow];
+    // The rows above and tile kt0 have landed; a wait the compiler sees (see
+    // the forward).
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
     f32x16 acc[NDB];
 #pragma unroll
     for (int i = 0; i < NDB; i++) acc[i] = zero16();
 
-    auto dma = [&](int kt, float* Kd, float* Vd) {
-        f32_tile_dma<DP, NW>(kg, kvrs, kt * BN, p.seq - 1, Kd, wv, lane);
-        f32_tile_dma<DP, NW>(vg, kvrs, kt * BN, p.seq - 1, Vd, wv, lane);
-    };
     auto step = [&](int kt, const float* Ks, const float* Vs, float* Kn, float* Vn) {
-        const bool more = kt + 1 < n_kt;
+        const bool ahead = kt + 2 < n_kt;
         const int k0 = kt * BN;
         if (wave_active && k0 <= wave_last) {
             f32x16 sc = zero16(), dp = zero16();
@@ -327,8 +392,8 @@ attn_bwd_dq_f32_kernel(const BwdParams p) {
                 dp = mfma_f32(v.z, of[4 * c + 2], dp);
                 sc = mfma_f32(a.w, qf[4 * c + 3], sc);
                 dp = mfma_f32(v.w, of[4 * c + 3], dp);
+                if (c == 0 && ahead) dma(kt + 2, Kn, Vn);  // behind the first MFMAs, as the forward
             }
-            if (more) dma(kt + 1, Kn, Vn);
             const bool masked = k0 + 31 > t_wave;
             float ds[16];
 #pragma unroll
@@ -342,19 +407,18 @@ attn_bwd_dq_f32_kernel(const BwdParams p) {
 #pragma unroll
                 for (int j = 0; j < 16; j++)
                     acc[db] = mfma_f32(Ks[f32_at<DP>(acc_row(j, hh), db * 32 + l32)], ds[j], acc[db]);
-        } else if (more) {
-            dma(kt + 1, Kn, Vn);
+        } else if (ahead) {
+            dma(kt + 2, Kn, Vn);
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        f32_step_end<DP, NW>(ahead);
     };
 
-    dma(kt0, sK0, sV0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    for (int kt = kt0; kt < n_kt; kt += 2) {
-        step(kt, sK0, sV0, sK1, sV1);
+    if (kt0 + 1 < n_kt) dma(kt0 + 1, sK1, sV1);
+    f32_step_end<DP, NW>(kt0 + 1 < n_kt);
+    for (int kt = kt0; kt < n_kt; kt += 3) {
+        step(kt, sK0, sV0, sK2, sV2);
         if (kt + 1 < n_kt) step(kt + 1, sK1, sV1, sK0, sV0);
+        if (kt + 2 < n_kt) step(kt + 2, sK2, sV2, sK1, sV1);
     }
     if (!wave_active || tq >= p.seq) return;
     if (un.ns > 1) {
@@ -387,6 +451,30 @@ attn_bwd_dq_f32_kernel(const BwdParams p) {
         }
 }
 
+// Two waves per SIMD at head_dim 64 (the registers fit; measured 7% faster
+// at B8 S2048 9/3 heads), one at 128.
+template <int DP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 2 : 1, DP == 64 ? 2 : 1))) void
+attn_bwd_dq_f32_kernel(const BwdParams p) {
+    constexpr int BN = 32;
+    __shared__ __attribute__((aligned(16))) float sK0[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sK1[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sK2[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sV0[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sV1[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sV2[BN * DP];
+    if (p.q_xcd_wgs > 0) {
+        const int n_groups = p.q_items / p.n_ttiles;
+        int tile, grp;
+        for (int it = 0; f32_persistent_item(it, n_groups, p.n_ttiles, p.q_xcd_wgs, tile, grp); it++)
+            dq_f32_unit<DP>(p, F32Unit{tile, 0, 1}, grp, sK0, sK1, sK2, sV0, sV1, sV2);
+        return;
+    }
+    const int id = xcd_remap(blockIdx.x, p.n_wg_q, p.xcd);
+    const F32Unit un = f32_unit(id % p.units_q, p.n_ttiles, 32 * p.tpw, p.seq, p.ksplit);
+    dq_f32_unit<DP>(p, un, id / p.units_q, sK0, sK1, sK2, sV0, sV1, sV2);
+}
+
 // ------------------------------------------------------------------ dK/dV
 // Workgroup = (128-key tile, query head h, sequence, query split qs): four
 // waves of 32 keys share 32-query Q/dO tiles of head h; the workgroup visits
@@ -403,6 +491,7 @@ struct F32DkdvArgs {
     int slots;       // group * qs_n
     int qt_run;      // query tiles per split at most
     int units;       // workgroups per (sequence, query head)
+    int xcd_wgs;     // persistent grid: workgroups per XCD (0: one unit per workgroup)
 };
 
 // Query splits of 128-key tile kvt: its n_qt - 4 kvt query tiles in runs of
@@ -411,15 +500,15 @@ __device__ __forceinline__ int f32_kv_splits(int kvt, int n_qt, int qt_run) {
     return (n_qt - 4 * kvt + qt_run - 1) / qt_run;
 }
 
+// One work unit of the dK/dV grid: unit u of group rest = sequence * nh +
+// query head (units in key-tile order, a key tile's query splits
+// consecutive).  As fwd_f32_unit, every wave passes the same barriers and no
+// LDS read follows the last one.
 template <int DP>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams p, const F32DkdvArgs a) {
+__device__ __forceinline__ void dkdv_f32_unit(const BwdParams& p, const F32DkdvArgs& a, int u, int rest, float* sQ0,
+                                              float* sQ1, float* sQ2, float* sO0, float* sO1, float* sO2,
+                                              float (*sLD)[64]) {
     constexpr int NW = 4, BM = 32, HALF = DP / 2, NDB = DP / 32;
-    __shared__ __attribute__((aligned(16))) float sQ0[BM * DP];
-    __shared__ __attribute__((aligned(16))) float sQ1[BM * DP];
-    __shared__ __attribute__((aligned(16))) float sO0[BM * DP];
-    __shared__ __attribute__((aligned(16))) float sO1[BM * DP];
-    __shared__ __attribute__((aligned(16))) float sL[2][BM];
-    __shared__ __attribute__((aligned(16))) float sD[2][BM];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -427,15 +516,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams 
     const int wv = wave_uniform(wave);
 
     const int n_qt = (p.seq + BM - 1) / BM;
-    const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
-    int u = id % a.units, kvt = 0, qs_n = 1;  // low key tiles see the most queries: first
+    int kvt = 0, qs_n = 1;  // low key tiles see the most queries: first
     for (;; kvt++) {
         qs_n = f32_kv_splits(kvt, n_qt, a.qt_run);
         if (u < qs_n || kvt == p.n_kvtiles - 1) break;
         u -= qs_n;
     }
     const int qs = u;
-    int rest = id / a.units;
     const int h = rest % p.nh;
     const int b = rest / p.nh;
     const int g = h / p.group;
@@ -450,6 +537,22 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams 
     const float* lse_h = p.lse + ((long)b * p.nh + h) * p.seq;
     const float* dlt_h = p.delta + ((long)b * p.nh + h) * p.seq;
 
+    const int qt_first = wg_key0 / BM + qs;
+    const int n_steps = qt_first < n_qt ? (n_qt - qt_first + qs_n - 1) / qs_n : 0;
+    auto step_q0 = [&](int s) { return (qt_first + s * qs_n) * BM; };
+
+    // Step s's Q and dO tiles, and its lse / delta entries (every wave
+    // loads all 64, so each wave's load count per step is the same; rows
+    // past the end repeat the last row and are masked in the step).
+    auto dma = [&](int s, float* Qd, float* Od, float* LDd) {
+        const int q0 = step_q0(s);
+        f32_tile_dma<DP, NW>(qg, qrs, q0, p.seq - 1, Qd, wv, lane);
+        f32_tile_dma<DP, NW>(og, qrs, q0, p.seq - 1, Od, wv, lane);
+        const int t = min(q0 + (lane & (BM - 1)), p.seq - 1);
+        lds_load4_asm((lane < BM ? lse_h : dlt_h) + t, LDd);
+    };
+    if (n_steps > 0) dma(0, sQ0, sO0, sLD[0]);
+
     // K^T / V^T operands: key kw, head dims hh*HALF + kd.
     float kf[HALF], vf[HALF];
     {
@@ -462,37 +565,17 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams 
             vf[4 * i] = y.x, vf[4 * i + 1] = y.y, vf[4 * i + 2] = y.z, vf[4 * i + 3] = y.w;
         }
     }
+    // The K/V rows and step 0's loads have landed; a wait the compiler sees
+    // (see the forward).
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     f32x16 dkt[NDB], dvt[NDB];
 #pragma unroll
     for (int i = 0; i < NDB; i++) dkt[i] = zero16(), dvt[i] = zero16();
 
-    const int qt_first = wg_key0 / BM + qs;
-    const int n_steps = qt_first < n_qt ? (n_qt - qt_first + qs_n - 1) / qs_n : 0;
-    auto step_q0 = [&](int s) { return (qt_first + s * qs_n) * BM; };
-
-    float pl = 0.0f;
-    auto dma = [&](int s, float* Qd, float* Od) {
-        const int q0 = step_q0(s);
-        f32_tile_dma<DP, NW>(qg, qrs, q0, p.seq - 1, Qd, wv, lane);
-        f32_tile_dma<DP, NW>(og, qrs, q0, p.seq - 1, Od, wv, lane);
-        if (tid < 2 * BM) {
-            const int t = min(q0 + (tid & (BM - 1)), p.seq - 1);
-            pl = tid < BM ? lse_h[t] : dlt_h[t];
-        }
-    };
-    auto store_ld = [&](int s, int st) {
-        if (tid >= 2 * BM) return;
-        const int i = tid & (BM - 1);
-        const bool ok = step_q0(s) + i < p.seq;
-        if (tid < BM)
-            sL[st][i] = ok ? pl * kLog2e : INFINITY;  // rows past the end: P = 0
-        else
-            sD[st][i] = ok ? pl : 0.0f;
-    };
-
-    auto step = [&](int s, const float* Qs, const float* Os, float* Qn, float* On) {
-        const int st = s & 1;
-        const bool more = s + 1 < n_steps;
+    // Three Q/dO buffers: the tiles two steps ahead are loaded during a
+    // step, into the buffers the previous step read.
+    auto step = [&](int s, const float* Qs, const float* Os, const float* LDs, float* Qn, float* On, float* LDn) {
+        const bool ahead = s + 2 < n_steps;
         const int q0 = step_q0(s);
         if (wave_active && q0 + BM - 1 >= key0 && q0 < p.seq) {
             // S and dP: rows = queries q0 + [0, 32), columns = this wave's keys.
@@ -509,20 +592,24 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams 
                 dp = mfma_f32(y.z, vf[4 * c + 2], dp);
                 sc = mfma_f32(x.w, kf[4 * c + 3], sc);
                 dp = mfma_f32(y.w, vf[4 * c + 3], dp);
+                if (c == 0 && ahead) dma(s + 2, Qn, On, LDn);  // behind the first MFMAs, as the forward
             }
-            if (more) dma(s + 1, Qn, On);
-            const bool masked = q0 < key0 + 31;
+            // Masked: the diagonal steps and the one past the sequence end
+            // (P = 0 for keys after the query and for queries >= seq).
+            const bool masked = q0 < key0 + 31 || q0 + BM > p.seq;
             float pr[16], ds[16];
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) {
-                const float4 l4 = *reinterpret_cast<const float4*>(&sL[st][g4 * 8 + hh * 4]);
-                const float4 d4 = *reinterpret_cast<const float4*>(&sD[st][g4 * 8 + hh * 4]);
-                const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
+                const float4 l4 = *reinterpret_cast<const float4*>(LDs + g4 * 8 + hh * 4);
+                const float4 d4 = *reinterpret_cast<const float4*>(LDs + BM + g4 * 8 + hh * 4);
+                const float lv[4] = {l4.x * kLog2e, l4.y * kLog2e, l4.z * kLog2e, l4.w * kLog2e};
+                const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = g4 * 4 + i;
+                    const int qr = q0 + acc_row(r, hh);
                     float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], p.sl2, -lv[i]));
-                    if (masked && kw > q0 + acc_row(r, hh)) pv = 0.0f;
+                    if (masked && (kw > qr || qr >= p.seq)) pv = 0.0f;
                     pr[r] = pv;
                     ds[r] = pv * (dp[r] - dv[i]);
                 }
@@ -537,23 +624,18 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams 
                     dvt[db] = mfma_f32(Os[at], pr[j], dvt[db]);
                     dkt[db] = mfma_f32(Qs[at], ds[j], dkt[db]);
                 }
-        } else if (more) {
-            dma(s + 1, Qn, On);
+        } else if (ahead) {
+            dma(s + 2, Qn, On, LDn);
         }
-        if (more) store_ld(s + 1, st ^ 1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        f32_step_end<DP, NW, 1>(ahead);  // step s + 1's tiles and entries are in LDS
     };
 
-    if (n_steps > 0) {
-        dma(0, sQ0, sO0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        store_ld(0, 0);
-        __syncthreads();
-    }
-    for (int s = 0; s < n_steps; s += 2) {
-        step(s, sQ0, sO0, sQ1, sO1);
-        if (s + 1 < n_steps) step(s + 1, sQ1, sO1, sQ0, sO0);
+    if (n_steps > 1) dma(1, sQ1, sO1, sLD[1]);
+    f32_step_end<DP, NW, 1>(n_steps > 1);
+    for (int s = 0; s < n_steps; s += 3) {
+        step(s, sQ0, sO0, sLD[0], sQ2, sO2, sLD[2]);
+        if (s + 1 < n_steps) step(s + 1, sQ1, sO1, sLD[1], sQ0, sO0, sLD[0]);
+        if (s + 2 < n_steps) step(s + 2, sQ2, sO2, sLD[2], sQ1, sO1, sLD[1]);
     }
 
     if (!wave_active || kw >= p.seq) return;
@@ -572,6 +654,29 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams 
             *reinterpret_cast<float4*>(pv + d) =
                 make_float4(dvt[db][rq * 4], dvt[db][rq * 4 + 1], dvt[db][rq * 4 + 2], dvt[db][rq * 4 + 3]);
         }
+}
+
+template <int DP>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_f32_kernel(const BwdParams p, const F32DkdvArgs a) {
+    constexpr int BM = 32;
+    __shared__ __attribute__((aligned(16))) float sQ0[BM * DP];
+    __shared__ __attribute__((aligned(16))) float sQ1[BM * DP];
+    __shared__ __attribute__((aligned(16))) float sQ2[BM * DP];
+    __shared__ __attribute__((aligned(16))) float sO0[BM * DP];
+    __shared__ __attribute__((aligned(16))) float sO1[BM * DP];
+    __shared__ __attribute__((aligned(16))) float sO2[BM * DP];
+    // lse (entries 0..31) and delta (32..63) of a step's queries, one ring
+    // slot per tile buffer.
+    __shared__ __attribute__((aligned(16))) float sLD[3][2 * BM];
+    if (a.xcd_wgs > 0) {
+        // Persistent: units longest (lowest key tile) first, as the forward.
+        int t, grp;
+        for (int it = 0; f32_persistent_item(it, p.batch * p.nh, a.units, a.xcd_wgs, t, grp); it++)
+            dkdv_f32_unit<DP>(p, a, a.units - 1 - t, grp, sQ0, sQ1, sQ2, sO0, sO1, sO2, sLD);
+        return;
+    }
+    const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
+    dkdv_f32_unit<DP>(p, a, id % a.units, id / a.units, sQ0, sQ1, sQ2, sO0, sO1, sO2, sLD);
 }
 
 // dk += sum over slots (query head of the group, then query split) of the
@@ -703,6 +808,28 @@ static F32KvPlan f32_kv_plan(const Dims& d) {
     return pl;
 }
 
+static hipError_t f32_cus(int* cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return hipErrorInvalidDevice;
+    return hipSuccess;
+}
+
+// Workgroups per XCD of the persistent dK/dV grid (one workgroup per CU: the
+// kernel's registers allow no second), or 0 for one workgroup per unit:
+// persistent when XCD-aware with a (sequence, head) group per XCD and units
+// for every CU.
+static hipError_t f32_kv_persistent(const Dims& d, int xcd, long units, int* wgs) {
+    *wgs = 0;
+    if (!xcd) return hipSuccess;
+    int cus = 0;
+    const hipError_t e = f32_cus(&cus);
+    if (e != hipSuccess) return e;
+    if (cus >= 8 && cus % 8 == 0 && (long)d.batch * d.nh >= 8 && units >= cus) *wgs = cus / 8;
+    return hipSuccess;
+}
+
 // Grid of the forward and dQ kernels: hpw heads x tpw 32-query blocks per
 // workgroup, and the key split.  A causal grid is as slow as its longest query
 // tile, and at one wave per SIMD the kernels also wait on every load; when
@@ -749,6 +876,21 @@ static F32Plan f32_plan(const Dims& d, int group) {
 
 static size_t f32_rows(const Dims& d) { return (size_t)d.batch * d.nh * d.seq; }
 
+// Workgroups per XCD of the persistent forward / dQ grid, or 0 for one
+// workgroup per unit: persistent when the grid is unsplit, XCD-aware, has a
+// group per XCD and fills every workgroup slot (two per CU at head_dim 64,
+// where two waves per SIMD fit, one at 128).
+static int f32_persistent_wgs(const Dims& d, const F32Plan& pl, int xcd, long units, hipError_t* err) {
+    *err = hipSuccess;
+    if (pl.ks || !xcd) return 0;
+    int cus = 0;
+    if ((*err = f32_cus(&cus)) != hipSuccess) return 0;
+    const int per_cu = d.hd == 64 ? 2 : 1;
+    const long groups = (long)d.nkv * pl.n_sub * d.batch;
+    if (cus < 8 || cus % 8 != 0 || groups < 8 || units < (long)cus * per_cu) return 0;
+    return cus / 8 * per_cu;
+}
+
 size_t attn_f32_scratch_bytes(const Dims& d) {
     if (!f32_fast_ok(d.hd) || d.batch <= 0 || d.seq <= 0 || d.nkv <= 0) return 0;
     const size_t half = (size_t)d.batch * d.seq * d.nkv * d.hd;
@@ -773,8 +915,8 @@ bool attn_f32_fast_applies(const Dims& d, int vec_ok, int o_vec_ok) {
 
 // `scratch` (attn_f32_fwd_scratch_bytes(d) bytes) holds the key splits'
 // partial results; without it the grid runs unsplit.
-hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t scratch_bytes, hipStream_t st,
-                               KernelTimer* tm) {
+hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t scratch_bytes, bool persistent,
+                               hipStream_t st, KernelTimer* tm) {
     F32Plan pl = f32_plan(d, p.group);
     const size_t need = attn_f32_fwd_scratch_bytes(d);
     if (pl.ks && (scratch == nullptr || scratch_bytes < need)) pl.ks = 0, pl.units = pl.n_ttiles;
@@ -790,6 +932,11 @@ hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t
     const long n_wg = (long)pl.units * d.nkv * p.n_sub * d.batch;
     if (n_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
     p.n_wg = (int)n_wg;
+    hipError_t pe = hipSuccess;
+    p.xcd_wgs = persistent ? f32_persistent_wgs(d, pl, p.xcd, n_wg, &pe) : 0;
+    if (pe != hipSuccess) return pe;
+    p.n_items = p.n_wg;
+    if (p.xcd_wgs > 0) p.n_wg = 8 * p.xcd_wgs;
     TimedLaunch tl(tm, kKernFwd, st);
     if (d.hd == 128)
         hipLaunchKernelGGL(attn_fwd_f32_kernel<128>, dim3(p.n_wg), dim3(256), 0, st, p);
@@ -808,7 +955,8 @@ hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t
 
 // dK/dV then dQ (delta is already computed); `scratch` holds
 // attn_f32_scratch_bytes(d) bytes.
-hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStream_t st, KernelTimer* tm) {
+hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, bool persistent, hipStream_t st,
+                               KernelTimer* tm) {
     F32DkdvArgs a;
     const F32KvPlan kp = f32_kv_plan(d);
     a.qs_n = kp.qs_max;
@@ -822,7 +970,9 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStr
     const long nkv_wg = (long)kp.units * d.nh * d.batch;
     if (nkv_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
     p.n_wg_kv = (int)nkv_wg;
-    hipError_t e;
+    hipError_t e = f32_kv_persistent(d, p.xcd && persistent, nkv_wg, &a.xcd_wgs);
+    if (e != hipSuccess) return e;
+    if (a.xcd_wgs > 0) p.n_wg_kv = 8 * a.xcd_wgs;
     {
         TimedLaunch tl(tm, kKernBwdDkdv, st);
         if (d.hd == 128)
@@ -849,6 +999,11 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStr
     const long nq_wg = (long)pl.units * d.nkv * p.n_sub * d.batch;
     if (nq_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
     p.n_wg_q = (int)nq_wg;
+    hipError_t pe = hipSuccess;
+    p.q_xcd_wgs = persistent ? f32_persistent_wgs(d, pl, p.xcd, nq_wg, &pe) : 0;
+    if (pe != hipSuccess) return pe;
+    p.q_items = p.n_wg_q;
+    if (p.q_xcd_wgs > 0) p.n_wg_q = 8 * p.q_xcd_wgs;
     TimedLaunch tl(tm, kKernBwdDq, st);
     if (d.hd == 128)
         hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<128>, dim3(p.n_wg_q), dim3(256), 0, st, p);

@@ -554,7 +554,7 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
     }
     if (dt == kF32 && attn_f32_fast_applies(d, p.vec_ok, p.o_vec_ok) && tu.fwd_heads_per_wg == 0 &&
         tu.fwd_tblocks_per_wg == 0)
-        return launch_attn_fwd_f32(d, p, scratch, scratch_bytes, st, tu.timer);
+        return launch_attn_fwd_f32(d, p, scratch, scratch_bytes, tu.f32_persistent != 0, st, tu.timer);
     const int nwaves = p.hpw * p.tpw;
     const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;
     if (dt == kBF16) {

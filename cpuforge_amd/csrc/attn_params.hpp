@@ -20,8 +20,9 @@ struct FwdParams {
     float sl2;  // softmax scale * log2(e)
     long q_bs, kv_bs;
     int vec_ok, o_vec_ok, xcd;
-    // Persistent grid of the bf16 head_dim 128 kernel: n_items query tiles,
-    // xcd_wgs workgroups per XCD (0: one item per workgroup).
+    // Persistent grid of the bf16 head_dim 128 kernel and of the fp32
+    // kernel: n_items query tiles, xcd_wgs workgroups per XCD (0: one item
+    // per workgroup).
     int n_items, xcd_wgs;
     // Key split of the fp32 kernel (0: none): a query tile's key tiles are
     // cut into runs of `ksplit`, one workgroup each; `units` workgroups per
@@ -69,6 +70,9 @@ struct BwdParams {
     int ksplit, units_q;
     long part_rows;
     float* qpart;
+    // Persistent fp32 dQ grid (no key split): q_items query tiles,
+    // q_xcd_wgs workgroups per XCD (0: one unit per workgroup).
+    int q_items, q_xcd_wgs;
     // Epilogue of the fast bf16 kernels' dQ and dK rows (BwdEpilogue).
     int epi;
     const float* rope_cos;
@@ -95,9 +99,10 @@ bool attn_f32_fast_applies(const Dims& d, int vec_ok, int o_vec_ok);
 size_t attn_f32_scratch_bytes(const Dims& d);
 // Scratch of the fp32 forward's key split (0 when the grid needs none).
 size_t attn_f32_fwd_scratch_bytes(const Dims& d);
-hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t scratch_bytes, hipStream_t st,
+hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t scratch_bytes, bool persistent,
+                               hipStream_t st, KernelTimer* tm);
+hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, bool persistent, hipStream_t st,
                                KernelTimer* tm);
-hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, hipStream_t st, KernelTimer* tm);
 // bf16 dK/dV at head_dim 128, one wave per SIMD (attn_dkdv.hip); with
 // `wds` it also stores dS for the stored-dS dQ kernel.  p.kv_tile is 128.
 void launch_attn_bwd_dkdv_k64(const BwdParams& p, bool wds, hipStream_t st);

@@ -161,6 +161,11 @@ struct cfattn_ctx {
         // for comparison and measurement).
         const char* n = std::getenv("CFATTN_NORM_EPILOGUE");
         if (n && std::strcmp(n, "0") == 0) t.norm_epilogue = 0;
+        // CFATTN_F32_GRID=unit launches the fp32 kernels with one workgroup
+        // per work unit instead of persistent grids (same bits; kept for
+        // comparison and measurement).
+        const char* g = std::getenv("CFATTN_F32_GRID");
+        if (g && std::strcmp(g, "unit") == 0) t.f32_persistent = 0;
         return t;
     }
 };

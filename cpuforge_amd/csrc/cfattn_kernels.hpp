@@ -59,6 +59,9 @@ struct Tuning {
     // The fused backward's Qwen3 norm in the dQ/dK epilogues (kEpiUnrotNorm);
     // 0: the epilogues store the unrotated rows and a separate norm pass runs.
     int norm_epilogue = 1;
+    // fp32 kernels: persistent grids (0: one workgroup per work unit; the
+    // same bits either way).
+    int f32_persistent = 1;
     KernelTimer* timer = nullptr;
     // Device counter of the bf16 head_dim-128 forward's settled wave-tiles
     // (the slow path of its row-sum guard), incremented when non-null.

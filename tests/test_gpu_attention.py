@@ -474,6 +474,32 @@ def test_bf16_backward_is_bitwise_repeatable(cf, shape, ds):
             assert np.array_equal(a, b), f"{shape} {ds} {name}: max diff {np.abs(a - b).max()}"
 
 
+@pytest.mark.parametrize("shape", [(8, 2048, 9, 3, 64), (4, 1500, 16, 4, 64), (2, 1000, 16, 8, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_f32_persistent_grids_match_unit_grids(cf, shape, monkeypatch):
+    """The fp32 forward, dQ and dK/dV kernels run persistent grids (each
+    workgroup walks a snake of work units) on shapes that fill every
+    workgroup slot; CFATTN_F32_GRID=unit launches one workgroup per unit.
+    Each unit computes the same sums either way: O, lse, dQ, dK, dV must be
+    bitwise equal."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    print(f"f32 persistent vs unit grids, shape {shape}", flush=True)
+    _, (q, k, v, g) = _fast_inputs(shape, seed=2100, mode="f32")
+    out = {}
+    for grid in ("unit", "persistent"):
+        if grid == "unit":
+            monkeypatch.setenv("CFATTN_F32_GRID", "unit")
+        else:
+            monkeypatch.delenv("CFATTN_F32_GRID", raising=False)
+        o, lse = D.fwd(q, k, v, ctx=ctx)
+        out[grid] = [x.cpu().numpy() for x in (o, lse, *D.bwd(g, q, k, v, o, lse, ctx=ctx))]
+    torch.cuda.synchronize()
+    for name, a, b in zip(("o", "lse", "dq", "dk", "dv"), out["persistent"], out["unit"]):
+        assert np.array_equal(a, b), f"{shape} {name}: max diff {np.abs(a - b).max()}"
+
+
 @pytest.mark.parametrize("shape", [(8, 512, 9, 3, 64), (1, 2048, 4, 1, 128), (1, 1000, 8, 8, 64)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_f32_key_split_matches_oracle_and_unsplit(cf, shape):
