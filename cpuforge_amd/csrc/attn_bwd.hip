@@ -449,9 +449,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 // a 32-key block is key qperm(i) of the block (see BlkTile).
 // The NORM instance runs the kEpiUnrotNorm epilogue, the other one every
 // other mode.
+// One query tile (tile `tile` of group rest = (sequence * nkv + KV head) *
+// n_sub + head subset); without NORM no LDS read follows its last barrier,
+// so the next tile of a persistent workgroup may load into the buffers.
 template <int DP, int BN, int NW, bool NORM>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq_bf16_kernel(
-    const BwdParams p) {
+__device__ __forceinline__ void dq_bf16_unit(const BwdParams& p, const int tile, int rest, bf16_bits* sK0,
+                                             bf16_bits* sK1, bf16_bits* sV0, bf16_bits* sV1) {
     constexpr int CPR = DP / 8;
     using L = BlkTile<DP, BN>;
     constexpr int CPW = L::NB / NW;  // 1 KiB loads per wave per tile
@@ -460,18 +463,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16;
     static_assert(L::NB % NW == 0, "tile must split evenly over the waves");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NKB = BN / 32;
-    __shared__ __attribute__((aligned(16))) bf16_bits sK0[L::SIZE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sK1[L::SIZE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sV0[L::SIZE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sV1[L::SIZE];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int l32 = lane & 31, hh = lane >> 5;
 
-    const int id = xcd_remap(blockIdx.x, p.n_wg_q, p.xcd);
-    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;
-    int rest = id / p.n_ttiles;
     const int sub = rest % p.n_sub;
     rest /= p.n_sub;
     const int g = rest % p.nkv;
@@ -648,6 +644,29 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
     for (int db = 0; db < NDB; db++) dqt[db] *= p.scale;  // dS was accumulated without the softmax scale
     write_grad_row<NDB>(p.dq + qoff, dqt, hh, tq, p);
+}
+
+template <int DP, int BN, int NW, bool NORM>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dq_bf16_kernel(
+    const BwdParams p) {
+    using L = BlkTile<DP, BN>;
+    __shared__ __attribute__((aligned(16))) bf16_bits sK0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sK1[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV1[L::SIZE];
+    if constexpr (!NORM && DP == 64) {
+        // Persistent grid at head_dim 64 (the NORM epilogue's gain partials
+        // are per workgroup, so that instance keeps one workgroup per tile;
+        // at 128 the loop's registers would spill).
+        if (p.q_xcd_wgs > 0) {
+            int tile, grp;
+            for (int it = 0; persistent_item(it, p.q_items / p.n_ttiles, p.n_ttiles, p.q_xcd_wgs, p.q_walk_gm, tile, grp); it++)
+                dq_bf16_unit<DP, BN, NW, NORM>(p, tile, grp, sK0, sK1, sV0, sV1);
+            return;
+        }
+    }
+    const int id = xcd_remap(blockIdx.x, p.n_wg_q, p.xcd);
+    dq_bf16_unit<DP, BN, NW, NORM>(p, p.n_ttiles - 1 - id % p.n_ttiles, id / p.n_ttiles, sK0, sK1, sV0, sV1);
 }
 
 // dQ from the stored dS: dQ^T += K^T dS^T over the key blocks at or before
@@ -1548,8 +1567,29 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
                     hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<128, 64, kDqDsWaves, false>), dim3(p.n_wg_q),
                                        dim3(64 * kDqDsWaves), 0, st, p);
             } else {
-                const dim3 g(p.n_wg_q), blk(64 * kDqWaves);
                 const bool norm = p.epi == kEpiUnrotNorm;
+                // Persistent grid (two workgroups per CU) at head_dim 64 when
+                // the tiles fill every workgroup slot with a group per XCD,
+                // up to four tiles per slot (as the forward); not with the
+                // norm epilogue (its gain partials are per workgroup).
+                p.q_items = p.n_wg_q;
+                p.q_xcd_wgs = 0;
+                if (!norm && d.hd == 64 && tu.bf16_persistent && p.xcd) {
+                    int dev = 0, cus = 0;
+                    if (hipGetDevice(&dev) != hipSuccess ||
+                        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+                        return hipErrorInvalidDevice;
+                    if (cus >= 8 && cus % 8 == 0 && (long)d.nkv * p.n_sub * d.batch >= 8 && nq_wg >= 2L * cus &&
+                        nq_wg <= 8L * cus) {
+                        p.q_xcd_wgs = cus / 8 * 2;
+                        p.n_wg_q = 8 * p.q_xcd_wgs;
+                        const int tt = 32 * p.tpw, seq = d.seq;
+                        p.q_walk_gm = persistent_group_major(
+                            p.q_items / p.n_ttiles, p.n_ttiles, p.q_xcd_wgs,
+                            [&](int t) { return (long)(std::min(seq, (t + 1) * tt) + 127) / 128; });
+                    }
+                }
+                const dim3 g(p.n_wg_q), blk(64 * kDqWaves);
                 if (d.hd == 128 && norm)
                     hipLaunchKernelGGL((attn_bwd_dq_bf16_kernel<128, 64, kDqWaves, true>), g, blk, 0, st, p);
                 else if (d.hd == 128)

@@ -24,6 +24,7 @@
 // attn_f32_reduce_kernel adds the slots of a KV head in a fixed order (query
 // head, then query split), so results are reproducible bit for bit.
 #include <algorithm>
+#include <vector>
 
 #include "attn_params.hpp"
 #include "cfattn_common.hpp"
@@ -90,27 +91,6 @@ __device__ __forceinline__ void f32_step_end(bool newer) {
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-}
-
-// Work unit `it` of a persistent workgroup of the forward or dQ grid (no key
-// split): the XCD of workgroup w (w % 8; the dispatcher deals workgroups
-// round robin) takes a contiguous run of the n_groups (sequence, KV head,
-// head subset) groups, so that its L2 holds few KV heads, and its W
-// workgroups walk the run's query tiles longest first in a snake (positions
-// l, 2W - 1 - l, 2W + l, ...), which gives every workgroup nearly the same
-// number of key tiles.  (A grid of one workgroup per unit leaves CUs idle
-// while units remain: units of very different lengths stall the in-order
-// dispatch.)  False past the run.
-__device__ __forceinline__ bool f32_persistent_item(int it, int n_groups, int n_ttiles, int W, int& tile, int& grp) {
-    const int xq = blockIdx.x % 8, xl = blockIdx.x / 8;
-    const int q = n_groups / 8, r = n_groups % 8;
-    const int g0 = xq < r ? xq * (q + 1) : r * (q + 1) + (xq - r) * q;
-    const int gn = q + (xq < r ? 1 : 0);
-    const int pos = (it >> 1) * 2 * W + ((it & 1) ? 2 * W - 1 - xl : xl);
-    if (gn == 0 || pos >= gn * n_ttiles) return false;
-    tile = n_ttiles - 1 - pos / gn;
-    grp = g0 + pos % gn;
-    return true;
 }
 
 // Query tile, key split and split count of work unit u of one (sequence, KV
@@ -305,7 +285,7 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(const FwdParams p) {
     if (p.xcd_wgs > 0) {
         const int n_groups = p.n_items / p.n_ttiles;
         int tile, grp;
-        for (int it = 0; f32_persistent_item(it, n_groups, p.n_ttiles, p.xcd_wgs, tile, grp); it++)
+        for (int it = 0; persistent_item(it, n_groups, p.n_ttiles, p.xcd_wgs, p.walk_gm, tile, grp); it++)
             fwd_f32_unit<DP>(p, F32Unit{tile, 0, 1}, grp, sK0, sK1, sK2, sV0, sV1, sV2);
         return;
     }
@@ -466,7 +446,7 @@ attn_bwd_dq_f32_kernel(const BwdParams p) {
     if (p.q_xcd_wgs > 0) {
         const int n_groups = p.q_items / p.n_ttiles;
         int tile, grp;
-        for (int it = 0; f32_persistent_item(it, n_groups, p.n_ttiles, p.q_xcd_wgs, tile, grp); it++)
+        for (int it = 0; persistent_item(it, n_groups, p.n_ttiles, p.q_xcd_wgs, p.q_walk_gm, tile, grp); it++)
             dq_f32_unit<DP>(p, F32Unit{tile, 0, 1}, grp, sK0, sK1, sK2, sV0, sV1, sV2);
         return;
     }
@@ -492,6 +472,7 @@ struct F32DkdvArgs {
     int qt_run;      // query tiles per split at most
     int units;       // workgroups per (sequence, query head)
     int xcd_wgs;     // persistent grid: workgroups per XCD (0: one unit per workgroup)
+    int walk_gm;     // its walk order (persistent_item)
 };
 
 // Query splits of 128-key tile kvt: its n_qt - 4 kvt query tiles in runs of
@@ -675,7 +656,7 @@ attn_bwd_dkdv_f32_kernel(const BwdParams p, const F32DkdvArgs a) {
     if (a.xcd_wgs > 0) {
         // Persistent: units longest (lowest key tile) first, as the forward.
         int t, grp;
-        for (int it = 0; f32_persistent_item(it, p.batch * p.nh, a.units, a.xcd_wgs, t, grp); it++)
+        for (int it = 0; persistent_item(it, p.batch * p.nh, a.units, a.xcd_wgs, a.walk_gm, t, grp); it++)
             dkdv_f32_unit<DP>(p, a, a.units - 1 - t, grp, sQ0, sQ1, sQ2, sO0, sO1, sO2, sLD);
         return;
     }
@@ -882,6 +863,14 @@ static F32Plan f32_plan(const Dims& d, int group) {
 
 static size_t f32_rows(const Dims& d) { return (size_t)d.batch * d.nh * d.seq; }
 
+// Walk order of the persistent forward / dQ grid: a query tile's work is its
+// 32-key tiles.
+static int f32_walk_order(const Dims& d, const F32Plan& pl, long items, int wgs) {
+    const int tt = 32 * pl.tpw, seq = d.seq;
+    return persistent_group_major((int)(items / pl.n_ttiles), pl.n_ttiles, wgs,
+                                  [&](int t) { return (long)(std::min(seq, (t + 1) * tt) + 31) / 32; });
+}
+
 // Workgroups per XCD of the persistent forward / dQ grid, or 0 for one
 // workgroup per unit: persistent when the grid is unsplit, XCD-aware, has a
 // group per XCD and fills every workgroup slot (two per CU at head_dim 64,
@@ -942,7 +931,10 @@ hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t
     p.xcd_wgs = persistent ? f32_persistent_wgs(d, pl, p.xcd, n_wg, &pe) : 0;
     if (pe != hipSuccess) return pe;
     p.n_items = p.n_wg;
-    if (p.xcd_wgs > 0) p.n_wg = 8 * p.xcd_wgs;
+    if (p.xcd_wgs > 0) {
+        p.n_wg = 8 * p.xcd_wgs;
+        p.walk_gm = f32_walk_order(d, pl, p.n_items, p.xcd_wgs);
+    }
     TimedLaunch tl(tm, kKernFwd, st);
     if (d.hd == 128)
         hipLaunchKernelGGL(attn_fwd_f32_kernel<128>, dim3(p.n_wg), dim3(256), 0, st, p);
@@ -978,7 +970,24 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, bool p
     p.n_wg_kv = (int)nkv_wg;
     hipError_t e = f32_kv_persistent(d, p.xcd && persistent, nkv_wg, &a.xcd_wgs);
     if (e != hipSuccess) return e;
-    if (a.xcd_wgs > 0) p.n_wg_kv = 8 * a.xcd_wgs;
+    a.walk_gm = 0;
+    if (a.xcd_wgs > 0) {
+        p.n_wg_kv = 8 * a.xcd_wgs;
+        // A unit's work is its steps (query tiles); units in key-tile
+        // order, a key tile's splits consecutive (as dkdv_f32_unit decodes).
+        const int n_qt = (d.seq + 31) / 32;
+        std::vector<long> steps;
+        for (int kvt = 0; kvt < p.n_kvtiles; kvt++) {
+            const int qs_n = (n_qt - 4 * kvt + a.qt_run - 1) / a.qt_run;
+            for (int qs = 0; qs < qs_n; qs++) {
+                const int first = 4 * kvt + qs;
+                steps.push_back(first < n_qt ? (n_qt - first + qs_n - 1) / qs_n : 0);
+            }
+        }
+        if ((int)steps.size() == a.units)
+            a.walk_gm = persistent_group_major(d.batch * d.nh, a.units, a.xcd_wgs,
+                                               [&](int t) { return steps[a.units - 1 - t]; });
+    }
     {
         TimedLaunch tl(tm, kKernBwdDkdv, st);
         if (d.hd == 128)
@@ -1009,7 +1018,10 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, bool p
     p.q_xcd_wgs = persistent ? f32_persistent_wgs(d, pl, p.xcd, nq_wg, &pe) : 0;
     if (pe != hipSuccess) return pe;
     p.q_items = p.n_wg_q;
-    if (p.q_xcd_wgs > 0) p.n_wg_q = 8 * p.q_xcd_wgs;
+    if (p.q_xcd_wgs > 0) {
+        p.n_wg_q = 8 * p.q_xcd_wgs;
+        p.q_walk_gm = f32_walk_order(d, pl, p.q_items, p.q_xcd_wgs);
+    }
     TimedLaunch tl(tm, kKernBwdDq, st);
     if (d.hd == 128)
         hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<128>, dim3(p.n_wg_q), dim3(256), 0, st, p);

@@ -19,6 +19,8 @@
 //        straight from the S^T accumulators, rounded to bf16 in bf16 mode).
 // Workgroups are ordered longest-first (most key tiles) and remapped so each
 // XCD works through contiguous (sequence, KV head) ranges.
+#include <algorithm>
+
 #include "cfattn_common.hpp"
 #include "attn_params.hpp"
 #include "cfattn_kernels.hpp"
@@ -228,9 +230,13 @@ constexpr float kLazyRescale = 8.0f;
 // four (two workgroups per CU) measured faster than eight (one).
 constexpr int kFastWaves = 4;
 
+// One query tile of hpw heads x tpw 32-query blocks: tile `tile` of group
+// rest = (sequence * nkv + KV head) * n_sub + head subset.  Every wave passes
+// the same barriers and no LDS read follows the last one, so the next tile of
+// a persistent workgroup may load into the buffers.
 template <int DP, int BN, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_bf16_kernel(
-    const FwdParams p) {
+__device__ __forceinline__ void fwd_bf16_unit(const FwdParams& p, const int tile, int rest, bf16_bits* sK0,
+                                              bf16_bits* sK1, bf16_bits* sV0, bf16_bits* sV1) {
     constexpr int CPR = DP / 8;  // 16-byte chunks per row
     using L = BlkTile<DP, BN>;
     constexpr int CPW = L::NB / NW;  // 1 KiB loads per wave per tile
@@ -239,18 +245,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     constexpr int BSTRIDE = L::STRIDE, ROW16 = L::ROW16;
     static_assert(L::NB % NW == 0, "tile must split evenly over the waves");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NKB = BN / 32;
-    __shared__ __attribute__((aligned(16))) bf16_bits sK0[L::SIZE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sK1[L::SIZE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sV0[L::SIZE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sV1[L::SIZE];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int l32 = lane & 31, hh = lane >> 5;
 
-    const int id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
-    const int tile = p.n_ttiles - 1 - id % p.n_ttiles;  // longest tiles first
-    int rest = id / p.n_ttiles;
     const int sub = rest % p.n_sub;
     rest /= p.n_sub;
     const int g = rest % p.nkv;
@@ -471,6 +470,24 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
     if (hh == 0) p.lse[((long)b * p.nh + head) * p.seq + tq] = (m2 + __log2f(ltot)) * kLn2;
 }
 
+template <int DP, int BN, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_bf16_kernel(
+    const FwdParams p) {
+    using L = BlkTile<DP, BN>;
+    __shared__ __attribute__((aligned(16))) bf16_bits sK0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sK1[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sV1[L::SIZE];
+    if (p.xcd_wgs > 0) {
+        int tile, grp;
+        for (int it = 0; persistent_item(it, p.n_items / p.n_ttiles, p.n_ttiles, p.xcd_wgs, p.walk_gm, tile, grp); it++)
+            fwd_bf16_unit<DP, BN, NW>(p, tile, grp, sK0, sK1, sV0, sV1);
+        return;
+    }
+    const int id = xcd_remap(blockIdx.x, p.n_wg, p.xcd);
+    fwd_bf16_unit<DP, BN, NW>(p, p.n_ttiles - 1 - id % p.n_ttiles, id / p.n_ttiles, sK0, sK1, sV0, sV1);  // longest first
+}
+
 // Heads per workgroup: the largest divisor of `group` not above `cap`.
 static int pick_hpw(int group, int cap) {
     for (int h = cap < group ? cap : group; h >= 1; h--)
@@ -543,6 +560,28 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
         n_wg = (long)p.n_ttiles * d.nkv * p.n_sub * d.batch;
         if (n_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
         p.n_wg = (int)n_wg;
+        // Persistent grid (two workgroups per CU) when the tiles fill every
+        // workgroup slot with a group per XCD, up to four tiles per slot;
+        // else one workgroup per tile.  (With few tiles per slot the in-
+        // order dispatch leaves CUs idle: C2's grid, 2.25 tiles per slot, runs
+        // 16% faster persistent; with many the idle share is small and the
+        // persistent grid measured slower: C3's, 8 per slot, 7%.)
+        p.n_items = p.n_wg;
+        p.xcd_wgs = 0;
+        if (tu.bf16_persistent && p.xcd) {
+            int dev = 0, cus = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+                return hipErrorInvalidDevice;
+            if (cus >= 8 && cus % 8 == 0 && (long)d.nkv * p.n_sub * d.batch >= 8 && n_wg >= 2L * cus &&
+                n_wg <= 8L * cus) {
+                p.xcd_wgs = cus / 8 * 2;
+                p.n_wg = 8 * p.xcd_wgs;
+                const int bn = d.hd == 128 ? 64 : 128, tt = 32 * p.tpw, seq = d.seq;
+                p.walk_gm = persistent_group_major(p.n_items / p.n_ttiles, p.n_ttiles, p.xcd_wgs,
+                                                   [&](int t) { return (long)(std::min(seq, (t + 1) * tt) + bn - 1) / bn; });
+            }
+        }
         TimedLaunch tl(tu.timer, kKernFwd, st);
         if (d.hd == 128)
             hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 64, kFastWaves>), dim3(p.n_wg), dim3(64 * kFastWaves), 0, st,

@@ -20,10 +20,10 @@ struct FwdParams {
     float sl2;  // softmax scale * log2(e)
     long q_bs, kv_bs;
     int vec_ok, o_vec_ok, xcd;
-    // Persistent grid of the bf16 head_dim 128 kernel and of the fp32
-    // kernel: n_items query tiles, xcd_wgs workgroups per XCD (0: one item
-    // per workgroup).
-    int n_items, xcd_wgs;
+    // Persistent grid of the bf16 kernels and of the fp32 kernel: n_items
+    // query tiles, xcd_wgs workgroups per XCD (0: one item per workgroup),
+    // walk_gm the walk order (persistent_item).
+    int n_items, xcd_wgs, walk_gm;
     // Key split of the fp32 kernel (0: none): a query tile's key tiles are
     // cut into runs of `ksplit`, one workgroup each; `units` workgroups per
     // (sequence, KV head, head subset).  Split s of a row writes its
@@ -70,9 +70,10 @@ struct BwdParams {
     int ksplit, units_q;
     long part_rows;
     float* qpart;
-    // Persistent fp32 dQ grid (no key split): q_items query tiles,
-    // q_xcd_wgs workgroups per XCD (0: one unit per workgroup).
-    int q_items, q_xcd_wgs;
+    // Persistent dQ grid (fp32, and bf16 recompute at head_dim 64): q_items
+    // query tiles, q_xcd_wgs workgroups per XCD (0: one unit per workgroup),
+    // q_walk_gm the walk order (persistent_item).
+    int q_items, q_xcd_wgs, q_walk_gm;
     // Epilogue of the fast bf16 kernels' dQ and dK rows (BwdEpilogue).
     int epi;
     const float* rope_cos;

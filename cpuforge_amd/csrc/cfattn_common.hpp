@@ -138,6 +138,37 @@ __device__ __forceinline__ int xcd_remap(int hw_id, int n, int enable) {
     return start + local;
 }
 
+// Work unit `it` of a workgroup of a persistent grid (8 * W workgroups) over
+// n_groups groups of n_units units each, unit n_units - 1 the longest (a
+// query tile, or a key tile counted from the end): the XCD of workgroup w
+// (w % 8; the dispatcher deals workgroups round robin) takes a contiguous run
+// of the groups (sequence and KV head, or query head), so that its L2 holds
+// few of their K/V or Q/dO rows, and its W workgroups walk the run's units
+// in a snake (positions l, 2W - 1 - l, 2W + l, ...), which gives every
+// workgroup nearly the same work: ordered longest unit first across the run
+// (unit-major), or group by group, each longest first (group-major: fewer
+// groups in flight at once, for the L2; persistent_group_major picks it where
+// it balances as well).  (A grid of one workgroup per unit leaves CUs idle
+// while units remain: units of very different lengths stall the in-order
+// dispatch.)  False past the run.
+__device__ __forceinline__ bool persistent_item(int it, int n_groups, int n_units, int W, int group_major, int& unit,
+                                                int& grp) {
+    const int xq = blockIdx.x % 8, xl = blockIdx.x / 8;
+    const int q = n_groups / 8, r = n_groups % 8;
+    const int g0 = xq < r ? xq * (q + 1) : r * (q + 1) + (xq - r) * q;
+    const int gn = q + (xq < r ? 1 : 0);
+    const int pos = (it >> 1) * 2 * W + ((it & 1) ? 2 * W - 1 - xl : xl);
+    if (gn == 0 || pos >= gn * n_units) return false;
+    if (group_major) {
+        unit = n_units - 1 - pos % n_units;
+        grp = g0 + pos / n_units;
+    } else {
+        unit = n_units - 1 - pos / gn;
+        grp = g0 + pos % gn;
+    }
+    return true;
+}
+
 // ------------------------------------------------------------ LDS staging
 template <typename T>
 union Chunk {

@@ -166,6 +166,10 @@ struct cfattn_ctx {
         // comparison and measurement).
         const char* g = std::getenv("CFATTN_F32_GRID");
         if (g && std::strcmp(g, "unit") == 0) t.f32_persistent = 0;
+        // CFATTN_BF16_GRID=unit: the same for the bf16 two-waves-per-SIMD
+        // kernels.
+        const char* h = std::getenv("CFATTN_BF16_GRID");
+        if (h && std::strcmp(h, "unit") == 0) t.bf16_persistent = 0;
         return t;
     }
 };

@@ -48,6 +48,29 @@ enum FwdVariant {
     kFwdTwoPerSimd = 1   // two waves per SIMD, 32 queries per wave
 };
 
+// Walk order of a persistent grid (persistent_item): 1 (group-major) when it
+// gives the busiest workgroup at most 2% more work than the unit-major walk,
+// else 0.  len(u) is the work of unit u (unit n_units - 1 the longest).
+template <class Len>
+inline int persistent_group_major(int n_groups, int n_units, int W, Len len) {
+    long worst[2] = {0, 0};
+    const int q = n_groups / 8, r = n_groups % 8;
+    for (int gn : {q, q + 1}) {
+        if (gn == 0 || (gn == q + 1 && r == 0)) continue;
+        for (int order = 0; order < 2; order++)
+            for (int l = 0; l < W; l++) {
+                long sum = 0;
+                for (int it = 0;; it++) {
+                    const long pos = (long)(it >> 1) * 2 * W + ((it & 1) ? 2 * W - 1 - l : l);
+                    if (pos >= (long)gn * n_units) break;
+                    sum += len(n_units - 1 - (int)(order ? pos % n_units : pos / gn));
+                }
+                if (sum > worst[order]) worst[order] = sum;
+            }
+    }
+    return worst[1] * 100 <= worst[0] * 102 ? 1 : 0;
+}
+
 // Tuning knobs of one launch; defaults are chosen by the launchers.
 struct Tuning {
     int xcd_remap = 1;  // XCD-aware workgroup ordering
@@ -62,6 +85,9 @@ struct Tuning {
     // fp32 kernels: persistent grids (0: one workgroup per work unit; the
     // same bits either way).
     int f32_persistent = 1;
+    // bf16 two-waves-per-SIMD kernels (forward, recompute dQ, wave-
+    // specialised dK/dV): persistent grids (0: one workgroup per unit).
+    int bf16_persistent = 1;
     KernelTimer* timer = nullptr;
     // Device counter of the bf16 head_dim-128 forward's settled wave-tiles
     // (the slow path of its row-sum guard), incremented when non-null.

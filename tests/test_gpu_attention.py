@@ -500,6 +500,38 @@ def test_f32_persistent_grids_match_unit_grids(cf, shape, monkeypatch):
         assert np.array_equal(a, b), f"{shape} {name}: max diff {np.abs(a - b).max()}"
 
 
+@pytest.mark.parametrize("shape", [(8, 2048, 9, 3, 64), (4, 1500, 16, 4, 64), (1, 4096, 32, 8, 64),
+                                   (4, 1000, 16, 8, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_bf16_persistent_grids_match_unit_grids(cf, shape, monkeypatch):
+    """The bf16 two-waves-per-SIMD forward and the recompute dQ kernel run
+    persistent grids where the tiles fill every workgroup slot, up to four per
+    slot (walked tile-major at 8x2048, group-major at 1x4096);
+    CFATTN_BF16_GRID=unit launches one workgroup per tile.  At head_dim 128
+    the two-waves-per-SIMD forward is selected (CFATTN_FWD_KERNEL=two) and dQ
+    recomputes the softmax.  Each tile computes the same sums either way: O,
+    lse, dQ, dK, dV must be bitwise equal."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    print(f"bf16 persistent vs unit grids, shape {shape}", flush=True)
+    _, (q, k, v, g) = _fast_inputs(shape, seed=2200)
+    if shape[4] == 128:
+        monkeypatch.setenv("CFATTN_FWD_KERNEL", "two")
+    out = {}
+    with _DsLimit(ctx, 0):
+        for grid in ("unit", "persistent"):
+            if grid == "unit":
+                monkeypatch.setenv("CFATTN_BF16_GRID", "unit")
+            else:
+                monkeypatch.delenv("CFATTN_BF16_GRID", raising=False)
+            o, lse = D.fwd(q, k, v, ctx=ctx)
+            out[grid] = [x.cpu().numpy() for x in (o, lse, *D.bwd(g, q, k, v, o, lse, ctx=ctx))]
+    torch.cuda.synchronize()
+    for name, a, b in zip(("o", "lse", "dq", "dk", "dv"), out["persistent"], out["unit"]):
+        assert np.array_equal(a, b), f"{shape} {name}: max diff {np.abs(a - b).max()}"
+
+
 @pytest.mark.parametrize("shape", [(8, 512, 9, 3, 64), (1, 2048, 4, 1, 128), (1, 1000, 8, 8, 64)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_f32_key_split_matches_oracle_and_unsplit(cf, shape):
