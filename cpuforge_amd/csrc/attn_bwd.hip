@@ -1352,7 +1352,13 @@ static hipError_t bwd_dp(const BwdParams& p, hipStream_t st, int kv_waves, int q
 }
 
 size_t attn_bwd_ds_bytes(Dtype dt, const Dims& d) {
-    if (dt == kF32) return attn_f32_scratch_bytes(d);
+    if (dt == kF32) {
+        // The slots, then (256-aligned) room for the stored dS; a caller
+        // whose limit does not hold that passes the slots alone
+        // (attn_f32_scratch_bytes) and dQ recomputes S and dP.
+        const size_t slots = attn_f32_scratch_bytes(d), ds = attn_f32_ds_bytes(d);
+        return slots && ds ? (slots + 255) / 256 * 256 + ds : slots;
+    }
     // head_dim 128 only: at 64 the recompute costs half the matrix work per
     // stored byte and measured faster than the dS round trip through HBM.
     if (dt != kBF16 || d.hd != 128 || d.batch <= 0 || d.seq <= 0) return 0;
@@ -1613,7 +1619,8 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        return launch_attn_bwd_f32(d, p, ds, tu.f32_persistent != 0, st, tu.timer);
+        return launch_attn_bwd_f32(d, p, ds, ds_bytes, tu.f32_persistent != 0, tu.f32_stored_ds != 0, st,
+                                   tu.timer);
     }
     const int q_waves = p.hpw * p.tpw;
     const int dp = d.hd <= 32 ? 32 : d.hd <= 64 ? 64 : d.hd <= 128 ? 128 : 256;

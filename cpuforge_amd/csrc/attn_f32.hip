@@ -85,12 +85,22 @@ __device__ __forceinline__ void f32_tile_dma(const float* __restrict__ g, long r
 template <int DP, int NW, int EXTRA = 0>
 __device__ __forceinline__ void f32_step_end(bool newer) {
     constexpr int kNewer = 2 * (32 * DP / 256) / NW + EXTRA;
+    static_assert(kNewer >= 0 && kNewer < 64, "vmcnt range");
     if (newer)
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(kNewer) : "memory");
     else
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+}
+
+// Stored fp32 dS block (32 queries x 32 keys): the value of query row q and
+// key column k sits where the dQ kernel's lane (q, (k >> 2) & 1) finds
+// operand j = 4 * (k >> 3) + (k & 3) (its key acc_row(j, hh) = k), chunk-
+// major so that each of the four 16-byte loads of a lane covers one
+// contiguous KiB: slot (j / 4) * 256 + lane * 4 + j % 4.
+__device__ __forceinline__ int f32_ds_slot(int q, int k) {
+    return (k >> 3) * 256 + (q + 32 * ((k >> 2) & 1)) * 4 + (k & 3);
 }
 
 // Query tile, key split and split count of work unit u of one (sequence, KV
@@ -455,6 +465,123 @@ attn_bwd_dq_f32_kernel(const BwdParams p) {
     dq_f32_unit<DP>(p, un, id / p.units_q, sK0, sK1, sK2, sV0, sV1, sV2);
 }
 
+// ------------------------------------------------------ dQ from stored dS
+// dQ^T += K^T dS^T with dS read from the blocks the dK/dV kernel stored
+// (p.ds32), no S / dP recompute: the dQ kernel's decomposition and product
+// order, so dQ is bitwise the recompute's.  Per 32-key tile the workgroup
+// loads the K tile (shared) and each wave its own dS block, both straight
+// into three-buffer LDS rings; every wave loads a block each step (past its
+// diagonal, or past the end, a valid block it does not use), so the per-wave
+// load count stays uniform for the exact waits.
+template <int DP>
+__device__ __forceinline__ void dq_f32_ds_unit(const BwdParams& p, const int tile, int rest, float* sK0, float* sK1,
+                                               float* sK2, float* sD0, float* sD1, float* sD2) {
+    constexpr int NW = 4, BN = 32, NDB = DP / 32;
+    constexpr int BPW = (32 * DP / 256) / NW;  // K tile loads per wave
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int wv = wave_uniform(wave);
+
+    const int TT = 32 * p.tpw;
+    const int sub = rest % p.n_sub;
+    rest /= p.n_sub;
+    const int g = rest % p.nkv;
+    const int b = rest / p.nkv;
+    const int head = g * p.group + sub * p.hpw + wave % p.hpw;
+    const int t_wave = tile * TT + (wave / p.hpw) * 32;
+    const int tq = t_wave + l32;
+    const int wg_end = min(p.seq, tile * TT + TT);
+    const int n_kt = (wg_end + BN - 1) / BN;
+    const bool wave_active = t_wave < p.seq;
+    const int wave_last = min(t_wave + 31, p.seq - 1);
+
+    const long qrs = (long)p.nh * DP, kvrs = (long)p.nkv * DP;
+    const float* kg = static_cast<const float*>(p.k) + (long)b * p.kv_bs + (long)g * DP;
+    // The wave's dS row of blocks: query block qi (clamped to the last one,
+    // whose blocks exist, for a wave past the end), key block kt at + kt.
+    const int qi = min(t_wave, p.seq - 1) >> 5;
+    const float* dsrow = p.ds32 + (((long)b * p.nh + head) * p.ds_ntri + (long)qi * (qi + 1) / 2) * 1024;
+
+    auto dma = [&](int kt, float* Kd, float* Dd) {
+        f32_tile_dma<DP, NW>(kg, kvrs, kt * BN, p.seq - 1, Kd, wv, lane);
+        const float* src = dsrow + (long)min(kt, qi) * 1024 + lane * 4;
+        float* dst = Dd + wv * 1024;
+#pragma unroll
+        for (int c = 0; c < 4; c++) lds_load16_asm(src + c * 256, dst + c * 256);
+    };
+    dma(0, sK0, sD0);
+
+    f32x16 acc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; i++) acc[i] = zero16();
+
+    auto step = [&](int kt, const float* Ks, const float* Ds, float* Kn, float* Dn) {
+        const bool ahead = kt + 2 < n_kt;
+        const int k0 = kt * BN;
+        if (ahead) dma(kt + 2, Kn, Dn);
+        if (wave_active && k0 <= wave_last) {
+            float ds[16];
+            const float* dsl = Ds + wv * 1024 + lane * 4;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float4 v = *reinterpret_cast<const float4*>(dsl + c * 256);
+                ds[4 * c] = v.x, ds[4 * c + 1] = v.y, ds[4 * c + 2] = v.z, ds[4 * c + 3] = v.w;
+            }
+#pragma unroll
+            for (int db = 0; db < NDB; db++)
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    acc[db] = mfma_f32(Ks[f32_at<DP>(acc_row(j, hh), db * 32 + l32)], ds[j], acc[db]);
+        }
+        f32_step_end<DP, NW, 4 - BPW>(ahead);  // tile kt + 1 and its dS blocks are in LDS
+    };
+
+    if (n_kt > 1) dma(1, sK1, sD1);
+    f32_step_end<DP, NW, 4 - BPW>(n_kt > 1);
+    for (int kt = 0; kt < n_kt; kt += 3) {
+        step(kt, sK0, sD0, sK2, sD2);
+        if (kt + 1 < n_kt) step(kt + 1, sK1, sD1, sK0, sD0);
+        if (kt + 2 < n_kt) step(kt + 2, sK2, sD2, sK1, sD1);
+    }
+    if (!wave_active || tq >= p.seq) return;
+    const long qoff = (long)b * p.q_bs + (long)tq * qrs + (long)head * DP;
+    float* row = p.dq + qoff;
+#pragma unroll
+    for (int db = 0; db < NDB; db++)
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+            float4* dst = reinterpret_cast<float4*>(row + db * 32 + rq * 8 + hh * 4);
+            float4 v = *dst;
+            v.x += acc[db][rq * 4] * p.scale;
+            v.y += acc[db][rq * 4 + 1] * p.scale;
+            v.z += acc[db][rq * 4 + 2] * p.scale;
+            v.w += acc[db][rq * 4 + 3] * p.scale;
+            *dst = v;
+        }
+}
+
+template <int DP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 64 ? 2 : 1, DP == 64 ? 2 : 1))) void
+attn_bwd_dq_f32_ds_kernel(const BwdParams p) {
+    constexpr int BN = 32;
+    __shared__ __attribute__((aligned(16))) float sK0[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sK1[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sK2[BN * DP];
+    __shared__ __attribute__((aligned(16))) float sD0[4 * 1024];
+    __shared__ __attribute__((aligned(16))) float sD1[4 * 1024];
+    __shared__ __attribute__((aligned(16))) float sD2[4 * 1024];
+    if (p.q_xcd_wgs > 0) {
+        int tile, grp;
+        for (int it = 0;
+             persistent_item(it, p.q_items / p.n_ttiles, p.n_ttiles, p.q_xcd_wgs, p.q_walk_gm, tile, grp); it++)
+            dq_f32_ds_unit<DP>(p, tile, grp, sK0, sK1, sK2, sD0, sD1, sD2);
+        return;
+    }
+    const int id = xcd_remap(blockIdx.x, p.n_wg_q, p.xcd);
+    dq_f32_ds_unit<DP>(p, p.n_ttiles - 1 - id % p.n_ttiles, id / p.n_ttiles, sK0, sK1, sK2, sD0, sD1, sD2);
+}
+
 // ------------------------------------------------------------------ dK/dV
 // Workgroup = (128-key tile, query head h, sequence, query split qs): four
 // waves of 32 keys share 32-query Q/dO tiles of head h; the workgroup visits
@@ -594,6 +721,15 @@ __device__ __forceinline__ void dkdv_f32_unit(const BwdParams& p, const F32DkdvA
                     pr[r] = pv;
                     ds[r] = pv * (dp[r] - dv[i]);
                 }
+            }
+            if (p.ds32) {
+                // dS block (query block q0 / 32, key block key0 / 32) for the
+                // stored-dS dQ kernel: the values it would recompute, bit for
+                // bit (the same S, dP, lse and delta arithmetic).
+                const int qi = q0 >> 5, ki = key0 >> 5;
+                float* blk = p.ds32 + (((long)b * p.nh + h) * p.ds_ntri + (long)qi * (qi + 1) / 2 + ki) * 1024;
+#pragma unroll
+                for (int r = 0; r < 16; r++) blk[f32_ds_slot(acc_row(r, hh), l32)] = ds[r];
             }
             // dV^T += dO^T P and dK^T += Q^T dS; product j pairs query
             // acc_row(j, hh) of both operands.
@@ -953,8 +1089,14 @@ hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t
 
 // dK/dV then dQ (delta is already computed); `scratch` holds
 // attn_f32_scratch_bytes(d) bytes.
-hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, bool persistent, hipStream_t st,
-                               KernelTimer* tm) {
+size_t attn_f32_ds_bytes(const Dims& d) {
+    if (!f32_fast_ok(d.hd) || d.batch <= 0 || d.seq <= 0 || d.nkv <= 0) return 0;
+    const size_t nqb = ((size_t)d.seq + 31) / 32;
+    return (size_t)d.batch * d.nh * (nqb * (nqb + 1) / 2) * 1024 * sizeof(float);
+}
+
+hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, size_t scratch_bytes, bool persistent,
+                               bool stored_ds, hipStream_t st, KernelTimer* tm) {
     F32DkdvArgs a;
     const F32KvPlan kp = f32_kv_plan(d);
     a.qs_n = kp.qs_max;
@@ -965,6 +1107,16 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, bool p
     const int slots = p.group * a.qs_n;
     a.slots = slots;
     p.n_kvtiles = (d.seq + 127) / 128;
+    // Stored dS: when the dQ grid runs unsplit and the scratch holds it past
+    // the slots (whose dQ-split reuse the unsplit grid does not need).
+    const F32Plan pl = f32_plan(d, p.group);
+    const size_t ds_off = (attn_f32_scratch_bytes(d) + 255) / 256 * 256, ds_need = attn_f32_ds_bytes(d);
+    p.ds32 = nullptr;
+    if (stored_ds && pl.ks == 0 && ds_need > 0 && scratch_bytes >= ds_off + ds_need) {
+        p.ds32 = reinterpret_cast<float*>(static_cast<char*>(scratch) + ds_off);
+        const long nqb = (d.seq + 31) / 32;
+        p.ds_ntri = nqb * (nqb + 1) / 2;
+    }
     const long nkv_wg = (long)kp.units * d.nh * d.batch;
     if (nkv_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;
     p.n_wg_kv = (int)nkv_wg;
@@ -1002,7 +1154,6 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, bool p
         e = hipGetLastError();
     }
     if (e != hipSuccess) return e;
-    const F32Plan pl = f32_plan(d, p.group);
     p.hpw = pl.hpw;
     p.tpw = pl.tpw;
     p.n_sub = pl.n_sub;
@@ -1023,7 +1174,11 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, bool p
         p.q_walk_gm = f32_walk_order(d, pl, p.q_items, p.q_xcd_wgs);
     }
     TimedLaunch tl(tm, kKernBwdDq, st);
-    if (d.hd == 128)
+    if (p.ds32 && d.hd == 128)
+        hipLaunchKernelGGL(attn_bwd_dq_f32_ds_kernel<128>, dim3(p.n_wg_q), dim3(256), 0, st, p);
+    else if (p.ds32)
+        hipLaunchKernelGGL(attn_bwd_dq_f32_ds_kernel<64>, dim3(p.n_wg_q), dim3(256), 0, st, p);
+    else if (d.hd == 128)
         hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<128>, dim3(p.n_wg_q), dim3(256), 0, st, p);
     else
         hipLaunchKernelGGL(attn_bwd_dq_f32_kernel<64>, dim3(p.n_wg_q), dim3(256), 0, st, p);

@@ -74,6 +74,11 @@ struct BwdParams {
     // query tiles, q_xcd_wgs workgroups per XCD (0: one unit per workgroup),
     // q_walk_gm the walk order (persistent_item).
     int q_items, q_xcd_wgs, q_walk_gm;
+    // Stored fp32 dS (fp32 fast path, null otherwise): per (sequence, query
+    // head), the 32x32 blocks (query block qi, key block ki <= qi) of the
+    // causal triangle, block qi*(qi+1)/2 + ki, ds_ntri blocks each, 1024
+    // floats per block in the dQ kernel's operand order (f32_ds_slot).
+    float* ds32;
     // Epilogue of the fast bf16 kernels' dQ and dK rows (BwdEpilogue).
     int epi;
     const float* rope_cos;
@@ -102,8 +107,13 @@ size_t attn_f32_scratch_bytes(const Dims& d);
 size_t attn_f32_fwd_scratch_bytes(const Dims& d);
 hipError_t launch_attn_fwd_f32(const Dims& d, FwdParams p, void* scratch, size_t scratch_bytes, bool persistent,
                                hipStream_t st, KernelTimer* tm);
-hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, bool persistent, hipStream_t st,
-                               KernelTimer* tm);
+// fp32 backward; `scratch` holds scratch_bytes >= attn_f32_scratch_bytes(d):
+// with attn_f32_ds_bytes(d) more (after the first attn_f32_scratch_bytes(d)
+// rounded up to 256) and `stored_ds`, dK/dV stores dS for the dQ kernel.
+hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, size_t scratch_bytes, bool persistent,
+                               bool stored_ds, hipStream_t st, KernelTimer* tm);
+// Bytes of the stored fp32 dS (0 where the fp32 fast path does not apply).
+size_t attn_f32_ds_bytes(const Dims& d);
 // bf16 dK/dV at head_dim 128, one wave per SIMD (attn_dkdv.hip); with
 // `wds` it also stores dS for the stored-dS dQ kernel.  p.kv_tile is 128.
 void launch_attn_bwd_dkdv_k64(const BwdParams& p, bool wds, hipStream_t st);

@@ -30,6 +30,8 @@ using cfattn::Dtype;
 // allocation fails.  Never an error: the recompute path needs no scratch.
 void* ds_scratch(cfattn_ctx* c, Dtype dt, const Dims& d, size_t* bytes) {
     *bytes = cfattn::attn_bwd_ds_bytes(dt, d);
+    // fp32: the slots alone when the stored dS does not fit under the limit.
+    if (dt == cfattn::kF32 && *bytes > c->ds_limit) *bytes = cfattn::attn_f32_scratch_bytes(d);
     if (*bytes == 0 || *bytes > c->ds_limit) {
         *bytes = 0;
         return nullptr;

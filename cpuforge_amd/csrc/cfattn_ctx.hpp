@@ -166,6 +166,10 @@ struct cfattn_ctx {
         // comparison and measurement).
         const char* g = std::getenv("CFATTN_F32_GRID");
         if (g && std::strcmp(g, "unit") == 0) t.f32_persistent = 0;
+        // CFATTN_F32_DS=0: the fp32 dQ recomputes S and dP instead of reading
+        // the dS that dK/dV stored (same bits; kept for comparison).
+        const char* fd = std::getenv("CFATTN_F32_DS");
+        if (fd && std::strcmp(fd, "0") == 0) t.f32_stored_ds = 0;
         // CFATTN_BF16_GRID=unit: the same for the bf16 two-waves-per-SIMD
         // kernels.
         const char* h = std::getenv("CFATTN_BF16_GRID");

@@ -85,6 +85,9 @@ struct Tuning {
     // fp32 kernels: persistent grids (0: one workgroup per work unit; the
     // same bits either way).
     int f32_persistent = 1;
+    // fp32 backward: dK/dV stores dS and dQ reads it when the scratch holds
+    // it (0: dQ recomputes S and dP; the same bits either way).
+    int f32_stored_ds = 1;
     // bf16 two-waves-per-SIMD kernels (forward, recompute dQ, wave-
     // specialised dK/dV): persistent grids (0: one workgroup per unit).
     int bf16_persistent = 1;
@@ -125,8 +128,12 @@ hipError_t launch_attn_fwd(Dtype dt, const Dims& d, const void* q, const void* k
 // the dK/dV kernel writes dS (bf16, causal blocks only) and dQ is one
 // product over it instead of a second softmax recompute.  Otherwise dQ
 // recomputes S and dP.  Both paths give the same result up to bf16
-// rounding of dS, which both apply.
+// rounding of dS, which both apply.  In fp32 the same scratch first holds
+// the dK/dV slots (attn_f32_scratch_bytes, the least the fast fp32 path
+// takes), then the stored fp32 dS, with which dQ reads dS instead of
+// recomputing it (the same bits).
 size_t attn_bwd_ds_bytes(Dtype dt, const Dims& d);
+size_t attn_f32_scratch_bytes(const Dims& d);
 // How the fast bf16 kernels write the dQ and dK rows (dV rows are always
 // added).  The inverse-RoPE modes fold the prologue backward's rotation
 // (RopeCache::apply with inverse = true, rope.rs:71-89) into the kernels:

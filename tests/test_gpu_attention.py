@@ -500,6 +500,35 @@ def test_f32_persistent_grids_match_unit_grids(cf, shape, monkeypatch):
         assert np.array_equal(a, b), f"{shape} {name}: max diff {np.abs(a - b).max()}"
 
 
+@pytest.mark.parametrize("grid", ["persistent", "unit"])
+@pytest.mark.parametrize("shape", [(8, 2048, 9, 3, 64), (4, 1500, 16, 4, 64), (8, 1024, 8, 2, 128),
+                                   (8, 777, 12, 3, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_f32_stored_ds_matches_recompute(cf, shape, grid, monkeypatch):
+    """fp32 backward: dK/dV stores dS (fp32 blocks) and dQ reads it instead
+    of recomputing S and dP (CFATTN_F32_DS=0).  dK/dV forms dS with the same
+    arithmetic as the recompute and dQ sums it in the same order, so dQ, dK
+    and dV must be bitwise equal, on persistent and per-unit grids."""
+    import torch
+    from cpuforge_amd import device as D
+    mod, ctx = cf
+    print(f"f32 stored dS vs recompute, shape {shape}, {grid} grids", flush=True)
+    _, (q, k, v, g) = _fast_inputs(shape, seed=2300, mode="f32")
+    if grid == "unit":
+        monkeypatch.setenv("CFATTN_F32_GRID", "unit")
+    o, lse = D.fwd(q, k, v, ctx=ctx)
+    out = {}
+    for ds in ("recompute", "stored"):
+        if ds == "recompute":
+            monkeypatch.setenv("CFATTN_F32_DS", "0")
+        else:
+            monkeypatch.delenv("CFATTN_F32_DS", raising=False)
+        out[ds] = [x.cpu().numpy() for x in D.bwd(g, q, k, v, o, lse, ctx=ctx)]
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv"), out["stored"], out["recompute"]):
+        assert np.array_equal(a, b), f"{shape} {grid} {name}: max diff {np.abs(a - b).max()}"
+
+
 @pytest.mark.parametrize("shape", [(8, 2048, 9, 3, 64), (4, 1500, 16, 4, 64), (1, 4096, 32, 8, 64),
                                    (4, 1000, 16, 8, 128)],
                          ids=lambda s: "x".join(map(str, s)))
