@@ -1107,15 +1107,19 @@ hipError_t launch_attn_bwd_f32(const Dims& d, BwdParams p, void* scratch, size_t
     const int slots = p.group * a.qs_n;
     a.slots = slots;
     p.n_kvtiles = (d.seq + 127) / 128;
-    // Stored dS: when the dQ grid runs unsplit and the scratch holds it past
-    // the slots (whose dQ-split reuse the unsplit grid does not need).
-    const F32Plan pl = f32_plan(d, p.group);
+    // Stored dS when the scratch holds it past the slots.  Its dQ grid runs
+    // unsplit: one product per key tile makes even the longest query tile of
+    // a small grid short (the split, with its partials and merge, is for the
+    // recompute's three).
+    F32Plan pl = f32_plan(d, p.group);
     const size_t ds_off = (attn_f32_scratch_bytes(d) + 255) / 256 * 256, ds_need = attn_f32_ds_bytes(d);
     p.ds32 = nullptr;
-    if (stored_ds && pl.ks == 0 && ds_need > 0 && scratch_bytes >= ds_off + ds_need) {
+    if (stored_ds && ds_need > 0 && scratch_bytes >= ds_off + ds_need) {
         p.ds32 = reinterpret_cast<float*>(static_cast<char*>(scratch) + ds_off);
         const long nqb = (d.seq + 31) / 32;
         p.ds_ntri = nqb * (nqb + 1) / 2;
+        pl.ks = 0;
+        pl.units = pl.n_ttiles;
     }
     const long nkv_wg = (long)kp.units * d.nh * d.batch;
     if (nkv_wg > 0x7fffffffL) return hipErrorInvalidConfiguration;

@@ -502,13 +502,16 @@ def test_f32_persistent_grids_match_unit_grids(cf, shape, monkeypatch):
 
 @pytest.mark.parametrize("grid", ["persistent", "unit"])
 @pytest.mark.parametrize("shape", [(8, 2048, 9, 3, 64), (4, 1500, 16, 4, 64), (8, 1024, 8, 2, 128),
-                                   (8, 777, 12, 3, 64)],
+                                   (8, 777, 12, 3, 64), (8, 512, 9, 3, 64), (3, 300, 8, 2, 128)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_f32_stored_ds_matches_recompute(cf, shape, grid, monkeypatch):
     """fp32 backward: dK/dV stores dS (fp32 blocks) and dQ reads it instead
     of recomputing S and dP (CFATTN_F32_DS=0).  dK/dV forms dS with the same
     arithmetic as the recompute and dQ sums it in the same order, so dQ, dK
-    and dV must be bitwise equal, on persistent and per-unit grids."""
+    and dV must be bitwise equal, on persistent and per-unit grids; where the
+    recompute's grid splits a query tile's keys (the last two shapes: its
+    partial sums are added in split order), dQ agrees to 1e-5, as the split
+    does with the unsplit grid."""
     import torch
     from cpuforge_amd import device as D
     mod, ctx = cf
@@ -525,8 +528,12 @@ def test_f32_stored_ds_matches_recompute(cf, shape, grid, monkeypatch):
             monkeypatch.delenv("CFATTN_F32_DS", raising=False)
         out[ds] = [x.cpu().numpy() for x in D.bwd(g, q, k, v, o, lse, ctx=ctx)]
     torch.cuda.synchronize()
+    split = shape in ((8, 512, 9, 3, 64), (3, 300, 8, 2, 128))
     for name, a, b in zip(("dq", "dk", "dv"), out["stored"], out["recompute"]):
-        assert np.array_equal(a, b), f"{shape} {grid} {name}: max diff {np.abs(a - b).max()}"
+        if split and name == "dq":
+            assert max_abs(a.reshape(-1), b.reshape(-1)) <= 1e-5, f"{shape} {grid} dq"
+        else:
+            assert np.array_equal(a, b), f"{shape} {grid} {name}: max diff {np.abs(a - b).max()}"
 
 
 @pytest.mark.parametrize("shape", [(8, 2048, 9, 3, 64), (4, 1500, 16, 4, 64), (1, 4096, 32, 8, 64),
