@@ -899,9 +899,14 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dq_ds_kernel(const BwdParams
 // kDsBlock.
 // The NORM instance runs the kEpiUnrotNorm epilogue for the dK rows, the
 // other one every other mode.
+// One key tile (kvt) of group rest = sequence * nkv + KV head, walking its
+// query tiles down or up.  Without NORM no LDS read follows the last step's
+// barrier, so the next tile of a persistent workgroup may load into the
+// buffers.
 template <int DP, int BM, bool WDS, bool NORM>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dkdv_ws_kernel(
-    const BwdParams p) {
+__device__ __forceinline__ void dkdv_ws_unit(const BwdParams& p, const int kvt, const int rest, const bool down,
+                                             bf16_bits* sQ0, bf16_bits* sQ1, bf16_bits* sO0, bf16_bits* sO1,
+                                             float (*sL)[BM], float (*sD)[BM], uint4 (*sPb)[BM / 32][2][64]) {
     constexpr int NT = 512;
     constexpr int CPR = DP / 8;
     using L = BlkTile<DP, BM>;
@@ -912,16 +917,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     static_assert(L::NB % 4 == 0 && 2 * BM <= NT / 2, "tile must split evenly over the four dS waves");
     static_assert(BM % 32 == 0, "query tile must be whole 32-row blocks");
     constexpr int HALF = DP / 2, NKD = HALF / 8, NDB = DP / 32, NQB = BM / 32;
-    // Query tiles: MFMA row i of block qb is query q0 + 32*qb + qperm(i).
-    __shared__ __attribute__((aligned(16))) bf16_bits sQ0[L::SIZE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sQ1[L::SIZE];
-    __shared__ __attribute__((aligned(16))) bf16_bits sO0[L::SIZE];  // dO rows
-    __shared__ __attribute__((aligned(16))) bf16_bits sO1[L::SIZE];
-    __shared__ __attribute__((aligned(16))) float sL[2][BM];  // lse * log2(e), by MFMA row
-    __shared__ __attribute__((aligned(16))) float sD[2][BM];  // delta, by MFMA row
-    // P of each (key slice, query block) as the P waves' bf16 MFMA operands:
-    // lane l's eight values of row groups 2h and 2h + 1 (h = 0, 1).
-    __shared__ uint4 sPb[4][NQB][2][64];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -929,9 +924,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const bool pwave = wave < 4;
     const int l32 = lane & 31, hh = lane >> 5;
 
-    const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
-    const int kvt = id % p.n_kvtiles;  // low key tiles see the most queries: first
-    const int rest = id / p.n_kvtiles;
     const int g = rest % p.nkv;
     const int b = rest / p.nkv;
     const int wg_key0 = kvt * p.kv_tile;
@@ -965,7 +957,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // n_qt - 1 - s / group (walking down) or qt_begin + s / group (walking
     // up): the order of attn_bwd_dkdv_k64_kernel, whose sums this kernel
     // reproduces bit for bit.
-    const bool down = dkdv_walks_down(blockIdx.x, p.xcd_cus);
     auto step_q0 = [&](int s) { return (down ? n_qt - 1 - s / p.group : qt_begin + s / p.group) * BM; };
     auto step_h = [&](int s) { return g * p.group + s % p.group; };
 
@@ -1322,6 +1313,43 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         run(RoleTag<false>{});
 }
 
+template <int DP, int BM, bool WDS, bool NORM>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_bwd_dkdv_ws_kernel(
+    const BwdParams p) {
+    using L = BlkTile<DP, BM>;
+    constexpr int NQB = BM / 32;
+    // Query tiles: MFMA row i of block qb is query q0 + 32*qb + qperm(i).
+    __shared__ __attribute__((aligned(16))) bf16_bits sQ0[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sQ1[L::SIZE];
+    __shared__ __attribute__((aligned(16))) bf16_bits sO0[L::SIZE];  // dO rows
+    __shared__ __attribute__((aligned(16))) bf16_bits sO1[L::SIZE];
+    __shared__ __attribute__((aligned(16))) float sL[2][BM];  // lse * log2(e), by MFMA row
+    __shared__ __attribute__((aligned(16))) float sD[2][BM];  // delta, by MFMA row
+    // P of each (key slice, query block) as the P waves' bf16 MFMA operands:
+    // lane l's eight values of row groups 2h and 2h + 1 (h = 0, 1).
+    __shared__ uint4 sPb[4][NQB][2][64];
+    if constexpr (!NORM && !WDS && DP == 64) {
+        // Persistent grid (head_dim 64): key tile kvt of group grp is unit id
+        // grp * n_kvtiles + kvt of the one-workgroup-per-tile grid, and walks
+        // the way that grid's workgroup for it does (the same sums).
+        if (p.kv_xcd_wgs > 0) {
+            int unit, grp;
+            for (int it = 0;
+                 persistent_item(it, p.kv_items / p.n_kvtiles, p.n_kvtiles, p.kv_xcd_wgs, p.kv_walk_gm, unit, grp);
+                 it++) {
+                const int kvt = p.n_kvtiles - 1 - unit;
+                const int id = grp * p.n_kvtiles + kvt;
+                const bool down = ((xcd_local(id, p.kv_items) / p.xcd_cus) & 1) == 0;
+                dkdv_ws_unit<DP, BM, WDS, NORM>(p, kvt, grp, down, sQ0, sQ1, sO0, sO1, sL, sD, sPb);
+            }
+            return;
+        }
+    }
+    const int id = xcd_remap(blockIdx.x, p.n_wg_kv, p.xcd);
+    dkdv_ws_unit<DP, BM, WDS, NORM>(p, id % p.n_kvtiles, id / p.n_kvtiles, dkdv_walks_down(blockIdx.x, p.xcd_cus),
+                                    sQ0, sQ1, sO0, sO1, sL, sD, sPb);  // low key tiles (the most queries) first
+}
+
 static int pick_hpw_b(int group, int cap) {
     for (int h = cap < group ? cap : group; h >= 1; h--)
         if (group % h == 0) return h;
@@ -1550,6 +1578,23 @@ hipError_t launch_attn_bwd(Dtype dt, const Dims& d, const void* d_o, const void*
                 else
                     hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<128, 64, false, false>), g, blk, 0, st, p);
             } else {
+                // Persistent grid (one workgroup per CU) at head_dim 64 when
+                // the key tiles fill every CU, up to two per CU, with a group
+                // per XCD; not with the norm epilogue (its gain partials are
+                // per workgroup).  (C2, 1.5 tiles per CU: 0.170 -> 0.150 ms;
+                // C3, 4 per CU: 0.752 -> 0.765 ms, so it keeps the per-tile
+                // grid.)
+                p.kv_items = p.n_wg_kv;
+                p.kv_xcd_wgs = 0;
+                const int cus = 8 * p.xcd_cus;
+                if (mode_k != kEpiUnrotNorm && tu.bf16_persistent && p.xcd && cus % 8 == 0 &&
+                    (long)d.nkv * d.batch >= 8 && p.n_wg_kv >= cus && p.n_wg_kv <= 2L * cus) {
+                    p.kv_xcd_wgs = p.xcd_cus;
+                    p.n_wg_kv = cus;
+                    const int n_qt = (d.seq + 127) / 128, nkvt = p.n_kvtiles;
+                    p.kv_walk_gm = persistent_group_major(p.kv_items / nkvt, nkvt, p.kv_xcd_wgs,
+                                                          [&](int u) { return (long)(n_qt - (nkvt - 1 - u)); });
+                }
                 const dim3 g(p.n_wg_kv), blk(512);
                 if (mode_k == kEpiUnrotNorm)
                     hipLaunchKernelGGL((attn_bwd_dkdv_ws_kernel<64, 128, false, true>), g, blk, 0, st, p);

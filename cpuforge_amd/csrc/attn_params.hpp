@@ -74,6 +74,10 @@ struct BwdParams {
     // query tiles, q_xcd_wgs workgroups per XCD (0: one unit per workgroup),
     // q_walk_gm the walk order (persistent_item).
     int q_items, q_xcd_wgs, q_walk_gm;
+    // Persistent wave-specialised dK/dV grid (head_dim 64): kv_items key
+    // tiles, kv_xcd_wgs workgroups per XCD (0: one unit per workgroup),
+    // kv_walk_gm the walk order (persistent_item).
+    int kv_items, kv_xcd_wgs, kv_walk_gm;
     // Stored fp32 dS (fp32 fast path, null otherwise): per (sequence, query
     // head), the 32x32 blocks (query block qi, key block ki <= qi) of the
     // causal triangle, block qi*(qi+1)/2 + ki, ds_ntri blocks each, 1024

@@ -138,6 +138,13 @@ __device__ __forceinline__ int xcd_remap(int hw_id, int n, int enable) {
     return start + local;
 }
 
+// Position of logical id `id` within its XCD's run under xcd_remap (n ids,
+// remapping on, n >= 8): the workgroup that runs it is local * 8 + its XCD.
+__device__ __forceinline__ int xcd_local(int id, int n) {
+    const int q = n / 8, r = n % 8;
+    return id < r * (q + 1) ? id % (q + 1) : (id - r * (q + 1)) % q;
+}
+
 // Work unit `it` of a workgroup of a persistent grid (8 * W workgroups) over
 // n_groups groups of n_units units each, unit n_units - 1 the longest (a
 // query tile, or a key tile counted from the end): the XCD of workgroup w

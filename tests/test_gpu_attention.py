@@ -542,7 +542,9 @@ def test_f32_stored_ds_matches_recompute(cf, shape, grid, monkeypatch):
 def test_bf16_persistent_grids_match_unit_grids(cf, shape, monkeypatch):
     """The bf16 two-waves-per-SIMD forward and the recompute dQ kernel run
     persistent grids where the tiles fill every workgroup slot, up to four per
-    slot (walked tile-major at 8x2048, group-major at 1x4096);
+    slot (walked tile-major at 8x2048, group-major at 1x4096), and the head_dim-
+    64 wave-specialised dK/dV up to two key tiles per CU (8x2048, 1x4096; its
+    persistent workgroups walk each key tile the way the per-tile grid does);
     CFATTN_BF16_GRID=unit launches one workgroup per tile.  At head_dim 128
     the two-waves-per-SIMD forward is selected (CFATTN_FWD_KERNEL=two) and dQ
     recomputes the softmax.  Each tile computes the same sums either way: O,
