@@ -725,11 +725,13 @@ __device__ __forceinline__ void dkdv_f32_unit(const BwdParams& p, const F32DkdvA
             if (p.ds32) {
                 // dS block (query block q0 / 32, key block key0 / 32) for the
                 // stored-dS dQ kernel: the values it would recompute, bit for
-                // bit (the same S, dP, lse and delta arithmetic).
+                // bit (the same S, dP, lse and delta arithmetic).  Non-
+                // temporal: read once, by the dQ kernel.  (Issued after the
+                // step's barrier instead, the values held across it spill.)
                 const int qi = q0 >> 5, ki = key0 >> 5;
                 float* blk = p.ds32 + (((long)b * p.nh + h) * p.ds_ntri + (long)qi * (qi + 1) / 2 + ki) * 1024;
 #pragma unroll
-                for (int r = 0; r < 16; r++) blk[f32_ds_slot(acc_row(r, hh), l32)] = ds[r];
+                for (int r = 0; r < 16; r++) __builtin_nontemporal_store(ds[r], blk + f32_ds_slot(acc_row(r, hh), l32));
             }
             // dV^T += dO^T P and dK^T += Q^T dS; product j pairs query
             // acc_row(j, hh) of both operands.
