@@ -10,9 +10,9 @@
 //   - a "column" operand (V^T for O^T += V^T P^T, K^T for dQ, dO^T and Q^T for
 //     dK/dV) is one head dim per lane of one row per half-wave, a ds_read_b32.
 // Tiles go straight from global memory into LDS (global_load_lds, 16 bytes a
-// lane), one tile ahead of the compute; 16-byte chunk c of tile row r sits at
-// chunk slot c ^ swz(r) of its row, so both read shapes are bank-conflict-free
-// (see f32_swz).  The per-query softmax follows the bf16 kernels: the running
+// lane) through three-buffer rings, two tiles ahead of the compute; 16-byte
+// chunk c of tile row r sits at chunk slot c ^ swz(r) of its row, so both
+// read shapes are bank-conflict-free (see f32_swz).  The per-query softmax follows the bf16 kernels: the running
 // max moves lazily, P is formed in the exp2 domain, and the MFMA k-index of
 // every P/dS product is chosen so the accumulator registers of one product are
 // the operands of the next.
@@ -22,7 +22,14 @@
 // serial chain of a workgroup is one head's query tiles, not the whole
 // group's.  Each workgroup writes its dK/dV contribution to a scratch slot;
 // attn_f32_reduce_kernel adds the slots of a KV head in a fixed order (query
-// head, then query split), so results are reproducible bit for bit.
+// head, then query split), so results are reproducible bit for bit.  Where the
+// scratch holds it, dK/dV also stores dS and dQ is one product per key tile
+// over it (attn_bwd_dq_f32_ds_kernel), bit for bit the recompute's dQ.
+//
+// Grids: where the work units fill every workgroup slot, a persistent grid
+// whose workgroups walk their XCD's units (persistent_item); else one
+// workgroup per unit, with small grids' key (forward, dQ) or query (dK/dV)
+// ranges split for balance.
 #include <algorithm>
 #include <vector>
 
