@@ -97,7 +97,7 @@ def parse():
                          "the wave-tiles whose row-sum guard settles); prints its own JSON line")
     ap.add_argument("--power", type=float, default=0.0, metavar="SECONDS",
                     help="board power and GFX clocks (amd-smi) while the --config forward, backward and whole step "
-                         "(bf16) each run back to back for SECONDS; prints its own JSON line")
+                         "(--mode, bf16 by default) each run back to back for SECONDS; prints its own JSON line")
     ap.add_argument("--zero-inputs", action="store_true",
                     help="diagnostic: q, k, v, dO all zero (the same kernels and instructions with the least bit "
                          "activity, to show what the board's power limit costs); not a benchmark figure")
@@ -465,13 +465,14 @@ def energy_probes(a):
                       "classes": out}), flush=True)
 
 
-def power_clock(a):
+def power_clock(a, mode="bf16"):
     """Board power (SOCKET_POWER) and the GFX clocks of the 8 XCDs, read with
-    amd-smi every ~0.1 s while the bf16 forward, backward or whole step of
-    config a.config (C5 by default; q, k, v, dO drawn from N(0,1), no RoPE)
-    runs back to back for a.power seconds each.  Samples from the first 0.5 s
-    of each run (the clock settling) are dropped.  Reports per phase the
-    median power, median XCD clock and the kernels' mean time."""
+    amd-smi every ~0.1 s while the forward, backward or whole step of config
+    a.config (C5 by default; q, k, v, dO drawn from N(0,1), no RoPE) in
+    `mode` (bf16 or f32) runs back to back for a.power seconds each.  Samples
+    from the first 0.5 s of each run (the clock settling) are dropped.
+    Reports per phase the median power, median XCD clock and the kernels'
+    mean time."""
     import re
     import shutil
     import subprocess
@@ -486,10 +487,11 @@ def power_clock(a):
     ctx = cf.Context(0)
     g = torch.Generator(device="cuda")
     g.manual_seed(1234)
-    q = torch.randn(B, S, Hq, D, device="cuda", generator=g).to(torch.bfloat16)
-    k = torch.randn(B, S, Hk, D, device="cuda", generator=g).to(torch.bfloat16)
-    v = torch.randn(B, S, Hk, D, device="cuda", generator=g).to(torch.bfloat16)
-    d_o = torch.randn(B, S, Hq, D, device="cuda", generator=g).to(torch.bfloat16)
+    tdt = torch.bfloat16 if mode == "bf16" else torch.float32
+    q = torch.randn(B, S, Hq, D, device="cuda", generator=g).to(tdt)
+    k = torch.randn(B, S, Hk, D, device="cuda", generator=g).to(tdt)
+    v = torch.randn(B, S, Hk, D, device="cuda", generator=g).to(tdt)
+    d_o = torch.randn(B, S, Hq, D, device="cuda", generator=g).to(tdt)
     o, lse = torch.empty(B, S, Hq, D, device="cuda"), torch.empty(B, Hq, S, device="cuda")
     dq, dk, dv = torch.zeros_like(o), torch.zeros(B, S, Hk, D, device="cuda"), torch.zeros(B, S, Hk, D, device="cuda")
     dev.fwd(q, k, v, o, lse, ctx=ctx)
@@ -531,9 +533,9 @@ def power_clock(a):
                      "gfx_clock_mhz_range": [cs[0], cs[-1]] if cs else None}
         print(f"bench: power {name}: {out[name]}", file=sys.stderr, flush=True)
     ctx.close()
-    print(json.dumps({"metric": f"board power and GFX clock under the {a.config} bf16 kernels (amd-smi)",
+    print(json.dumps({"metric": f"board power and GFX clock under the {a.config} {mode} kernels (amd-smi)",
                       "value": out["step"]["power_w_median"], "unit": "W", "higher_is_better": False,
-                      "dtype": "bf16", "seconds_per_phase": a.power,
+                      "dtype": mode, "seconds_per_phase": a.power,
                       "config": {"workload": WORKLOAD[a.config], "config": a.config},
                       "data": "synthetic (torch.randn, seed 1234)", "phases": out}), flush=True)
 
@@ -1040,7 +1042,7 @@ def main():
         fwd_distributions(a)
         return
     if a.power > 0:
-        power_clock(a)
+        power_clock(a, mode)
         return
     if a.sweep:
         shape_sweep(a)
