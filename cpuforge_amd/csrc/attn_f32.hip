@@ -206,14 +206,21 @@ __device__ __forceinline__ void fwd_f32_unit(const FwdParams& p, const F32Unit u
             // S^T: rows = keys k0 + [0, 32), columns = this wave's queries.
             // The loads two tiles ahead issue behind the first MFMAs, whose
             // shadow covers their address arithmetic.
+            // Each group's K row operands are read before the previous
+            // group's MFMAs issue (pinned: the compiler otherwise reads them
+            // after, and the products wait for the read).
             f32x16 sc = zero16();
+            float4 an = *reinterpret_cast<const float4*>(Ks + f32_at<DP>(l32, hh * HALF));
 #pragma unroll
             for (int c = 0; c < HALF / 4; c++) {
-                const float4 a = *reinterpret_cast<const float4*>(Ks + f32_at<DP>(l32, hh * HALF + 4 * c));
+                const float4 a = an;
+                if (c + 1 < HALF / 4) an = *reinterpret_cast<const float4*>(Ks + f32_at<DP>(l32, hh * HALF + 4 * c + 4));
+                __builtin_amdgcn_sched_barrier(0);
                 sc = mfma_f32(a.x, qf[4 * c], sc);
                 sc = mfma_f32(a.y, qf[4 * c + 1], sc);
                 sc = mfma_f32(a.z, qf[4 * c + 2], sc);
                 sc = mfma_f32(a.w, qf[4 * c + 3], sc);
+                __builtin_amdgcn_sched_barrier(0);
                 if (c == 0 && ahead) dma(kt + 2, Kn, Vn);
             }
             float mx = -INFINITY;
@@ -694,11 +701,18 @@ __device__ __forceinline__ void dkdv_f32_unit(const BwdParams& p, const F32DkdvA
         const int q0 = step_q0(s);
         if (wave_active && q0 + BM - 1 >= key0 && q0 < p.seq) {
             // S and dP: rows = queries q0 + [0, 32), columns = this wave's keys.
+            // Q / dO row operands read a group ahead, as the forward's K rows.
             f32x16 sc = zero16(), dp = zero16();
+            float4 xn = *reinterpret_cast<const float4*>(Qs + f32_at<DP>(l32, hh * HALF));
+            float4 yn = *reinterpret_cast<const float4*>(Os + f32_at<DP>(l32, hh * HALF));
 #pragma unroll
             for (int c = 0; c < HALF / 4; c++) {
-                const float4 x = *reinterpret_cast<const float4*>(Qs + f32_at<DP>(l32, hh * HALF + 4 * c));
-                const float4 y = *reinterpret_cast<const float4*>(Os + f32_at<DP>(l32, hh * HALF + 4 * c));
+                const float4 x = xn, y = yn;
+                if (c + 1 < HALF / 4) {
+                    xn = *reinterpret_cast<const float4*>(Qs + f32_at<DP>(l32, hh * HALF + 4 * c + 4));
+                    yn = *reinterpret_cast<const float4*>(Os + f32_at<DP>(l32, hh * HALF + 4 * c + 4));
+                }
+                __builtin_amdgcn_sched_barrier(0);
                 sc = mfma_f32(x.x, kf[4 * c], sc);
                 dp = mfma_f32(y.x, vf[4 * c], dp);
                 sc = mfma_f32(x.y, kf[4 * c + 1], sc);
@@ -707,6 +721,7 @@ __device__ __forceinline__ void dkdv_f32_unit(const BwdParams& p, const F32DkdvA
                 dp = mfma_f32(y.z, vf[4 * c + 2], dp);
                 sc = mfma_f32(x.w, kf[4 * c + 3], sc);
                 dp = mfma_f32(y.w, vf[4 * c + 3], dp);
+                __builtin_amdgcn_sched_barrier(0);
                 if (c == 0 && ahead) dma(s + 2, Qn, On, LDn);  // behind the first MFMAs, as the forward
             }
             // Masked: the diagonal steps and the one past the sequence end
