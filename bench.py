@@ -636,15 +636,10 @@ def fused_timing(cfg, mode, steps, warmup):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    # Per-kernel times over `steps` untimed steps; the timed steps bracket
-    # the dK/dV kernel only, as the attention step's timing does.
-    ctx.profile_select(None)
-    ctx.profile_enable(True)
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    kernels = {n: round(ms / max(1, c), 4) for n, (ms, c) in ctx.profile_read().items() if c}
-    ctx.profile_enable(False)
+    # Per-kernel times over untimed steps, each kernel bracketed alone; the
+    # timed steps bracket the dK/dV kernel only, as the attention step's
+    # timing does.
+    kernels = {n: round(ms, 4) for n, (ms, _) in kernel_times(ctx, step, steps).items()}
     ctx.profile_select(["attn_bwd_dkdv"])
     ctx.profile_enable(True)
     t0 = time.perf_counter()
@@ -914,6 +909,41 @@ def io_formats(a):
                       "io": out, "cpu_baseline": cpu or None}), flush=True)
 
 
+def kernel_times(ctx, step, steps, dominant=False):
+    """{kernel: (ms per launch, launches)} from the library's hipEvents.  A
+    pass with every launch bracketed names the kernels; each bracket adds
+    queue time around its kernel, so each kernel is then timed in a pass of
+    `steps` steps of its own in which only it is bracketed.  With `dominant`
+    the kernel of the most time (among ALGO_UNITS) keeps the first pass's
+    figure: the caller times it in its timed steps."""
+    import torch
+
+    ctx.profile_select(None)
+    ctx.profile_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    every = {n: (t / c, c) for n, (t, c) in ctx.profile_read().items() if c}
+    ctx.profile_enable(False)
+    skip = None
+    if dominant:
+        skip = max((n for n in every if n in ALGO_UNITS), key=lambda n: every[n][0] * every[n][1])
+    for n in list(every):
+        if n == skip:
+            continue
+        ctx.profile_select([n])
+        ctx.profile_enable(True)
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        t, c = ctx.profile_read().get(n, (0.0, 0))
+        ctx.profile_enable(False)
+        if c:
+            every[n] = (t / c, c)
+    ctx.profile_select(None)
+    return every
+
+
 def attn_timing(cfg, mode, steps, warmup, ctx, traffic_file, copy_probe, zero_inputs=False):
     """Times `steps` attention steps (cfattn_fwd then cfattn_bwd on
     device-resident tensors) of config `cfg` after `warmup` untimed ones.
@@ -966,17 +996,9 @@ def attn_timing(cfg, mode, steps, warmup, ctx, traffic_file, copy_probe, zero_in
     torch.cuda.synchronize()
     print(f"bench: {cfg} {mode} warmup done ({warmup} steps)", file=sys.stderr, flush=True)
 
-    # Per-kernel times: every launch bracketed by the library's hipEvents,
-    # over `steps` steps before the timed ones.  The brackets add queue time
-    # between the kernels, so the timed steps bracket only the kernel that
-    # takes the most time (the roofline's), whose duration comes from them.
-    ctx.profile_select(None)
-    ctx.profile_enable(True)
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    every = {n: (t / c if c else 0.0, c) for n, (t, c) in ctx.profile_read().items() if c}
-    ctx.profile_enable(False)
+    # Per-kernel times, each kernel bracketed alone; the kernel that takes
+    # the most time (the roofline's) is bracketed in the timed steps.
+    every = kernel_times(ctx, step, steps, dominant=True)
     dom = max((n for n in every if n in ALGO_UNITS), key=lambda n: every[n][0] * every[n][1])
     ctx.profile_select([dom])
     ctx.profile_enable(True)
